@@ -1,0 +1,76 @@
+/* ref_harness.c — builds the reference engine's own GDN code into a checker.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Compiled by oracle/Makefile, from the reference
+ * sources where they lie (REF=/root/reference), into oracle/_ref/ — never
+ * committed, never part of the product.  tests/golden/make_golden.py calls
+ * it to write golden vectors, and tests/test_oracle.py uses it (when built)
+ * to check the restatement in gdn_oracle.c bit for bit.
+ *
+ * The reference keeps deltanet_step and its helpers `static` inside
+ * engines/qwen.c; including the file here gives this translation unit access
+ * to them.  Its main() is renamed so it does not clash.
+ */
+#define main qwen_reference_main
+#include "qwen.c"
+#undef main
+
+/* One GDN layer run token by token through the reference deltanet_step
+ * (qwen.c:301-364) on a synthetic Model/Layer.  stream != 0 quantises
+ * qkv/z/out with the reference's qw_make (qwen.c:142-147) first, which is
+ * the int8 path of DM (qwen.c:139-141).  conv_st/rec_st are in/out. */
+int ref_gdn_layer_run(int kh, int vh, int kd, int vd, int K, int hidden, float eps, int stream,
+                      const float *W_qkv, const float *W_z, const float *W_b, const float *W_a,
+                      const float *W_out, const float *conv_w, const float *A_log,
+                      const float *dt_bias, const float *gnorm,
+                      int T, const float *x, float *out, float *conv_st, float *rec_st) {
+    Model m; memset(&m, 0, sizeof(m));
+    Layer l; memset(&l, 0, sizeof(l));
+    m.c.hidden = hidden; m.c.lin_kh = kh; m.c.lin_vh = vh; m.c.lin_kd = kd; m.c.lin_vd = vd;
+    m.c.conv_k = K; m.c.eps = eps;
+    m.stream = stream;
+    const int key_dim = kh * kd, val_dim = vh * vd, conv_dim = 2 * key_dim + val_dim;
+    float *cp[5]; const float *src[5] = {W_qkv, W_z, W_b, W_a, W_out};
+    const int64_t nel[5] = {(int64_t)conv_dim * hidden, (int64_t)val_dim * hidden,
+                            (int64_t)vh * hidden, (int64_t)vh * hidden, (int64_t)hidden * val_dim};
+    for (int i = 0; i < 5; i++) {
+        cp[i] = falloc(nel[i]);
+        memcpy(cp[i], src[i], nel[i] * sizeof(float));
+    }
+    l.qkv = cp[0]; l.z = cp[1]; l.b = cp[2]; l.a = cp[3]; l.outp = cp[4];
+    l.conv_w = (float *)conv_w; l.A_log = (float *)A_log; l.dt_bias = (float *)dt_bias;
+    l.gnorm = (float *)gnorm;
+    if (stream) {
+        l.Qqkv = qw_make(&l.qkv, conv_dim, hidden);
+        l.Qz = qw_make(&l.z, val_dim, hidden);
+        l.Qout = qw_make(&l.outp, hidden, val_dim);
+    }
+    float *convs[1] = {conv_st}, *recs[1] = {rec_st};
+    m.conv_st = convs; m.rec_st = recs;
+    float *tmp = falloc(val_dim > hidden ? val_dim : hidden);
+    for (int t = 0; t < T; t++) {
+        deltanet_step(&m, &l, 0, x + (int64_t)t * hidden, tmp);
+        memcpy(out + (int64_t)t * hidden, tmp, hidden * sizeof(float));
+    }
+    free(tmp);
+    /* qw_make freed (and NULLed) the fp32 originals it quantised */
+    free(l.qkv); free(l.z); free(l.b); free(l.a); free(l.outp);
+    if (stream) {
+        free(l.Qqkv.q); free(l.Qqkv.s); free(l.Qz.q); free(l.Qz.s); free(l.Qout.q); free(l.Qout.s);
+    }
+    return 0;
+}
+
+/* qwen.c:124-138 */
+void ref_quantize_rows(const float *w, int8_t *q, float *scale, int O, int I) {
+    quantize_rows(w, q, scale, O, I);
+}
+
+/* qwen.c:94-122 (x86 scalar branch) */
+void ref_matmul_q(float *y, const float *x, const int8_t *q, const float *scale, int I, int O) {
+    matmul_q(y, x, q, scale, I, O);
+}
+
+/* qwen.c:70-77 */
+void ref_matvec(float *y, const float *x, const float *W, int I, int O) {
+    matvec(y, x, W, I, O);
+}
