@@ -1,0 +1,131 @@
+/* om_hip.h — C-ABI of the MI355X Gated DeltaNet (GDN) layer.
+ *
+ * The drop-in for the GDN path of the overhang Qwen3.5/3.6 engine
+ * (engines/qwen.c).  The engine stays C and keeps its layer call
+ *     static void deltanet_step(Model *m, Layer *l, int li, const float *x, float *out)
+ * (engines/qwen.c:301); inside it, under -DOM_HIP, it calls omh_gdn_decode()
+ * and falls back to its CPU body on any non-zero return.
+ *
+ * Conventions follow the engine's existing GPU shim (metal/om_metal.h:9-50):
+ *   - C linkage, plain pointers and sizes;
+ *   - omh_init() returns 1 = ready, 0 = unavailable, memoised; OM_HIP=0 in
+ *     the environment opts out (the OM_METAL=0 precedent, engines/olmoe.c:22-29);
+ *   - entry points return 0 on success, a negative OMH_ERR_* code otherwise
+ *     (om_metal.mm:168,197,267), and the caller falls back to the CPU;
+ *   - host-pointer entry points are synchronous (om_metal's
+ *     waitUntilCompleted); the *_dev variants take device pointers and a
+ *     hipStream_t (as void*, NULL = the null stream) and only enqueue.
+ *
+ * Layouts are the reference's, row-major fp32 unless stated:
+ *   projection weights W[O][I]; int8 twins q[O][I] + per-row scale s[O]
+ *   (engines/qwen.c:34, 124-138); conv1d weight [conv_dim][K]; conv state
+ *   [conv_dim][K-1] oldest..newest (qwen.c:275, 308); recurrent state
+ *   S[vh][kd][vd] (qwen.c:276, 332); conv_dim = 2*kh*kd + vh*vd;
+ *   mixed_qkv = [q | k | v] channels (qwen.c:321).
+ *
+ * After the first successful GPU call for a layer the device state is the
+ * authoritative copy; a caller that falls back to the CPU mid-sequence must
+ * first fetch it with omh_gdn_state_get().
+ */
+#ifndef OM_HIP_H
+#define OM_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OMH_OK            0
+#define OMH_ERR_ALLOC    -1   /* device allocation failed                  */
+#define OMH_ERR_ARG      -2   /* unknown layer/sequence, bad pointer/size  */
+#define OMH_ERR_SHAPE    -3   /* shape not supported by the kernels        */
+#define OMH_ERR_DEVICE   -4   /* no usable gfx950 device / HIP error       */
+
+/* 1 = an MI355X (gfx950) is ready, 0 = unavailable.  Memoised.  Replaces
+ * omm_init (metal/om_metal.h:13-14) for this path. */
+int omh_init(void);
+
+/* Text of the last error on this thread's most recent failing call. */
+const char *omh_last_error(void);
+
+/* GDN layer dimensions: the linear_* fields the engine reads from
+ * config.json (engines/qwen.c:190-192, 196) plus hidden_size. */
+typedef struct {
+    int kh, vh, kd, vd;   /* linear_num_key/value_heads, linear_key/value_head_dim */
+    int conv_k;           /* linear_conv_kernel_dim                               */
+    int hidden;           /* hidden_size (0 for a core-only layer)                */
+    float eps;            /* rms_norm_eps, used by the gated norm                 */
+} omh_gdn_dims;
+
+/* Host copies of one layer's weights, as the engine's Layer holds them
+ * (engines/qwen.c:42, 47).  Projections may be fp32 (W_*) or int8 twins
+ * (Q_*, S_*); when a Q_ pointer is non-NULL it is used.  in_proj_b and
+ * in_proj_a are always fp32, as in the engine (qwen.c:324-325).  All
+ * projection pointers may be NULL for a core-only layer. */
+typedef struct {
+    const float *W_qkv, *W_z, *W_b, *W_a, *W_out;
+    const int8_t *Q_qkv, *Q_z, *Q_out;
+    const float *S_qkv, *S_z, *S_out;
+    const float *conv_w;             /* [conv_dim][K] */
+    const float *A_log, *dt_bias;    /* [vh]          */
+    const float *gnorm;              /* [vd]          */
+} omh_gdn_weights;
+
+/* Upload a layer's weights (copied; the host keeps its arrays) and allocate
+ * zeroed conv + recurrent state for max_seqs sequences.  Replaces the
+ * per-layer state allocation of model_init (engines/qwen.c:259-276).
+ * li in [0, 4096).  Re-initialising an existing li replaces it. */
+int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, int max_seqs);
+int omh_gdn_layer_free(int li);
+
+/* Zero one sequence's conv and recurrent state (seq < 0: every sequence):
+ * the reset branch of serve() (engines/qwen.c:576-582). */
+int omh_gdn_state_reset(int li, int seq);
+/* Copy one sequence's state out / in, in the reference layouts
+ * (conv [conv_dim][K-1], S [vh][kd][vd]); either pointer may be NULL. */
+int omh_gdn_state_get(int li, int seq, float *conv, float *S);
+int omh_gdn_state_set(int li, int seq, const float *conv, const float *S);
+
+/* ---- host-pointer, synchronous entry points (the engine's drop-in) ---- */
+
+/* One token for each of sequences 0..B-1 through the whole layer:
+ * x[B][hidden] (the input-layernorm output) -> out[B][hidden] (the out_proj
+ * output the caller adds to its residual).  B = 1 is exactly
+ * deltanet_step(m, l, li, x, out) (engines/qwen.c:301-364). */
+int omh_gdn_decode(int li, int B, const float *x, float *out);
+
+/* T consecutive tokens of sequence seq through the whole layer, continuing
+ * from its current state (chunked WY/UT form on the GPU).  Equivalent to T
+ * calls of deltanet_step; x[T][hidden] -> out[T][hidden].  New capability:
+ * the engine prefills token by token (engines/qwen.c:588, 637). */
+int omh_gdn_prefill(int li, int seq, int T, const float *x, float *out);
+
+/* Core only (no projections): pre-projected mixed_qkv[B][conv_dim],
+ * z[B][vh*vd], a[B][vh], b[B][vh] -> core[B][vh*vd], the gated-normed head
+ * outputs that out_proj consumes (engines/qwen.c:307-358). */
+int omh_gdn_decode_core(int li, int B, const float *qkv, const float *z,
+                        const float *a, const float *b, float *core);
+/* Core only, T tokens of one sequence: inputs/outputs [T][...]. */
+int omh_gdn_prefill_core(int li, int seq, int T, const float *qkv, const float *z,
+                         const float *a, const float *b, float *core);
+
+/* ---- device-pointer, stream-ordered variants (asynchronous) ---- */
+
+/* Core decode for nl layers at once (nl >= 1, all of identical dims), each
+ * with B sequences: inputs [nl][B][...] and core [nl][B][vh*vd] in device
+ * memory; lis[nl] is a host array of layer ids.  Layers are independent
+ * here (pre-projected inputs), so one launch serves them all. */
+int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
+                            const float *a, const float *b, float *core, void *stream);
+int omh_gdn_prefill_core_dev(int li, int seq, int T, const float *qkv, const float *z,
+                             const float *a, const float *b, float *core, void *stream);
+int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream);
+int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void *stream);
+
+/* Wait for all work this library enqueued on `stream`. */
+int omh_sync(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

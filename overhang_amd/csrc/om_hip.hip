@@ -1,0 +1,412 @@
+// om_hip.hip — the C-ABI of include/om_hip.h on the HIP runtime.
+//
+// Owns the device copies of each GDN layer's weights and per-sequence state
+// (the engine's conv_st / rec_st, engines/qwen.c:275-276) and the grow-only
+// scratch the entry points need (the om_metal ensure() precedent,
+// metal/om_metal.mm:148-151).  Host-pointer calls run on a library stream
+// and block until done (om_metal's waitUntilCompleted); *_dev calls only
+// enqueue on the caller's stream.
+#include "om_hip.h"
+#include "omh_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+using namespace omh;
+
+namespace {
+
+constexpr int kMaxLayers = 4096;
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_OK(expr)                                                                      \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(OMH_ERR_DEVICE, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),   \
+                        __FILE__, __LINE__);                                              \
+    } while (0)
+
+struct DevLayer {
+    bool live = false;
+    omh_gdn_dims d{};
+    int max_seqs = 0, conv_dim = 0, vdim = 0;
+    // core weights and state
+    float *conv_w = nullptr, *A_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
+    float *conv_st = nullptr, *S = nullptr;
+    // projections: in_proj rows [qkv | z | b | a]; rows < in_nq are int8
+    bool has_proj = false;
+    int in_rows = 0, in_nq = 0;
+    int8_t *Qin = nullptr;
+    float *Sin = nullptr, *Win = nullptr;
+    int out_nq = 0;
+    int8_t *Qout = nullptr;
+    float *Sout = nullptr, *Wout = nullptr;
+};
+
+DevLayer g_L[kMaxLayers];
+int g_ready = -1;
+hipStream_t g_stream = nullptr;
+
+// grow-only device scratch
+struct Scratch {
+    void *p = nullptr;
+    size_t n = 0;
+};
+Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b;
+
+int ensure(Scratch &s, size_t bytes) {
+    if (bytes <= s.n) return OMH_OK;
+    if (s.p) (void)hipFree(s.p);
+    s.p = nullptr;
+    s.n = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    if (hipMalloc(&s.p, want) != hipSuccess) return fail(OMH_ERR_ALLOC, "scratch alloc of %zu bytes failed", want);
+    s.n = want;
+    return OMH_OK;
+}
+
+template <typename T>
+int upload(T **dst, size_t count, const T *src) {
+    if (hipMalloc(reinterpret_cast<void **>(dst), count * sizeof(T) + 16) != hipSuccess)
+        return fail(OMH_ERR_ALLOC, "alloc of %zu bytes failed", count * sizeof(T));
+    if (src) HIP_OK(hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return OMH_OK;
+}
+
+void free_layer(DevLayer &L) {
+    void *ps[] = {L.conv_w, L.A_log, L.dt_bias, L.gnorm, L.conv_st, L.S, L.Qin, L.Sin, L.Win,
+                  L.Qout, L.Sout, L.Wout};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    L = DevLayer{};
+}
+
+int check_layer(int li) {
+    if (li < 0 || li >= kMaxLayers || !g_L[li].live) return fail(OMH_ERR_ARG, "layer %d not initialised", li);
+    return OMH_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+LayerPtrs ptrs(const DevLayer &L) {
+    LayerPtrs p;
+    p.conv_w = L.conv_w; p.A_log = L.A_log; p.dt_bias = L.dt_bias; p.gnorm = L.gnorm;
+    p.conv_st = L.conv_st; p.S = L.S;
+    return p;
+}
+
+// Core decode on device pointers for layers lis[0..nl), B sequences each.
+int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv, const float *z,
+                int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
+                hipStream_t st) {
+    if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
+    for (int i = 0; i < nl; i++)
+        if (int rc = check_layer(lis[i])) return rc;
+    const DevLayer &L0 = g_L[lis[0]];
+    const omh_gdn_dims &d = L0.d;
+    for (int i = 1; i < nl; i++) {
+        const omh_gdn_dims &e = g_L[lis[i]].d;
+        if (e.kh != d.kh || e.vh != d.vh || e.kd != d.kd || e.vd != d.vd || e.conv_k != d.conv_k)
+            return fail(OMH_ERR_ARG, "decode_core: layers %d and %d differ in shape", lis[0], lis[i]);
+    }
+    for (int i = 0; i < nl; i++)
+        if (B < 1 || B > g_L[lis[i]].max_seqs)
+            return fail(OMH_ERR_ARG, "decode_core: B=%d outside [1, %d] for layer %d", B,
+                        g_L[lis[i]].max_seqs, lis[i]);
+    if (!decode_core_supported(d.kd, d.vd, d.vh / d.kh))
+        return fail(OMH_ERR_SHAPE, "decode_core: kd=%d vd=%d rep=%d unsupported", d.kd, d.vd, d.vh / d.kh);
+    if (!qkv || !z || !a || !b || !core) return fail(OMH_ERR_ARG, "decode_core: null pointer");
+    if (!aligned16(z) || !aligned16(core) || (ld_z % 4) != 0)
+        return fail(OMH_ERR_ARG, "decode_core: z/core must be 16-byte aligned rows");
+    const int vdim = L0.vdim;
+    for (int l0 = 0; l0 < nl; l0 += kMaxDecodeLayers) {
+        const int n = nl - l0 < kMaxDecodeLayers ? nl - l0 : kMaxDecodeLayers;
+        DecodeArgs A{};
+        const size_t t0 = (size_t)l0 * B;
+        A.qkv = qkv + t0 * ld_qkv;
+        A.z = z + t0 * ld_z;
+        A.a = a + t0 * ld_ab;
+        A.b = b + t0 * ld_ab;
+        A.core = core + t0 * vdim;
+        A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
+        A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
+        for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
+        HIP_OK(launch_decode_core(A, d.kd, d.vd, st));
+    }
+    return OMH_OK;
+}
+
+int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    if (!L.has_proj) return fail(OMH_ERR_ARG, "layer %d was initialised without projections", li);
+    if (B < 1 || B > L.max_seqs) return fail(OMH_ERR_ARG, "decode: B=%d outside [1, %d]", B, L.max_seqs);
+    if (!x || !out || !aligned16(x) || !aligned16(out)) return fail(OMH_ERR_ARG, "decode: x/out must be 16-byte aligned");
+    const int D = L.d.hidden;
+    if (int rc = ensure(g_in, (size_t)B * L.in_rows * sizeof(float))) return rc;
+    if (int rc = ensure(g_core, (size_t)B * L.vdim * sizeof(float))) return rc;
+    float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
+    ProjArgs p{};
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows;
+    p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
+    HIP_OK(launch_proj(p, st));
+    const int vh = L.d.vh;
+    const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
+    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
+    ProjArgs q{};
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D;
+    q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
+    HIP_OK(launch_proj(q, st));
+    return OMH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int omh_init(void) {
+    if (g_ready >= 0) return g_ready;
+    g_ready = 0;
+    const char *e = getenv("OM_HIP");
+    if (e && e[0] == '0') { fail(OMH_ERR_DEVICE, "disabled by OM_HIP=0"); return 0; }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) { fail(OMH_ERR_DEVICE, "no HIP device"); return 0; }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) { fail(OMH_ERR_DEVICE, "hipGetDeviceProperties failed"); return 0; }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        fail(OMH_ERR_DEVICE, "device %d is %s, this library is built for gfx950", dev, prop.gcnArchName);
+        return 0;
+    }
+    if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
+        fail(OMH_ERR_DEVICE, "stream creation failed");
+        return 0;
+    }
+    g_ready = 1;
+    return 1;
+}
+
+const char *omh_last_error(void) { return g_err; }
+
+int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, int max_seqs) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (li < 0 || li >= kMaxLayers) return fail(OMH_ERR_ARG, "layer id %d outside [0, %d)", li, kMaxLayers);
+    if (!d || !w || max_seqs < 1) return fail(OMH_ERR_ARG, "layer_init: null dims/weights or max_seqs < 1");
+    if (d->kh < 1 || d->vh < d->kh || d->vh % d->kh || d->kd < 1 || d->vd < 1 || d->conv_k < 2)
+        return fail(OMH_ERR_ARG, "layer_init: bad dims kh=%d vh=%d kd=%d vd=%d K=%d", d->kh, d->vh, d->kd, d->vd, d->conv_k);
+    if (!decode_core_supported(d->kd, d->vd, d->vh / d->kh))
+        return fail(OMH_ERR_SHAPE, "layer_init: kd=%d vd=%d rep=%d unsupported", d->kd, d->vd, d->vh / d->kh);
+    if (!w->conv_w || !w->A_log || !w->dt_bias || !w->gnorm) return fail(OMH_ERR_ARG, "layer_init: core weights missing");
+    if (g_L[li].live) free_layer(g_L[li]);
+    DevLayer L;
+    L.d = *d;
+    L.max_seqs = max_seqs;
+    L.conv_dim = 2 * d->kh * d->kd + d->vh * d->vd;
+    L.vdim = d->vh * d->vd;
+    const int K = d->conv_k, D = d->hidden, vh = d->vh;
+    int rc = OMH_OK;
+#define UP(dst, n, src) do { if ((rc = upload(&(dst), (size_t)(n), (src))) != OMH_OK) { free_layer(L); return rc; } } while (0)
+    UP(L.conv_w, (size_t)L.conv_dim * K, w->conv_w);
+    UP(L.A_log, vh, w->A_log);
+    UP(L.dt_bias, vh, w->dt_bias);
+    UP(L.gnorm, d->vd, w->gnorm);
+    UP(L.conv_st, (size_t)max_seqs * L.conv_dim * (K - 1), (const float *)nullptr);
+    UP(L.S, (size_t)max_seqs * vh * d->kd * d->vd, (const float *)nullptr);
+    if (hipMemset(L.conv_st, 0, (size_t)max_seqs * L.conv_dim * (K - 1) * sizeof(float)) != hipSuccess ||
+        hipMemset(L.S, 0, (size_t)max_seqs * vh * d->kd * d->vd * sizeof(float)) != hipSuccess) {
+        free_layer(L);
+        return fail(OMH_ERR_DEVICE, "layer_init: state clear failed");
+    }
+    const bool any_proj = w->W_qkv || w->Q_qkv;
+    if (any_proj) {
+        if (D < 4 || D % 4 || L.vdim % 4) { free_layer(L); return fail(OMH_ERR_SHAPE, "layer_init: hidden and vh*vd must be multiples of 4"); }
+        const bool q8 = w->Q_qkv != nullptr;
+        if (q8 && (!w->Q_z || !w->S_qkv || !w->S_z)) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: int8 in_proj needs Q_qkv, Q_z and their scales"); }
+        if (!q8 && (!w->W_qkv || !w->W_z)) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: fp32 in_proj needs W_qkv and W_z"); }
+        if (!w->W_b || !w->W_a) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: W_b and W_a are required"); }
+        if (!w->Q_out && !w->W_out) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: out_proj missing"); }
+        if (w->Q_out && !w->S_out) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: out_proj scales missing"); }
+        L.in_rows = L.conv_dim + L.vdim + 2 * vh;
+        const size_t Dz = (size_t)D;
+        if (q8) {
+            L.in_nq = L.conv_dim + L.vdim;
+            std::vector<int8_t> q((size_t)L.in_nq * Dz);
+            memcpy(q.data(), w->Q_qkv, (size_t)L.conv_dim * Dz);
+            memcpy(q.data() + (size_t)L.conv_dim * Dz, w->Q_z, (size_t)L.vdim * Dz);
+            std::vector<float> s(L.in_nq);
+            memcpy(s.data(), w->S_qkv, L.conv_dim * sizeof(float));
+            memcpy(s.data() + L.conv_dim, w->S_z, L.vdim * sizeof(float));
+            UP(L.Qin, q.size(), q.data());
+            UP(L.Sin, s.size(), s.data());
+        }
+        const int nf = L.in_rows - L.in_nq;
+        std::vector<float> f((size_t)nf * Dz);
+        size_t off = 0;
+        if (!q8) {
+            memcpy(f.data(), w->W_qkv, (size_t)L.conv_dim * Dz * sizeof(float)); off += (size_t)L.conv_dim * Dz;
+            memcpy(f.data() + off, w->W_z, (size_t)L.vdim * Dz * sizeof(float)); off += (size_t)L.vdim * Dz;
+        }
+        memcpy(f.data() + off, w->W_b, (size_t)vh * Dz * sizeof(float)); off += (size_t)vh * Dz;
+        memcpy(f.data() + off, w->W_a, (size_t)vh * Dz * sizeof(float));
+        UP(L.Win, f.size(), f.data());
+        if (w->Q_out) {
+            L.out_nq = D;
+            UP(L.Qout, (size_t)D * L.vdim, w->Q_out);
+            UP(L.Sout, D, w->S_out);
+        } else {
+            UP(L.Wout, (size_t)D * L.vdim, w->W_out);
+        }
+        L.has_proj = true;
+    }
+#undef UP
+    L.live = true;
+    g_L[li] = L;
+    return OMH_OK;
+}
+
+int omh_gdn_layer_free(int li) {
+    if (int rc = check_layer(li)) return rc;
+    if (hipDeviceSynchronize() != hipSuccess) return fail(OMH_ERR_DEVICE, "layer_free: sync failed");
+    free_layer(g_L[li]);
+    return OMH_OK;
+}
+
+int omh_gdn_state_reset(int li, int seq) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    if (seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_reset: seq %d >= %d", seq, L.max_seqs);
+    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    const size_t s0 = seq < 0 ? 0 : (size_t)seq, ns = seq < 0 ? (size_t)L.max_seqs : 1;
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemset(L.conv_st + s0 * cn, 0, ns * cn * sizeof(float)));
+    HIP_OK(hipMemset(L.S + s0 * sn, 0, ns * sn * sizeof(float)));
+    HIP_OK(hipDeviceSynchronize());
+    return OMH_OK;
+}
+
+int omh_gdn_state_get(int li, int seq, float *conv, float *S) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    if (seq < 0 || seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_get: seq %d outside [0, %d)", seq, L.max_seqs);
+    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    HIP_OK(hipDeviceSynchronize());
+    if (conv) HIP_OK(hipMemcpy(conv, L.conv_st + seq * cn, cn * sizeof(float), hipMemcpyDeviceToHost));
+    if (S) HIP_OK(hipMemcpy(S, L.S + seq * sn, sn * sizeof(float), hipMemcpyDeviceToHost));
+    return OMH_OK;
+}
+
+int omh_gdn_state_set(int li, int seq, const float *conv, const float *S) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    if (seq < 0 || seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_set: seq %d outside [0, %d)", seq, L.max_seqs);
+    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    HIP_OK(hipDeviceSynchronize());
+    if (conv) HIP_OK(hipMemcpy(L.conv_st + seq * cn, conv, cn * sizeof(float), hipMemcpyHostToDevice));
+    if (S) HIP_OK(hipMemcpy(L.S + seq * sn, S, sn * sizeof(float), hipMemcpyHostToDevice));
+    return OMH_OK;
+}
+
+int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
+                            const float *a, const float *b, float *core, void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core_dev: nl=%d", nl);
+    if (int rc = check_layer(lis[0])) return rc;
+    const DevLayer &L = g_L[lis[0]];
+    return decode_core(nl, lis, B, qkv, L.conv_dim, z, L.vdim, a, b, L.d.vh, core,
+                       static_cast<hipStream_t>(stream));
+}
+
+int omh_gdn_decode_core(int li, int B, const float *qkv, const float *z, const float *a,
+                        const float *b, float *core) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    const DevLayer &L = g_L[li];
+    if (B < 1 || B > L.max_seqs) return fail(OMH_ERR_ARG, "decode_core: B=%d outside [1, %d]", B, L.max_seqs);
+    if (!qkv || !z || !a || !b || !core) return fail(OMH_ERR_ARG, "decode_core: null pointer");
+    const size_t nq = (size_t)B * L.conv_dim, nz = (size_t)B * L.vdim, nab = (size_t)B * L.d.vh;
+    if (int rc = ensure(g_qkv, nq * 4)) return rc;
+    if (int rc = ensure(g_z, nz * 4)) return rc;
+    if (int rc = ensure(g_a, nab * 4)) return rc;
+    if (int rc = ensure(g_b, nab * 4)) return rc;
+    if (int rc = ensure(g_core, nz * 4)) return rc;
+    float *dq = (float *)g_qkv.p, *dz = (float *)g_z.p, *da = (float *)g_a.p, *db = (float *)g_b.p, *dc = (float *)g_core.p;
+    HIP_OK(hipMemcpyAsync(dq, qkv, nq * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(dz, z, nz * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(da, a, nab * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(db, b, nab * 4, hipMemcpyHostToDevice, g_stream));
+    if (int rc = decode_core(1, &li, B, dq, L.conv_dim, dz, L.vdim, da, db, L.d.vh, dc, g_stream)) return rc;
+    HIP_OK(hipMemcpyAsync(core, dc, nz * 4, hipMemcpyDeviceToHost, g_stream));
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
+}
+
+int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    return decode_full(li, B, x, out, static_cast<hipStream_t>(stream));
+}
+
+int omh_gdn_decode(int li, int B, const float *x, float *out) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    const DevLayer &L = g_L[li];
+    if (!L.has_proj) return fail(OMH_ERR_ARG, "layer %d was initialised without projections", li);
+    if (B < 1 || B > L.max_seqs) return fail(OMH_ERR_ARG, "decode: B=%d outside [1, %d]", B, L.max_seqs);
+    if (!x || !out) return fail(OMH_ERR_ARG, "decode: null pointer");
+    const size_t n = (size_t)B * L.d.hidden;
+    if (int rc = ensure(g_x, n * 4)) return rc;
+    if (int rc = ensure(g_out, n * 4)) return rc;
+    HIP_OK(hipMemcpyAsync(g_x.p, x, n * 4, hipMemcpyHostToDevice, g_stream));
+    if (int rc = decode_full(li, B, (const float *)g_x.p, (float *)g_out.p, g_stream)) return rc;
+    HIP_OK(hipMemcpyAsync(out, g_out.p, n * 4, hipMemcpyDeviceToHost, g_stream));
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
+}
+
+int omh_gdn_prefill(int li, int seq, int T, const float *x, float *out) {
+    (void)li; (void)seq; (void)T; (void)x; (void)out;
+    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+}
+
+int omh_gdn_prefill_core(int li, int seq, int T, const float *qkv, const float *z, const float *a,
+                         const float *b, float *core) {
+    (void)li; (void)seq; (void)T; (void)qkv; (void)z; (void)a; (void)b; (void)core;
+    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+}
+
+int omh_gdn_prefill_core_dev(int li, int seq, int T, const float *qkv, const float *z, const float *a,
+                             const float *b, float *core, void *stream) {
+    (void)li; (void)seq; (void)T; (void)qkv; (void)z; (void)a; (void)b; (void)core; (void)stream;
+    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+}
+
+int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void *stream) {
+    (void)li; (void)seq; (void)T; (void)x; (void)out; (void)stream;
+    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+}
+
+int omh_sync(void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    HIP_OK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return OMH_OK;
+}
+
+}  // extern "C"

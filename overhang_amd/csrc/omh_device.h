@@ -1,0 +1,55 @@
+// omh_device.h — device helpers shared by the GDN kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define OMH_WAVE 64
+
+// Activations with the reference's definitions (engines/qwen.c:158-160):
+// sigmoid = 1/(1+e^-z); silu = z*sigmoid(z); softplus thresholded at 20.
+__device__ __forceinline__ float omh_sigmoid(float z) { return 1.f / (1.f + expf(-z)); }
+__device__ __forceinline__ float omh_silu(float z) { return z * omh_sigmoid(z); }
+__device__ __forceinline__ float omh_softplus(float z) { return z > 20.f ? z : log1pf(expf(z)); }
+
+// Workgroup barrier that orders LDS only: outstanding global loads stay in
+// flight across it (a plain __syncthreads also drains them).  Correct
+// wherever threads communicate through LDS alone.
+__device__ __forceinline__ void omh_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Butterfly sum over the lanes whose index differs in the bits [lo, 64).
+template <int LO>
+__device__ __forceinline__ float omh_xor_sum_from(float v) {
+#pragma unroll
+    for (int off = LO; off < OMH_WAVE; off <<= 1) v += __shfl_xor(v, off, OMH_WAVE);
+    return v;
+}
+// Butterfly sum over the lanes whose index differs in the bits [0, HI).
+template <int HI>
+__device__ __forceinline__ float omh_xor_sum_below(float v) {
+#pragma unroll
+    for (int off = 1; off < HI; off <<= 1) v += __shfl_xor(v, off, OMH_WAVE);
+    return v;
+}
+
+// Streaming (nontemporal) 16-byte load/store for data touched once per launch.
+typedef float omh_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 omh_ld_stream(const float *p) {
+    const omh_v4f v = __builtin_nontemporal_load(reinterpret_cast<const omh_v4f *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void omh_st_stream(float *p, float4 a) {
+    omh_v4f v = {a.x, a.y, a.z, a.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<omh_v4f *>(p));
+}
+
+__device__ __forceinline__ float4 f4_scale(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
+__device__ __forceinline__ float4 f4_sub(float4 a, float4 b) { return make_float4(a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w); }
+// c + a*s, component-wise
+__device__ __forceinline__ float4 f4_fma(float4 a, float s, float4 c) {
+    return make_float4(fmaf(a.x, s, c.x), fmaf(a.y, s, c.y), fmaf(a.z, s, c.z), fmaf(a.w, s, c.w));
+}
+__device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }

@@ -1,0 +1,53 @@
+// omh_internal.h — interface between the C-ABI layer (om_hip.hip) and the
+// kernel launchers.  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace omh {
+
+// Device pointers of one layer's core weights and state.
+struct LayerPtrs {
+    const float *conv_w;   // [conv_dim][K]
+    const float *A_log;    // [vh]
+    const float *dt_bias;  // [vh]
+    const float *gnorm;    // [vd]
+    float *conv_st;        // [max_seqs][conv_dim][K-1]
+    float *S;              // [max_seqs][vh][kd][vd]
+};
+
+// Decode-core launch: nl layers x B sequences, one token each.
+constexpr int kMaxDecodeLayers = 32;
+// Token t = l*B + b reads qkv + t*ld_qkv, z + t*ld_z, a + t*ld_ab, b + t*ld_ab
+// and writes core + t*vh*vd.
+struct DecodeArgs {
+    const float *qkv;   // [nl*B] rows of >= conv_dim
+    const float *z;     // [nl*B] rows of >= vh*vd
+    const float *a;     // [nl*B] rows of >= vh
+    const float *b;     // [nl*B] rows of >= vh
+    float *core;        // [nl][B][vh*vd]
+    int64_t ld_qkv, ld_z, ld_ab;
+    int B, nl, kh, vh, K;
+    float eps;
+    LayerPtrs L[kMaxDecodeLayers];
+};
+
+// y[t][o] = sum_i x[t][i] * W[o][i] for t < T, o < O.  Rows o < n_q come
+// from the int8 matrix Q (times scale[o]); rows o >= n_q from the fp32
+// matrix W (row o - n_q).  Either part may be empty.
+struct ProjArgs {
+    const float *x;        // [T][ldx]
+    float *y;              // [T][ldy]
+    const int8_t *Q;       // [n_q][I]
+    const float *scale;    // [n_q]
+    const float *W;        // [O - n_q][I]
+    int64_t ldx, ldy;
+    int T, I, O, n_q;
+};
+hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
+
+// Returns hipSuccess, or hipErrorInvalidValue for an unsupported (kd, vd, rep).
+hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, hipStream_t st);
+bool decode_core_supported(int kd, int vd, int rep);
+
+}  // namespace omh

@@ -1,0 +1,151 @@
+"""GPU parity of the decode path (one token per call) through the C-ABI.
+
+Against the reference's golden vectors (tests/golden, written by the
+reference deltanet_step) and the CPU oracle on seeded inputs, at the
+tolerance in tests/tol.py.  Every call goes through libom_hip.so."""
+import numpy as np
+import pytest
+
+import oracle
+from overhang_amd import gdn, synth
+from overhang_amd.dims import GdnDims, Q35B, CFG1
+from tests import fixtures
+from tests.tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+_next_li = [100]
+
+
+def new_li():
+    _next_li[0] += 1
+    return _next_li[0]
+
+
+@pytest.mark.parametrize("name", fixtures.CORE_FIXTURES)
+def test_decode_core_matches_reference_golden(name):
+    d, w, inp, (conv, S), exp = fixtures.load(name)
+    L = gdn.GdnLayer(new_li(), d, w)
+    L.set_state(0, conv, S)
+    T = inp["qkv"].shape[0]
+    core = np.stack([L.decode_core(inp["qkv"][t:t + 1], inp["z"][t:t + 1], inp["a"][t:t + 1],
+                                   inp["b"][t:t + 1])[0] for t in range(T)])
+    conv2, S2 = L.get_state(0)
+    assert_close(core, exp["core"], what=f"{name} core")
+    assert_close(S2, exp["S"], what=f"{name} S")
+    assert np.array_equal(conv2, exp["conv"]), "conv history is a copy of inputs: must be exact"
+    L.free()
+
+
+@pytest.mark.parametrize("name", fixtures.LAYER_FIXTURES)
+def test_decode_layer_matches_reference_golden(name):
+    d, w, inp, (conv, S), exp = fixtures.load(name)
+    L = gdn.GdnLayer(new_li(), d, w, int8=exp["int8"])
+    L.set_state(0, conv, S)
+    x = inp["x"]
+    out = np.concatenate([L.decode(x[t:t + 1]) for t in range(x.shape[0])])
+    conv2, S2 = L.get_state(0)
+    assert_close(out, exp["out"], what=f"{name} out")
+    assert_close(S2, exp["S"], what=f"{name} S")
+    assert_close(conv2, exp["conv"], atol=1e-5, rtol=1e-5, what=f"{name} conv")
+    L.free()
+
+
+def test_decode_core_35b_shape_batched_vs_oracle():
+    """Qwen3.6-35B-A3B GDN shape, 3 sequences with distinct states, 4 tokens."""
+    d = Q35B
+    w = synth.layer_weights(d, 31, gnorm_std=0.1, projections=False)
+    B, T = 3, 4
+    inp = synth.core_inputs(d, T, 31, B=B)
+    conv0, S0 = synth.states(d, 31, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    got = np.stack([L.decode_core(inp["qkv"][:, t], inp["z"][:, t], inp["a"][:, t], inp["b"][:, t])
+                    for t in range(T)], axis=1)
+    for s in range(B):
+        ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"][s], inp["z"][s], inp["a"][s], inp["b"][s],
+                                          conv0[s], S0[s])
+        conv, S = L.get_state(s)
+        assert_close(got[s], ref, what=f"seq {s} core")
+        assert_close(S, Sref, what=f"seq {s} S")
+        assert np.array_equal(conv, cref)
+    L.free()
+
+
+def test_multi_layer_dev_call_equals_per_layer_calls():
+    from overhang_amd import hip
+    d = CFG1
+    nl, B = 5, 2
+    lays, lays2 = [], []
+    for l in range(nl):
+        w = synth.layer_weights(d, 40 + l, gnorm_std=0.1, projections=False)
+        conv0, S0 = synth.states(d, 40 + l, B=B)
+        a = gdn.GdnLayer(new_li(), d, w, max_seqs=B)
+        b = gdn.GdnLayer(new_li(), d, w, max_seqs=B)
+        for s in range(B):
+            a.set_state(s, conv0[s], S0[s])
+            b.set_state(s, conv0[s], S0[s])
+        lays.append(a)
+        lays2.append(b)
+    inp = synth.core_inputs(d, nl, 50, B=B)       # [B][nl][...] -> need [nl][B][...]
+    host = {k: np.ascontiguousarray(np.swapaxes(v, 0, 1)) for k, v in inp.items()}
+    dev = {k: hip.Buffer.from_numpy(v) for k, v in host.items()}
+    core = hip.Buffer(nl * B * d.val_dim * 4)
+    st = hip.Stream()
+    gdn.decode_core_dev([L.li for L in lays], B, dev["qkv"], dev["z"], dev["a"], dev["b"], core, stream=st)
+    st.synchronize()
+    got = core.numpy((nl, B, d.val_dim))
+    for l in range(nl):
+        ref = lays2[l].decode_core(host["qkv"][l], host["z"][l], host["a"][l], host["b"][l])
+        np.testing.assert_array_equal(got[l], ref)
+        for s in range(B):
+            c1, S1 = lays[l].get_state(s)
+            c2, S2 = lays2[l].get_state(s)
+            assert np.array_equal(c1, c2) and np.array_equal(S1, S2)
+    for L in lays + lays2:
+        L.free()
+
+
+def test_state_roundtrip_reset_and_isolation():
+    d = CFG1
+    w = synth.layer_weights(d, 60, projections=False)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=3)
+    conv0, S0 = synth.states(d, 60, B=3)
+    for s in range(3):
+        L.set_state(s, conv0[s], S0[s])
+    for s in range(3):
+        c, S = L.get_state(s)
+        assert np.array_equal(c, conv0[s]) and np.array_equal(S, S0[s])
+    L.reset(1)
+    c, S = L.get_state(1)
+    assert not c.any() and not S.any()
+    c, S = L.get_state(2)
+    assert np.array_equal(S, S0[2])
+    # a B=1 call touches sequence 0 only
+    inp = synth.core_inputs(d, 1, 61)
+    L.decode_core(inp["qkv"], inp["z"], inp["a"], inp["b"])
+    c, S = L.get_state(2)
+    assert np.array_equal(S, S0[2]) and np.array_equal(c, conv0[2])
+    L.reset(-1)
+    for s in range(3):
+        c, S = L.get_state(s)
+        assert not c.any() and not S.any()
+    L.free()
+
+
+def test_argument_errors_are_reported():
+    d = CFG1
+    w = synth.layer_weights(d, 62, projections=False)
+    with pytest.raises(gdn.OmhError) as e:
+        gdn.GdnLayer(new_li(), GdnDims(2, 4, 48, 48, 4, 0), synth.layer_weights(GdnDims(2, 4, 48, 48, 4, 0), 0, projections=False))
+    assert e.value.code == gdn.OMH_ERR_SHAPE
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=2)
+    inp = synth.core_inputs(d, 3, 63)
+    with pytest.raises(gdn.OmhError) as e:
+        L.decode_core(inp["qkv"], inp["z"], inp["a"], inp["b"])      # B=3 > max_seqs
+    assert e.value.code == gdn.OMH_ERR_ARG
+    assert gdn.lib().omh_gdn_decode_core(4095, 1, None, None, None, None, None) == gdn.OMH_ERR_ARG
+    with pytest.raises(gdn.OmhError):
+        L.decode(np.zeros((1, 128), np.float32))                       # core-only layer
+    L.free()
