@@ -52,26 +52,31 @@ def make_layers(gdn, d, first_li, n, max_seqs, w, conv0, S0):
 
 
 def time_launches(hip, st, fn, steps, warmup):
-    """Run fn(k) for warmup + steps iterations on stream st, bracketed by
-    device synchronisation.  Returns (elapsed seconds of the timed region by
-    HIP events on st, per-step durations in s by event pairs on st around
-    each step's launches, host wall seconds)."""
+    """Run fn(k) for warmup + steps iterations on stream st.
+
+    Throughput pass: `steps` back-to-back steps bracketed by device
+    synchronisation, timed by one HIP event pair on st around the region.
+    Duration pass: the same steps again, each between its own event pair on
+    st (the per-launch kernel time the roofline uses).  Returns (elapsed s of
+    the throughput region, per-step durations in s, host wall s)."""
     for k in range(warmup):
         fn(k)
     hip.device_synchronize()
-    ev = [(hip.Event(), hip.Event()) for _ in range(steps)]
     t0, t1 = hip.Event(), hip.Event()
-    hip.device_synchronize()
     wall0 = time.perf_counter()
     t0.record(st)
     for k in range(steps):
-        ev[k][0].record(st)
         fn(warmup + k)
-        ev[k][1].record(st)
     t1.record(st)
     hip.device_synchronize()
     wall = time.perf_counter() - wall0
     el = t0.elapsed_ms(t1) / 1e3
+    ev = [(hip.Event(), hip.Event()) for _ in range(steps)]
+    for k in range(steps):
+        ev[k][0].record(st)
+        fn(warmup + steps + k)
+        ev[k][1].record(st)
+    hip.device_synchronize()
     durs = [a.elapsed_ms(b) / 1e3 for a, b in ev]
     return max(el, 1e-12), durs, wall
 

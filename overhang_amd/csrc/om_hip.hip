@@ -45,9 +45,13 @@ struct DevLayer {
     bool live = false;
     omh_gdn_dims d{};
     int max_seqs = 0, conv_dim = 0, vdim = 0;
-    // core weights and state
+    // core weights and state (conv history as a ring, omh_internal.h)
     float *conv_w = nullptr, *A_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
     float *conv_st = nullptr, *S = nullptr;
+    int *phase = nullptr;                  // [2][max_seqs]
+    int epoch = 0;                         // which phase buffer decode launches read
+    float *o_raw = nullptr, *ssq = nullptr;
+    int *cnt = nullptr;
     // projections: in_proj rows [qkv | z | b | a]; rows < in_nq are int8
     bool has_proj = false;
     int in_rows = 0, in_nq = 0;
@@ -89,8 +93,8 @@ int upload(T **dst, size_t count, const T *src) {
 }
 
 void free_layer(DevLayer &L) {
-    void *ps[] = {L.conv_w, L.A_log, L.dt_bias, L.gnorm, L.conv_st, L.S, L.Qin, L.Sin, L.Win,
-                  L.Qout, L.Sout, L.Wout};
+    void *ps[] = {L.conv_w, L.A_log, L.dt_bias, L.gnorm, L.conv_st, L.S, L.phase, L.o_raw, L.ssq,
+                  L.cnt, L.Qin, L.Sin, L.Win, L.Qout, L.Sout, L.Wout};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     L = DevLayer{};
@@ -106,8 +110,18 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 LayerPtrs ptrs(const DevLayer &L) {
     LayerPtrs p;
     p.conv_w = L.conv_w; p.A_log = L.A_log; p.dt_bias = L.dt_bias; p.gnorm = L.gnorm;
-    p.conv_st = L.conv_st; p.S = L.S;
+    p.conv_st = L.conv_st; p.S = L.S; p.phase = L.phase;
+    p.o_raw = L.o_raw; p.ssq = L.ssq; p.cnt = L.cnt;
+    p.epoch = L.epoch; p.max_seqs = L.max_seqs;
     return p;
+}
+
+// Column slices per value head for decode: OMH_DECODE_NCS (1, 2, 4 or 8)
+// overrides the kernel's default; read per call so it can be changed at run
+// time for tuning and tests.
+int decode_ncs() {
+    const char *e = getenv("OMH_DECODE_NCS");
+    return e ? atoi(e) : 0;
 }
 
 // Core decode on device pointers for layers lis[0..nl), B sequences each.
@@ -115,8 +129,11 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
                 int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
                 hipStream_t st) {
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
-    for (int i = 0; i < nl; i++)
+    for (int i = 0; i < nl; i++) {
         if (int rc = check_layer(lis[i])) return rc;
+        for (int j = 0; j < i; j++)
+            if (lis[j] == lis[i]) return fail(OMH_ERR_ARG, "decode_core: layer %d listed twice", lis[i]);
+    }
     const DevLayer &L0 = g_L[lis[0]];
     const omh_gdn_dims &d = L0.d;
     for (int i = 1; i < nl; i++) {
@@ -128,8 +145,9 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
         if (B < 1 || B > g_L[lis[i]].max_seqs)
             return fail(OMH_ERR_ARG, "decode_core: B=%d outside [1, %d] for layer %d", B,
                         g_L[lis[i]].max_seqs, lis[i]);
-    if (!decode_core_supported(d.kd, d.vd, d.vh / d.kh))
-        return fail(OMH_ERR_SHAPE, "decode_core: kd=%d vd=%d rep=%d unsupported", d.kd, d.vd, d.vh / d.kh);
+    if (!decode_core_supported(d.kd, d.vd, d.vh / d.kh, d.conv_k))
+        return fail(OMH_ERR_SHAPE, "decode_core: kd=%d vd=%d rep=%d K=%d unsupported", d.kd, d.vd,
+                    d.vh / d.kh, d.conv_k);
     if (!qkv || !z || !a || !b || !core) return fail(OMH_ERR_ARG, "decode_core: null pointer");
     if (!aligned16(z) || !aligned16(core) || (ld_z % 4) != 0)
         return fail(OMH_ERR_ARG, "decode_core: z/core must be 16-byte aligned rows");
@@ -146,7 +164,8 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
         A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
         A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
         for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
-        HIP_OK(launch_decode_core(A, d.kd, d.vd, st));
+        HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_ncs(), st));
+        for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
     }
     return OMH_OK;
 }
@@ -210,8 +229,9 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
     if (!d || !w || max_seqs < 1) return fail(OMH_ERR_ARG, "layer_init: null dims/weights or max_seqs < 1");
     if (d->kh < 1 || d->vh < d->kh || d->vh % d->kh || d->kd < 1 || d->vd < 1 || d->conv_k < 2)
         return fail(OMH_ERR_ARG, "layer_init: bad dims kh=%d vh=%d kd=%d vd=%d K=%d", d->kh, d->vh, d->kd, d->vd, d->conv_k);
-    if (!decode_core_supported(d->kd, d->vd, d->vh / d->kh))
-        return fail(OMH_ERR_SHAPE, "layer_init: kd=%d vd=%d rep=%d unsupported", d->kd, d->vd, d->vh / d->kh);
+    if (!decode_core_supported(d->kd, d->vd, d->vh / d->kh, d->conv_k))
+        return fail(OMH_ERR_SHAPE, "layer_init: kd=%d vd=%d rep=%d K=%d unsupported", d->kd, d->vd,
+                    d->vh / d->kh, d->conv_k);
     if (!w->conv_w || !w->A_log || !w->dt_bias || !w->gnorm) return fail(OMH_ERR_ARG, "layer_init: core weights missing");
     if (g_L[li].live) free_layer(g_L[li]);
     DevLayer L;
@@ -226,10 +246,18 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
     UP(L.A_log, vh, w->A_log);
     UP(L.dt_bias, vh, w->dt_bias);
     UP(L.gnorm, d->vd, w->gnorm);
-    UP(L.conv_st, (size_t)max_seqs * L.conv_dim * (K - 1), (const float *)nullptr);
-    UP(L.S, (size_t)max_seqs * vh * d->kd * d->vd, (const float *)nullptr);
-    if (hipMemset(L.conv_st, 0, (size_t)max_seqs * L.conv_dim * (K - 1) * sizeof(float)) != hipSuccess ||
-        hipMemset(L.S, 0, (size_t)max_seqs * vh * d->kd * d->vd * sizeof(float)) != hipSuccess) {
+    const size_t nring = (size_t)max_seqs * L.conv_dim * kConvRing;
+    const size_t nS = (size_t)max_seqs * vh * d->kd * d->vd;
+    UP(L.conv_st, nring, (const float *)nullptr);
+    UP(L.S, nS, (const float *)nullptr);
+    UP(L.phase, (size_t)2 * max_seqs, (const int *)nullptr);
+    UP(L.o_raw, (size_t)max_seqs * L.vdim, (const float *)nullptr);
+    UP(L.ssq, (size_t)max_seqs * vh * kMaxSlices, (const float *)nullptr);
+    UP(L.cnt, (size_t)max_seqs * vh, (const int *)nullptr);
+    if (hipMemset(L.conv_st, 0, nring * sizeof(float)) != hipSuccess ||
+        hipMemset(L.S, 0, nS * sizeof(float)) != hipSuccess ||
+        hipMemset(L.phase, 0, 2 * max_seqs * sizeof(int)) != hipSuccess ||
+        hipMemset(L.cnt, 0, (size_t)max_seqs * vh * sizeof(int)) != hipSuccess) {
         free_layer(L);
         return fail(OMH_ERR_DEVICE, "layer_init: state clear failed");
     }
@@ -292,11 +320,12 @@ int omh_gdn_state_reset(int li, int seq) {
     if (int rc = check_layer(li)) return rc;
     DevLayer &L = g_L[li];
     if (seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_reset: seq %d >= %d", seq, L.max_seqs);
-    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    const size_t cn = (size_t)L.conv_dim * kConvRing, sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
     const size_t s0 = seq < 0 ? 0 : (size_t)seq, ns = seq < 0 ? (size_t)L.max_seqs : 1;
     HIP_OK(hipDeviceSynchronize());
     HIP_OK(hipMemset(L.conv_st + s0 * cn, 0, ns * cn * sizeof(float)));
     HIP_OK(hipMemset(L.S + s0 * sn, 0, ns * sn * sizeof(float)));
+    HIP_OK(hipMemset(L.phase + (size_t)L.epoch * L.max_seqs + s0, 0, ns * sizeof(int)));
     HIP_OK(hipDeviceSynchronize());
     return OMH_OK;
 }
@@ -306,9 +335,18 @@ int omh_gdn_state_get(int li, int seq, float *conv, float *S) {
     if (int rc = check_layer(li)) return rc;
     DevLayer &L = g_L[li];
     if (seq < 0 || seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_get: seq %d outside [0, %d)", seq, L.max_seqs);
-    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    const int K = L.d.conv_k;
+    const size_t cn = (size_t)L.conv_dim * kConvRing, sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
     HIP_OK(hipDeviceSynchronize());
-    if (conv) HIP_OK(hipMemcpy(conv, L.conv_st + seq * cn, cn * sizeof(float), hipMemcpyDeviceToHost));
+    if (conv) {
+        std::vector<float> ring(cn);
+        int ph = 0;
+        HIP_OK(hipMemcpy(ring.data(), L.conv_st + seq * cn, cn * sizeof(float), hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(&ph, L.phase + (size_t)L.epoch * L.max_seqs + seq, sizeof(int), hipMemcpyDeviceToHost));
+        for (int c = 0; c < L.conv_dim; c++)
+            for (int j = 0; j < K - 1; j++)
+                conv[(size_t)c * (K - 1) + j] = ring[(size_t)c * kConvRing + ring_slot(ph, K, j)];
+    }
     if (S) HIP_OK(hipMemcpy(S, L.S + seq * sn, sn * sizeof(float), hipMemcpyDeviceToHost));
     return OMH_OK;
 }
@@ -318,9 +356,18 @@ int omh_gdn_state_set(int li, int seq, const float *conv, const float *S) {
     if (int rc = check_layer(li)) return rc;
     DevLayer &L = g_L[li];
     if (seq < 0 || seq >= L.max_seqs) return fail(OMH_ERR_ARG, "state_set: seq %d outside [0, %d)", seq, L.max_seqs);
-    const size_t cn = (size_t)L.conv_dim * (L.d.conv_k - 1), sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
+    const int K = L.d.conv_k;
+    const size_t cn = (size_t)L.conv_dim * kConvRing, sn = (size_t)L.d.vh * L.d.kd * L.d.vd;
     HIP_OK(hipDeviceSynchronize());
-    if (conv) HIP_OK(hipMemcpy(L.conv_st + seq * cn, conv, cn * sizeof(float), hipMemcpyHostToDevice));
+    if (conv) {
+        std::vector<float> ring(cn, 0.f);       // written at phase 0
+        for (int c = 0; c < L.conv_dim; c++)
+            for (int j = 0; j < K - 1; j++)
+                ring[(size_t)c * kConvRing + ring_slot(0, K, j)] = conv[(size_t)c * (K - 1) + j];
+        const int zero = 0;
+        HIP_OK(hipMemcpy(L.conv_st + seq * cn, ring.data(), cn * sizeof(float), hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(L.phase + (size_t)L.epoch * L.max_seqs + seq, &zero, sizeof(int), hipMemcpyHostToDevice));
+    }
     if (S) HIP_OK(hipMemcpy(L.S + seq * sn, S, sn * sizeof(float), hipMemcpyHostToDevice));
     return OMH_OK;
 }

@@ -6,15 +6,35 @@
 
 namespace omh {
 
-// Device pointers of one layer's core weights and state.
+// Conv history ring: every channel keeps kConvRing slots; at phase p the
+// K-1 history values, oldest first, sit in slots (p + kConvRing+1 - K + j)
+// mod kConvRing and slot p mod kConvRing is free.  Consuming a token writes
+// it into the free slot and advances p.  Readers never touch the free slot,
+// so any number of workgroups may read a channel while its owner appends.
+constexpr int kConvRing = 4;          // supports conv kernels K = 2..4
+
+__host__ __device__ inline int ring_slot(int p, int K, int j) {
+    return (p + kConvRing + 1 - K + j) & (kConvRing - 1);
+}
+
+// Device pointers of one layer's core weights and state.  The per-sequence
+// ring phase is double-buffered by launch parity (epoch): a decode launch
+// reads phase[epoch][b] and writes phase[1-epoch][b], and the host flips
+// the layer's epoch after enqueueing it.
 struct LayerPtrs {
     const float *conv_w;   // [conv_dim][K]
     const float *A_log;    // [vh]
     const float *dt_bias;  // [vh]
     const float *gnorm;    // [vd]
-    float *conv_st;        // [max_seqs][conv_dim][K-1]
+    float *conv_st;        // [max_seqs][conv_dim][kConvRing] ring
     float *S;              // [max_seqs][vh][kd][vd]
+    int *phase;            // [2][max_seqs]
+    float *o_raw;          // [max_seqs][vh][vd]   cross-slice gated-norm scratch
+    float *ssq;            // [max_seqs][vh][kMaxSlices]
+    int *cnt;              // [max_seqs][vh]  arrivals (reset to 0 by the last)
+    int epoch, max_seqs;
 };
+constexpr int kMaxSlices = 8;
 
 // Decode-core launch: nl layers x B sequences, one token each.
 constexpr int kMaxDecodeLayers = 32;
@@ -46,8 +66,9 @@ struct ProjArgs {
 };
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
 
-// Returns hipSuccess, or hipErrorInvalidValue for an unsupported (kd, vd, rep).
-hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, hipStream_t st);
-bool decode_core_supported(int kd, int vd, int rep);
+// Returns hipSuccess, or hipErrorInvalidValue for an unsupported shape.
+// ncs = column slices per value head (0: the kernel's default for kd, vd).
+hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int ncs, hipStream_t st);
+bool decode_core_supported(int kd, int vd, int rep, int K);
 
 }  // namespace omh

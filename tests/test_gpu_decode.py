@@ -149,3 +149,74 @@ def test_argument_errors_are_reported():
     with pytest.raises(gdn.OmhError):
         L.decode(np.zeros((1, 128), np.float32))                       # core-only layer
     L.free()
+
+
+@pytest.mark.parametrize("ncs", [1, 2, 4, 8])
+def test_column_slices_agree_with_oracle(ncs, monkeypatch):
+    """Every column-slice count (incl. the cross-slice gated-norm epilogue)."""
+    monkeypatch.setenv("OMH_DECODE_NCS", str(ncs))
+    d = GdnDims(2, 4, 128, 128, 4, 0)
+    w = synth.layer_weights(d, 70 + ncs, gnorm_std=0.2, projections=False)
+    T = 3
+    inp = synth.core_inputs(d, T, 70 + ncs)
+    conv0, S0 = synth.states(d, 70 + ncs)
+    L = gdn.GdnLayer(new_li(), d, w)
+    L.set_state(0, conv0, S0)
+    got = np.concatenate([L.decode_core(inp["qkv"][t:t + 1], inp["z"][t:t + 1], inp["a"][t:t + 1],
+                                        inp["b"][t:t + 1]) for t in range(T)])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    conv, S = L.get_state(0)
+    assert_close(got, ref, what=f"ncs={ncs} core")
+    assert_close(S, Sref, what=f"ncs={ncs} S")
+    assert np.array_equal(conv, cref)
+    L.free()
+
+
+def test_varying_batch_keeps_each_sequence_history():
+    """Calls with B = 3, 1, 2, 3, 1 on one layer: sequences left out of a call
+    keep their conv history and phase; each matches its own oracle run."""
+    d = CFG1
+    w = synth.layer_weights(d, 80, gnorm_std=0.1, projections=False)
+    conv0, S0 = synth.states(d, 80, B=3)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=3)
+    for s in range(3):
+        L.set_state(s, conv0[s], S0[s])
+    plan = [3, 1, 2, 3, 1, 3]
+    inp = synth.core_inputs(d, len(plan), 81, B=3)
+    fed = {s: [] for s in range(3)}
+    outs = {s: [] for s in range(3)}
+    for t, B in enumerate(plan):
+        core = L.decode_core(inp["qkv"][:B, t], inp["z"][:B, t], inp["a"][:B, t], inp["b"][:B, t])
+        for s in range(B):
+            fed[s].append(t)
+            outs[s].append(core[s])
+    for s in range(3):
+        ts = fed[s]
+        ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"][s, ts], inp["z"][s, ts], inp["a"][s, ts],
+                                          inp["b"][s, ts], conv0[s], S0[s])
+        conv, S = L.get_state(s)
+        assert_close(np.stack(outs[s]), ref, what=f"seq {s}")
+        assert_close(S, Sref, what=f"seq {s} S")
+        assert np.array_equal(conv, cref), f"seq {s} conv history"
+    L.free()
+
+
+def test_state_set_mid_stream_restarts_history():
+    """state_set after some decode steps (ring phase != 0) re-bases the ring."""
+    d = CFG1
+    w = synth.layer_weights(d, 90, projections=False)
+    L = gdn.GdnLayer(new_li(), d, w)
+    inp = synth.core_inputs(d, 7, 90)
+    for t in range(5):
+        L.decode_core(inp["qkv"][t:t + 1], inp["z"][t:t + 1], inp["a"][t:t + 1], inp["b"][t:t + 1])
+    conv0, S0 = synth.states(d, 91)
+    L.set_state(0, conv0, S0)
+    c, S = L.get_state(0)
+    assert np.array_equal(c, conv0) and np.array_equal(S, S0)
+    got = np.concatenate([L.decode_core(inp["qkv"][t:t + 1], inp["z"][t:t + 1], inp["a"][t:t + 1],
+                                        inp["b"][t:t + 1]) for t in (5, 6)])
+    ref, cref, _ = oracle.core_seq(d, w, inp["qkv"][5:7], inp["z"][5:7], inp["a"][5:7], inp["b"][5:7],
+                                   conv0, S0)
+    assert_close(got, ref)
+    assert np.array_equal(L.get_state(0)[0], cref)
+    L.free()
