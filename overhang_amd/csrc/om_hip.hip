@@ -71,7 +71,7 @@ struct Scratch {
     void *p = nullptr;
     size_t n = 0;
 };
-Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b;
+Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre;
 
 int ensure(Scratch &s, size_t bytes) {
     if (bytes <= s.n) return OMH_OK;
@@ -190,6 +190,57 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     ProjArgs q{};
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
+    HIP_OK(launch_proj(q, st));
+    return OMH_OK;
+}
+
+// Chunked prefill of T tokens of sequence seq on device pointers.
+int prefill_core(int li, int seq, int T, const float *qkv, int64_t ld_qkv, const float *z, int64_t ld_z,
+                 const float *a, const float *b, int64_t ld_ab, float *core, hipStream_t st) {
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    const omh_gdn_dims &d = L.d;
+    if (seq < 0 || seq >= L.max_seqs) return fail(OMH_ERR_ARG, "prefill: seq %d outside [0, %d)", seq, L.max_seqs);
+    if (T < 0) return fail(OMH_ERR_ARG, "prefill: T=%d", T);
+    if (T == 0) return OMH_OK;
+    if (!prefill_supported(d.kd, d.vd, d.vh / d.kh, d.conv_k))
+        return fail(OMH_ERR_SHAPE, "prefill: kd=%d vd=%d rep=%d K=%d unsupported", d.kd, d.vd, d.vh / d.kh, d.conv_k);
+    if (!qkv || !z || !a || !b || !core) return fail(OMH_ERR_ARG, "prefill: null pointer");
+    if (!aligned16(z) || !aligned16(core) || (ld_z % 4) != 0)
+        return fail(OMH_ERR_ARG, "prefill: z/core must be 16-byte aligned rows");
+    const int D = d.kd;
+    PrefillArgs A{};
+    A.qkv = qkv; A.ld_qkv = ld_qkv; A.z = z; A.ld_z = ld_z; A.a = a; A.b = b; A.ld_ab = ld_ab; A.core = core;
+    A.L = ptrs(L);
+    A.seq = seq; A.T = T; A.nc = (T + kChunk - 1) / kChunk; A.Tp = A.nc * kChunk;
+    A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
+    if (int rc = ensure(g_pre, prefill_scratch_bytes(D, d.kh, d.vh, T))) return rc;
+    prefill_bind_scratch(A, D, g_pre.p);
+    HIP_OK(launch_prefill_core(A, D, st));
+    return OMH_OK;
+}
+
+int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t st) {
+    if (int rc = check_layer(li)) return rc;
+    DevLayer &L = g_L[li];
+    if (!L.has_proj) return fail(OMH_ERR_ARG, "layer %d was initialised without projections", li);
+    if (T < 0) return fail(OMH_ERR_ARG, "prefill: T=%d", T);
+    if (T == 0) return OMH_OK;
+    if (!x || !out || !aligned16(x) || !aligned16(out)) return fail(OMH_ERR_ARG, "prefill: x/out must be 16-byte aligned");
+    const int D = L.d.hidden;
+    if (int rc = ensure(g_in, (size_t)T * L.in_rows * sizeof(float))) return rc;
+    if (int rc = ensure(g_core, (size_t)T * L.vdim * sizeof(float))) return rc;
+    float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
+    ProjArgs p{};
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows;
+    p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
+    HIP_OK(launch_proj(p, st));
+    const int vh = L.d.vh;
+    const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
+    if (int rc = prefill_core(li, seq, T, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
+    ProjArgs q{};
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D;
+    q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
 }
@@ -429,25 +480,57 @@ int omh_gdn_decode(int li, int B, const float *x, float *out) {
 }
 
 int omh_gdn_prefill(int li, int seq, int T, const float *x, float *out) {
-    (void)li; (void)seq; (void)T; (void)x; (void)out;
-    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    const DevLayer &L = g_L[li];
+    if (!L.has_proj) return fail(OMH_ERR_ARG, "layer %d was initialised without projections", li);
+    if (T < 0 || (T > 0 && (!x || !out))) return fail(OMH_ERR_ARG, "prefill: bad arguments");
+    if (T == 0) return OMH_OK;
+    const size_t n = (size_t)T * L.d.hidden;
+    if (int rc = ensure(g_x, n * 4)) return rc;
+    if (int rc = ensure(g_out, n * 4)) return rc;
+    HIP_OK(hipMemcpyAsync(g_x.p, x, n * 4, hipMemcpyHostToDevice, g_stream));
+    if (int rc = prefill_full(li, seq, T, (const float *)g_x.p, (float *)g_out.p, g_stream)) return rc;
+    HIP_OK(hipMemcpyAsync(out, g_out.p, n * 4, hipMemcpyDeviceToHost, g_stream));
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
 }
 
 int omh_gdn_prefill_core(int li, int seq, int T, const float *qkv, const float *z, const float *a,
                          const float *b, float *core) {
-    (void)li; (void)seq; (void)T; (void)qkv; (void)z; (void)a; (void)b; (void)core;
-    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    const DevLayer &L = g_L[li];
+    if (T < 0 || (T > 0 && (!qkv || !z || !a || !b || !core))) return fail(OMH_ERR_ARG, "prefill_core: bad arguments");
+    if (T == 0) return OMH_OK;
+    const size_t nq = (size_t)T * L.conv_dim, nz = (size_t)T * L.vdim, nab = (size_t)T * L.d.vh;
+    if (int rc = ensure(g_qkv, nq * 4)) return rc;
+    if (int rc = ensure(g_z, nz * 4)) return rc;
+    if (int rc = ensure(g_a, nab * 4)) return rc;
+    if (int rc = ensure(g_b, nab * 4)) return rc;
+    if (int rc = ensure(g_core, nz * 4)) return rc;
+    float *dq = (float *)g_qkv.p, *dz = (float *)g_z.p, *da = (float *)g_a.p, *db = (float *)g_b.p, *dc = (float *)g_core.p;
+    HIP_OK(hipMemcpyAsync(dq, qkv, nq * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(dz, z, nz * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(da, a, nab * 4, hipMemcpyHostToDevice, g_stream));
+    HIP_OK(hipMemcpyAsync(db, b, nab * 4, hipMemcpyHostToDevice, g_stream));
+    if (int rc = prefill_core(li, seq, T, dq, L.conv_dim, dz, L.vdim, da, db, L.d.vh, dc, g_stream)) return rc;
+    HIP_OK(hipMemcpyAsync(core, dc, nz * 4, hipMemcpyDeviceToHost, g_stream));
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
 }
 
 int omh_gdn_prefill_core_dev(int li, int seq, int T, const float *qkv, const float *z, const float *a,
                              const float *b, float *core, void *stream) {
-    (void)li; (void)seq; (void)T; (void)qkv; (void)z; (void)a; (void)b; (void)core; (void)stream;
-    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_layer(li)) return rc;
+    const DevLayer &L = g_L[li];
+    return prefill_core(li, seq, T, qkv, L.conv_dim, z, L.vdim, a, b, L.d.vh, core, static_cast<hipStream_t>(stream));
 }
 
 int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void *stream) {
-    (void)li; (void)seq; (void)T; (void)x; (void)out; (void)stream;
-    return fail(OMH_ERR_SHAPE, "prefill not available yet");
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    return prefill_full(li, seq, T, x, out, static_cast<hipStream_t>(stream));
 }
 
 int omh_sync(void *stream) {

@@ -66,6 +66,30 @@ struct ProjArgs {
 };
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
 
+// Chunked prefill of T tokens of one sequence (kd == vd == D).
+constexpr int kChunk = 64;
+struct PrefillArgs {
+    // inputs, token-major rows
+    const float *qkv; int64_t ld_qkv;    // [T][>= conv_dim]
+    const float *z;   int64_t ld_z;      // [T][>= vh*vd]
+    const float *a, *b; int64_t ld_ab;   // [T][>= vh]
+    float *core;                         // [T][vh*vd]
+    // the sequence's state and the layer's weights
+    LayerPtrs L;
+    int seq;
+    int T, Tp, nc;                       // tokens, padded to kChunk, chunks
+    int kh, vh, K;
+    float eps;
+    // scratch (device), sized by prefill_scratch_bytes()
+    float *qn, *kn, *v, *g, *beta;       // head-major P1 outputs
+    float *gc, *glast;                   // cumulative log-decay [vh][Tp], exp(g_last) [vh][nc]
+    float *pw, *pq, *pk, *pa, *pu;       // per-chunk operand panels for the scan
+};
+size_t prefill_scratch_bytes(int D, int kh, int vh, int T);
+void prefill_bind_scratch(PrefillArgs &a, int D, void *base);
+bool prefill_supported(int kd, int vd, int rep, int K);
+hipError_t launch_prefill_core(const PrefillArgs &a, int D, hipStream_t st);
+
 // Returns hipSuccess, or hipErrorInvalidValue for an unsupported shape.
 // ncs = column slices per value head (0: the kernel's default for kd, vd).
 hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int ncs, hipStream_t st);

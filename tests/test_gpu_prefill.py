@@ -1,0 +1,171 @@
+"""GPU parity of the chunked prefill through the C-ABI.
+
+The reference engine prefills token by token (overhang engines/qwen.c:588,
+637); the chunked form must agree with that recurrence (the CPU oracle, and
+the reference's own golden vectors) on outputs and final state, at every
+length around the 64-token chunk boundary, across split points, mixed with
+decode steps, at the Qwen3.6-35B-A3B shape up to T=4096, and under strong
+decay.  Tolerance: tests/tol.py."""
+import numpy as np
+import pytest
+
+import oracle
+from overhang_amd import gdn, synth
+from overhang_amd.dims import GdnDims, Q35B, CFG1, TINY
+from tests import fixtures
+from tests.tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+_next_li = [500]
+
+
+def new_li():
+    _next_li[0] += 1
+    return _next_li[0]
+
+
+def _layer(d, seed, gnorm_std=0.1, max_seqs=1):
+    w = synth.layer_weights(d, seed, gnorm_std=gnorm_std, projections=False)
+    conv0, S0 = synth.states(d, seed)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=max_seqs)
+    L.set_state(0, conv0, S0)
+    return L, w, conv0, S0
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128])
+@pytest.mark.parametrize("T", [1, 3, 63, 64, 65, 130])
+def test_prefill_matches_recurrent_oracle(D, T):
+    d = GdnDims(2, 4, D, D, 4, 0)
+    seed = 1000 + D + T
+    L, w, conv0, S0 = _layer(d, seed)
+    inp = synth.core_inputs(d, T, seed)
+    core = L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    conv, S = L.get_state(0)
+    assert_close(core, ref, what=f"D={D} T={T} core")
+    assert_close(S, Sref, what=f"D={D} T={T} S")
+    assert np.array_equal(conv, cref), "conv history is a copy of the inputs"
+    L.free()
+
+
+@pytest.mark.parametrize("name", ["core_rep3_d16", "core_d128", "core_d32_decay"])
+def test_prefill_matches_reference_golden(name):
+    d, w, inp, (conv, S), exp = fixtures.load(name)
+    L = gdn.GdnLayer(new_li(), d, w)
+    L.set_state(0, conv, S)
+    core = L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    conv2, S2 = L.get_state(0)
+    assert_close(core, exp["core"], what=f"{name} core")
+    assert_close(S2, exp["S"], what=f"{name} S")
+    assert np.array_equal(conv2, exp["conv"])
+    L.free()
+
+
+@pytest.mark.parametrize("name", fixtures.LAYER_FIXTURES)
+def test_full_layer_prefill_matches_reference_golden(name):
+    d, w, inp, (conv, S), exp = fixtures.load(name)
+    L = gdn.GdnLayer(new_li(), d, w, int8=exp["int8"])
+    L.set_state(0, conv, S)
+    out = L.prefill(0, inp["x"])
+    conv2, S2 = L.get_state(0)
+    assert_close(out, exp["out"], what=f"{name} out")
+    assert_close(S2, exp["S"], what=f"{name} S")
+    assert_close(conv2, exp["conv"], atol=1e-5, rtol=1e-5)
+    L.free()
+
+
+def test_unsupported_prefill_shape_is_rejected():
+    d, w, inp, (conv, S), exp = fixtures.load("core_kd32_vd16")
+    L = gdn.GdnLayer(new_li(), d, w)
+    with pytest.raises(gdn.OmhError) as e:
+        L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    assert e.value.code == gdn.OMH_ERR_SHAPE
+    L.free()
+
+
+@pytest.mark.parametrize("split", [[1, 199], [64, 136], [100, 37, 63], [5, 5, 5, 185]])
+def test_split_invariance_and_decode_interleave(split):
+    """prefill(T1); prefill(T2); ... == one recurrent pass over T1+T2+...,
+    with a decode step between the pieces."""
+    d = GdnDims(2, 4, 32, 32, 4, 0)
+    seed = 2000 + sum(split) + len(split)
+    L, w, conv0, S0 = _layer(d, seed)
+    T = sum(split) + len(split) - 1
+    inp = synth.core_inputs(d, T, seed)
+    got, t = [], 0
+    for i, n in enumerate(split):
+        sl = slice(t, t + n)
+        got.append(L.prefill_core(0, inp["qkv"][sl], inp["z"][sl], inp["a"][sl], inp["b"][sl]))
+        t += n
+        if i < len(split) - 1:
+            sl = slice(t, t + 1)
+            got.append(L.decode_core(inp["qkv"][sl], inp["z"][sl], inp["a"][sl], inp["b"][sl]))
+            t += 1
+    got = np.concatenate(got)
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    conv, S = L.get_state(0)
+    assert_close(got, ref, what=f"split {split}")
+    assert_close(S, Sref, what=f"split {split} S")
+    assert np.array_equal(conv, cref)
+    L.free()
+
+
+def test_prefill_leaves_other_sequences_alone():
+    d = CFG1
+    w = synth.layer_weights(d, 3000, projections=False)
+    conv0, S0 = synth.states(d, 3000, B=3)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=3)
+    for s in range(3):
+        L.set_state(s, conv0[s], S0[s])
+    inp = synth.core_inputs(d, 70, 3001)
+    core = L.prefill_core(1, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0[1], S0[1])
+    assert_close(core, ref)
+    for s in (0, 2):
+        c, S = L.get_state(s)
+        assert np.array_equal(c, conv0[s]) and np.array_equal(S, S0[s])
+    # a batched decode of all three afterwards continues each sequence correctly
+    nxt = synth.core_inputs(d, 1, 3002, B=3)
+    out = L.decode_core(nxt["qkv"][:, 0], nxt["z"][:, 0], nxt["a"][:, 0], nxt["b"][:, 0])
+    starts = {0: (conv0[0], S0[0]), 1: (cref, Sref), 2: (conv0[2], S0[2])}
+    for s in range(3):
+        r, _, _ = oracle.core_seq(d, w, nxt["qkv"][s], nxt["z"][s], nxt["a"][s], nxt["b"][s], *starts[s])
+        assert_close(out[s:s + 1], r, what=f"seq {s} decode after prefill")
+    L.free()
+
+
+@pytest.mark.parametrize("T", [300, 4096])
+def test_prefill_35b_shape(T):
+    """Qwen3.6-35B-A3B GDN shape (16 key / 32 value heads, d=128); T=4096 is
+    the prefill benchmark's length."""
+    d = Q35B
+    seed = 4000 + T
+    L, w, conv0, S0 = _layer(d, seed)
+    inp = synth.core_inputs(d, T, seed)
+    core = L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    conv, S = L.get_state(0)
+    assert_close(core, ref, what=f"35B T={T} core")
+    assert_close(S, Sref, what=f"35B T={T} S")
+    assert np.array_equal(conv, cref)
+    L.free()
+
+
+def test_prefill_strong_decay():
+    """Gate logits a ~ N(2, 1) with A_log = ln 16: per-chunk cumulative decay
+    far below exp(-100); only decay differences are exponentiated."""
+    d = GdnDims(2, 4, 64, 64, 4, 0)
+    w = synth.layer_weights(d, 5000, gnorm_std=0.1, projections=False)
+    w["A_log"][:] = np.log(16.0)
+    conv0, S0 = synth.states(d, 5000)
+    L = gdn.GdnLayer(new_li(), d, w)
+    L.set_state(0, conv0, S0)
+    T = 400
+    inp = synth.core_inputs(d, T, 5000, a_mean=2.0)
+    core = L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    assert np.isfinite(core).all()
+    assert_close(core, ref, what="strong decay core")
+    assert_close(L.get_state(0)[1], Sref, what="strong decay S")
+    L.free()
