@@ -9,10 +9,14 @@ a different set of 30 layer states out of >1 GiB so the 256 MB Infinity
 Cache cannot hold them (each step reads and writes 126 MB of state from HBM).
 
 Also reported: the same step launched layer by layer (the order an engine
-runs it), a batch sweep B=1..64 of one-layer launches, and the CPU oracle
-(the reference GDN restated in C, OpenMP) on the host cores.
+runs it), a batch sweep B=1..64 of one-layer launches, the chunked prefill
+of T=4096 tokens at the same head shape (MFMA roofline), a device-to-device
+copy of the decode step's bytes (the HBM bandwidth a plain copy reaches on
+this box), and the CPU oracle (the reference GDN restated in C, OpenMP) on
+the host cores.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--part all|decode|prefill]
 """
 from __future__ import annotations
 
@@ -81,7 +85,7 @@ def time_launches(hip, st, fn, steps, warmup):
     return max(el, 1e-12), durs, wall
 
 
-def bench_decode(hip, gdn, synth, steps, warmup):
+def bench_decode(hip, gdn, synth, steps, warmup, full=True):
     from overhang_amd.dims import Q35B
     d = Q35B
     per_layer = d.state_bytes + 4 * d.conv_dim * (d.K - 1)
@@ -102,11 +106,19 @@ def bench_decode(hip, gdn, synth, steps, warmup):
 
     el, durs, wall = time_launches(hip, st, step_fused, steps, warmup)
     alg_bytes = N_LAYERS * 2 * d.state_bytes                # state read + write, 30 layers
-    kern = statistics.mean(durs)
+    # average launch duration = the timed region of back-to-back launches / launches
+    kern = el / steps
     fused = {"tok_s": steps / el, "ms_per_step": 1e3 * el / steps, "kernel_us": 1e6 * kern,
+             "kernel_us_isolated": 1e6 * statistics.mean(durs),
              "achieved_GBs": alg_bytes / kern / 1e9, "wall_s": wall}
     log(f"decode fused 30-layer launch: {fused['tok_s']:.0f} tok/s, kernel {fused['kernel_us']:.1f} us, "
         f"{fused['achieved_GBs']:.0f} GB/s")
+
+    if not full:
+        for L in lays:
+            L.free()
+        hip.device_synchronize()
+        return fused, None, None, alg_bytes, R
 
     # engine order: one launch per layer
     def step_layers(k):
@@ -139,7 +151,7 @@ def bench_decode(hip, gdn, synth, steps, warmup):
                                 stream=st)
         nsteps = max(steps, 20)
         elB, dB, _ = time_launches(hip, st, stepB, nsteps, warmup)
-        kb = statistics.mean(dB)
+        kb = elB / nsteps
         gbs = B * 2 * d.state_bytes / kb / 1e9
         sweep.append({"B": B, "kernel_us": 1e6 * kb, "achieved_GBs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
                       "tok_s_30_layers": B / (N_LAYERS * kb)})
@@ -148,6 +160,94 @@ def bench_decode(hip, gdn, synth, steps, warmup):
         L.free()
     hip.device_synchronize()
     return fused, engine, sweep, alg_bytes, R
+
+
+def copy_probe(hip, nbytes, steps, warmup):
+    """Device-to-device copy of nbytes (reads nbytes, writes nbytes): the HBM
+    bandwidth a plain copy reaches on this box, next to the spec peak.  The
+    buffers are far larger than the 256 MB Infinity Cache."""
+    src, dst = hip.Buffer(nbytes), hip.Buffer(nbytes)
+    st = hip.Stream()
+
+    def one(k):
+        hip.ok(hip.rt().hipMemcpyAsync(dst.ptr, src.ptr, nbytes, hip.D2D, st.cuda_stream))
+
+    el, _, _ = time_launches(hip, st, one, steps, warmup)
+    src.close()
+    dst.close()
+    t = el / steps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": 1e6 * t, "GBs": 2 * nbytes / t / 1e9}
+
+
+def prefill_flops(d, T, C=64):
+    """Algorithmic FLOPs of the chunked WY/UT prefill of T tokens (per layer):
+    per value head and chunk 2C^2(3kd + 2vd) for K K^T, Q K^T, W, U and
+    Aqk v_new, 6 C kd vd for W S, (Q e^g) S and the state update, and C^3/3
+    for the triangular inverse."""
+    nc = -(-T // C)
+    return d.vh * nc * (2 * C * C * (3 * d.kd + 2 * d.vd) + 6 * C * d.kd * d.vd + C ** 3 / 3)
+
+
+def prefill_bytes(d, T):
+    """Compulsory HBM bytes of a core prefill of T tokens: q, k (read as
+    mixed_qkv), v, z in; core out; a, b in; the state read and written."""
+    return (2 * T * d.kh * d.kd * 4 + 2 * T * d.vh * d.vd * 4 + 2 * T * d.vh * 4
+            + 2 * d.state_bytes)
+
+
+def bench_prefill(hip, gdn, synth, T, steps, warmup):
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = synth.layer_weights(d, 0, projections=False)
+    L = gdn.GdnLayer(2000, d, w, max_seqs=1)
+    inp = synth.core_inputs(d, T, 7)
+    dev = {k: hip.Buffer.from_numpy(v) for k, v in inp.items()}
+    core = hip.Buffer(T * d.val_dim * 4)
+    st = hip.Stream()
+
+    def one(k):
+        gdn.prefill_core_dev(L.li, 0, T, dev["qkv"], dev["z"], dev["a"], dev["b"], core, stream=st)
+
+    el, durs, _ = time_launches(hip, st, one, steps, warmup)
+    L.free()
+    t = el / steps
+    fl = prefill_flops(d, T)
+    by = prefill_bytes(d, T)
+    tf = fl / t / 1e12
+    # attainable fp32 roofline at this arithmetic intensity
+    attain = min(FP32_MFMA_TFLOPS, fl / by * HBM_PEAK_GBS / 1e3)
+    out = {"T": T, "chunk": 64, "tok_s": T * steps / el, "us_per_call": 1e6 * t,
+           "flops_per_call": fl, "TFLOPs": tf, "peak_TFLOPs": FP32_MFMA_TFLOPS,
+           "frac_fp32_mfma": tf / FP32_MFMA_TFLOPS, "frac_attainable": tf / attain,
+           "hbm_bytes_alg": by, "recurrent_equiv_GFLOP": 7 * d.vh * T * d.kd * d.vd / 1e9,
+           "note": "one GDN layer core (5 launches: prep, conv commit, chunk, scan, gated norm), "
+                   "kh=16 vh=32 kd=vd=128, fp32 I/O and fp32 MFMA, state carried across calls"}
+    log(f"prefill T={T}: {1e6 * t:.0f} us/layer, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
+        f"({100 * out['frac_fp32_mfma']:.1f}% of fp32 MFMA peak)")
+    return out
+
+
+def cpu_prefill_baseline(synth, T=256, budget_s=8.0):
+    """The oracle prefills token by token (the reference has no chunked CPU
+    path): one layer core at the 35B shape over a bounded sample of T tokens."""
+    import oracle
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = synth.layer_weights(d, 0, projections=False)
+    inp = synth.core_inputs(d, T, 7)
+    conv0 = np.zeros((d.conv_dim, d.K - 1), np.float32)
+    S0 = np.zeros((d.vh, d.kd, d.vd), np.float32)
+    oracle.core_seq(d, w, inp["qkv"][:8], inp["z"][:8], inp["a"][:8], inp["b"][:8], conv0, S0)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": T / med, "unit": "tok/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{len(times)} runs of {T} tokens through one GDN layer core at the 35B shape, "
+                      f"token by token (median {1e3 * med:.0f} ms per run)"}
 
 
 def cpu_decode_baseline(synth, budget_s=10.0):
@@ -196,12 +296,26 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def committed_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--part", choices=("all", "decode", "prefill"), default="all",
+                    help="decode: the headline only (for profiling); prefill: the T=4096 prefill only")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN layer needs no collectives and this build "
@@ -210,13 +324,28 @@ def main():
     from overhang_amd import gdn, hip, synth
     gdn.require_gpu()
     log("device: gfx950 ready")
-    fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup)
+    if a.part == "prefill":
+        pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 3), a.warmup)
+        print(json.dumps({"prefill": pre}), flush=True)
+        return
+    fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
+                                                      full=a.part == "all")
+    pre = probe = None
+    if a.part == "all":
+        pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
+        probe = copy_probe(hip, 1 << 29, 20, 3)
+        log(f"copy probe: {probe['GBs']:.0f} GB/s (D2D copy of 512 MiB)")
     cpu = None
     if not a.no_cpu:
         log("cpu baseline (oracle, OpenMP) ...")
         cpu = cpu_decode_baseline(synth)
         log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        if pre is not None:
+            pre["cpu_baseline"] = cpu_prefill_baseline(synth)
+            log(f"cpu prefill baseline: {pre['cpu_baseline']['value']:.1f} tok/s")
     ach = fused["achieved_GBs"]
+    kname = "gdn_decode_paired_kernel<128, 128, 2>"
+    tr = committed_traffic(kname)
     line = {
         "metric": METRIC,
         "value": round(fused["tok_s"], 1),
@@ -232,12 +361,17 @@ def main():
         "data": "synthetic (splitmix64/Box-Muller, seeded); random-init GDN weights of the 35B GDN shape",
         "config": {"workload": "GDN core decode, 1 token x 30 layers (one launch), B=1, "
                                "kh=16 vh=32 kd=vd=128, fp32 state, pre-projected inputs",
-                   "layers": N_LAYERS, "batch": 1, "state_rotation_GiB": round(R * N_LAYERS * 2.19e6 / 2**30, 2)},
+                   "layers": N_LAYERS, "batch": 1,
+                   "state_rotation_GiB": round(R * N_LAYERS * 2.19e6 / 2**30, 2)},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gdn_decode_core_kernel<128,128,2>", "kernel_us": round(fused["kernel_us"], 2),
-                     "alg_bytes_per_launch": alg_bytes},
+                     "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": None if tr is None else tr["bytes_per_launch"],
+                     "kernel": kname, "kernel_us": round(fused["kernel_us"], 2),
+                     "alg_bytes_per_launch": alg_bytes,
+                     "traffic_source": None if tr is None else tr["source"]},
         "cpu_baseline": cpu,
+        "hbm_copy_probe": probe,
+        "prefill_T4096": pre,
         "decode_engine_order": engine,
         "decode_batch_sweep": sweep,
     }

@@ -9,51 +9,63 @@
 //       S <- S + k delta^T;  o = S^T q;
 //   (4) the gated RMSNorm  o * rsqrt(mean(o^2) + eps) * gnorm * silu(z).
 //
-// The kernel is bound by HBM: each value head's state is read once and
+// The step is bound by HBM: each value head's state is read once and
 // written once (2*kd*vd*4 bytes), with streaming (nontemporal) accesses.
-// The delta rule couples only the rows of one column (kv, delta and o of
-// column j involve S[:, j] alone), so a value head may be split into NCS
-// column slices, one workgroup each (a step of B sequences x nl layers runs
-// nl*B*vh*NCS workgroups); NCS = 1 is the default, see default_ncs().
+// One pass over the state computes both column sums S^T k and S^T q of
+// the old state; with them
+//     kv = gamma S^T k,   delta = beta (v - kv),
+//     o  = gamma S^T q + (k.q) delta        (= (gamma S + k delta^T)^T q),
+// so a head needs a single cross-row reduction, and the second pass only
+// forms gamma S + k delta^T and streams it back.  q and k are kept as raw
+// conv outputs; their L2-norm factors (qwen.c:153-157, 326-329) are applied
+// to the sums and to delta instead of to every element.
 //
-// Each workgroup recomputes the conv + L2 norm of its key head (q and k are
-// needed whole) and the conv of its own value columns.  Conv history lives
-// in a 4-slot ring per channel (omh_internal.h): readers use the K-1 history
-// slots, the single owner of a channel appends the new input into the free
-// slot, so no workgroup ever reads what another writes in the same launch.
-// The gated RMSNorm needs the whole row of o: with NCS > 1 each slice
-// publishes its raw o and its partial sum of squares (device-coherent
-// atomic stores), and the last slice of the head to arrive (arrival
-// counter) applies the norm to all vd columns, summing the partials in
-// slice order, so the result does not depend on arrival order.
+// Two kernels share that contract:
+//  * paired (large launches): one workgroup per (layer, sequence, key head)
+//    handles the rep = vh/kh value heads that share the key head.  The
+//    q/k conv + norm is done once for all of them, and the state of the
+//    next value head is loaded while the current one is reduced and stored,
+//    so every workgroup keeps reads in flight under its own writes.
+//  * sliced (small launches): one workgroup per value head, or per column
+//    slice of one.  The delta rule couples only the rows of one column, so
+//    a head may split into NCS slices.  The gated RMSNorm needs the whole
+//    row of o: each slice
+//    publishes its raw o and its partial sum of squares (device-coherent
+//    atomic stores), and the last slice of the head to arrive (arrival
+//    counter) applies the norm to all vd columns, summing the partials in
+//    slice order, so the result does not depend on arrival order.
+//
+// Conv history lives in a per-channel ring (omh_internal.h): readers use
+// the K-1 history slots, the single owner of a channel rewrites its entry
+// with the new input in the free slot.
 //
 // Thread layout: TPB threads hold RPT rows x 4 adjacent columns (a float4)
-// of the slice; a wavefront's loads cover whole consecutive row segments.
-// Column sums over rows are butterflies across the row groups of a wave,
-// then across waves through LDS.
+// of a head (or slice); a wavefront's loads cover whole consecutive row
+// segments.  Column sums over rows are butterflies across the row groups of
+// a wave, then across waves through LDS.
 #include "omh_device.h"
 #include "omh_internal.h"
 
 namespace omh {
 namespace {
 
-template <int KD, int VD, int NCS>
-struct DecShape {
-    static constexpr int CW = VD / NCS;                     // columns per workgroup
+constexpr int kMaxRep = 8;            // value heads per key head, paired kernel
+
+template <int KD, int CW>
+struct TileShape {
     static constexpr int C4 = CW / 4;                       // float4 columns per row
     static constexpr int TPB_RAW = KD * C4 / 4;             // aim for 4 float4 per thread
     static constexpr int TPB = TPB_RAW < 64 ? 64 : (TPB_RAW > 256 ? 256 : TPB_RAW);
     static constexpr int RG = TPB / C4;                     // row groups
     static constexpr int RPT = KD / RG;                     // rows per thread
     static constexpr int NW = TPB / OMH_WAVE;
-    static_assert(VD % NCS == 0 && CW % 4 == 0 && C4 >= 1 && C4 <= OMH_WAVE, "slice layout");
-    static_assert((C4 & (C4 - 1)) == 0 && TPB % C4 == 0, "slice layout");
+    static_assert(CW % 4 == 0 && C4 >= 1 && C4 <= OMH_WAVE, "tile layout");
+    static_assert((C4 & (C4 - 1)) == 0 && TPB % C4 == 0, "tile layout");
     static_assert(RG >= 1 && KD % RG == 0 && RPT >= 1, "row layout");
-    static_assert(NCS <= kMaxSlices && VD / 4 <= TPB, "norm epilogue layout");
 };
 
-// Whether DecShape<KD, VD, NCS> is a valid layout (checked before use).
-constexpr bool dec_valid_rt(int KD, int VD, int NCS) {
+// Whether TileShape<KD, VD / NCS> with the sliced norm epilogue is valid.
+constexpr bool slice_valid(int KD, int VD, int NCS) {
     if (NCS < 1 || VD % NCS != 0 || (VD / NCS) % 4 != 0 || NCS > kMaxSlices) return false;
     const int c4 = VD / NCS / 4;
     if (c4 < 1 || c4 > OMH_WAVE || (c4 & (c4 - 1)) != 0) return false;
@@ -62,27 +74,32 @@ constexpr bool dec_valid_rt(int KD, int VD, int NCS) {
     const int rg = tpb / c4;
     return tpb % c4 == 0 && rg <= KD && KD % rg == 0 && VD / 4 <= tpb;
 }
-template <int KD, int VD, int NCS>
-constexpr bool dec_valid() { return dec_valid_rt(KD, VD, NCS); }
 
-// Sum a float4 over the row groups of the workgroup.
-template <int C4, int NW>
-__device__ __forceinline__ float4 colsum(float4 x, float4 (*red)[C4], int wave, int lane, int c4) {
+template <int C4>
+__device__ __forceinline__ float4 f4_xor_sum_from(float4 x) {
     x.x = omh_xor_sum_from<C4>(x.x);
     x.y = omh_xor_sum_from<C4>(x.y);
     x.z = omh_xor_sum_from<C4>(x.z);
     x.w = omh_xor_sum_from<C4>(x.w);
-    if constexpr (NW > 1) {
-        if (lane < C4) red[wave][c4] = x;
-        omh_lds_barrier();
-        x = red[0][c4];
-#pragma unroll
-        for (int w = 1; w < NW; w++) {
-            const float4 y = red[w][c4];
-            x.x += y.x; x.y += y.y; x.z += y.z; x.w += y.w;
-        }
-    }
     return x;
+}
+__device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// Sum two float4 over the row groups of the workgroup (red: [NW][2][C4]).
+template <int C4, int NW>
+__device__ __forceinline__ void colsum2(float4 &a, float4 &b, float4 (*red)[2][C4], int wave, int lane, int c4) {
+    a = f4_xor_sum_from<C4>(a);
+    b = f4_xor_sum_from<C4>(b);
+    if constexpr (NW > 1) {
+        if (lane < C4) { red[wave][0][c4] = a; red[wave][1][c4] = b; }
+        omh_lds_barrier();
+        a = red[0][0][c4];
+        b = red[0][1][c4];
+#pragma unroll
+        for (int w = 1; w < NW; w++) { a = f4_add(a, red[w][0][c4]); b = f4_add(b, red[w][1][c4]); }
+    }
 }
 
 __device__ __forceinline__ float4 gated(float4 o, float rn, float4 gn, float4 zz) {
@@ -94,11 +111,256 @@ __device__ __forceinline__ float4 gated(float4 o, float rn, float4 gn, float4 zz
     return y;
 }
 
+// Conv inputs of the NIT channels a thread handles, loaded into registers
+// in one batch (vector memory operations complete in issue order for the
+// wait counter, so the first use waits for exactly these and what came
+// before them).
+template <int NIT>
+struct ConvIn {
+    float x[NIT];
+    float4 w[NIT], r[NIT];
+    int gch[NIT];
+
+    // gch_of(c) maps the workgroup's channel c < nch to a global channel.
+    // The loads are branch-free (out-of-range slots load channel 0 and are
+    // marked gch = -1), so the compiler's wait counts stay exact.
+    template <typename F>
+    __device__ __forceinline__ void load(F gch_of, int nch, int tid, int tpb, const float *qkv, const float *conv_w,
+                                         const float *ring, int conv_dim, int seq) {
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int c = tid + it * tpb;
+            const int g = gch_of(c < nch ? c : 0);
+            gch[it] = c < nch ? g : -1;
+            x[it] = qkv[g];
+            w[it] = *reinterpret_cast<const float4 *>(conv_w + (size_t)g * kConvRing);
+            r[it] = *reinterpret_cast<const float4 *>(ring + ring_at(seq, g, conv_dim));
+        }
+    }
+    // conv1d + SiLU (op order as engines/qwen.c:311-319) of the it-th channel.
+    __device__ __forceinline__ float conv(int it, int K, int ph) const {
+        float acc = 0.f;
+        for (int j = 0; j < K - 1; j++) acc += f4_get(w[it], j) * f4_get(r[it], ring_slot(ph, K, j));
+        acc += f4_get(w[it], K - 1) * x[it];
+        return omh_silu(acc);
+    }
+    // Ring entry with the new input in the free slot of phase ph.
+    __device__ __forceinline__ float4 appended(int it, int ph) const {
+        float4 e = r[it];
+        f4_set(e, ph & (kConvRing - 1), x[it]);
+        return e;
+    }
+};
+
+// L2-norm factors of the raw conv outputs q~, k~ of a key head, computed by
+// every wave from LDS: rq = (|q~|^2 + 1e-6)^-1/2 kd^-1/2 (the q scale),
+// rk = (|k~|^2 + 1e-6)^-1/2, and kq = q^.k^ (qwen.c:153-157, 326-329).
+template <int KD>
+__device__ __forceinline__ void qk_factors(const float *s_q, const float *s_k, int lane, float &rq, float &rk,
+                                           float &kq) {
+    float sq = 0.f, sk = 0.f, sqk = 0.f;
+    for (int i = lane; i < KD; i += OMH_WAVE) {
+        const float q = s_q[i], k = s_k[i];
+        sq += q * q;
+        sk += k * k;
+        sqk += q * k;
+    }
+    sq = omh_xor_sum_below<OMH_WAVE>(sq);
+    sk = omh_xor_sum_below<OMH_WAVE>(sk);
+    sqk = omh_xor_sum_below<OMH_WAVE>(sqk);
+    rq = (1.f / sqrtf(sq + 1e-6f)) * (1.f / sqrtf((float)KD));
+    rk = 1.f / sqrtf(sk + 1e-6f);
+    kq = sqk * rq * rk;
+}
+
+// Phase bookkeeping of the ring, per sequence: launch reads phase[epoch],
+// writes phase[1 - epoch]; sequences outside the launch carry theirs over.
+__device__ __forceinline__ void advance_phase(const LayerPtrs &L, int B, int b, bool writer, bool copier,
+                                              int ph, int tid, int tpb) {
+    if (writer && tid == 0) L.phase[(1 - L.epoch) * L.max_seqs + b] = (ph + 1) & (kConvRing - 1);
+    if (copier)
+        for (int bb = B + tid; bb < L.max_seqs; bb += tpb)
+            L.phase[(1 - L.epoch) * L.max_seqs + bb] = L.phase[L.epoch * L.max_seqs + bb];
+}
+
+// Per-head scalars of the delta rule.
+struct HeadCoef {
+    float gam, beta;      // decay gamma = e^g and beta
+    float rk, rq, kq;     // key head's norm factors (qk_factors)
+};
+
+// Pass 1: column sums of S k~ and S q~ over this thread's rows, reduced over
+// the workgroup, give kv, delta and o.  Pass 2: S <- gamma S + k~ (rk delta)^T,
+// streamed back.  Returns o (before the gated norm).
+template <int KD, int VD, int RG, int RPT, int C4, int NW>
+__device__ __forceinline__ float4 delta_rule(float4 (&s)[RPT], float *Sp, const float *s_q, const float *s_k,
+                                             float4 vv, const HeadCoef &hc, float4 (*red)[2][C4], int wave,
+                                             int lane, int c4, int rg) {
+    float4 ak = f4_zero(), aq = f4_zero();
+#pragma unroll
+    for (int m = 0; m < RPT; m++) {
+        const int i = rg + RG * m;
+        ak = f4_fma(s[m], s_k[i], ak);
+        aq = f4_fma(s[m], s_q[i], aq);
+    }
+    colsum2<C4, NW>(ak, aq, red, wave, lane, c4);
+    const float4 kv = f4_scale(ak, hc.gam * hc.rk);
+    const float4 delta = f4_scale(f4_sub(vv, kv), hc.beta);
+    const float4 o = f4_fma(delta, hc.kq, f4_scale(aq, hc.gam * hc.rq));
+    const float4 d2 = f4_scale(delta, hc.rk);
+#pragma unroll
+    for (int m = 0; m < RPT; m++) {
+        const int i = rg + RG * m;
+        s[m] = f4_fma(d2, s_k[i], f4_scale(s[m], hc.gam));
+        omh_st_stream(Sp + (size_t)i * VD + c4 * 4, s[m]);
+    }
+    return o;
+}
+
+// ------------------------------------------------------------- paired kernel
+template <int KD, int VD>
+struct PairShape : TileShape<KD, VD> {};
+
+template <int KD, int VD, int RPT>
+__device__ __forceinline__ void load_head(float4 (&s)[RPT], const float *Sp, int rg, int c4) {
+    using Sh = PairShape<KD, VD>;
+    static_assert(RPT == Sh::RPT, "tile rows");
+#pragma unroll
+    for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream(Sp + (size_t)(rg + Sh::RG * m) * VD + c4 * 4);
+}
+
+// Delta rule + gated norm of one value head of the workgroup.
+template <int KD, int VD, int RPT, int C4>
+__device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *core, const float *s_q,
+                                            const float *s_k, const float *s_v, const float *s_z,
+                                            const HeadCoef &hc, float4 gn, float eps, float4 (*red)[2][C4],
+                                            int wave, int lane, int c4, int rg) {
+    using Sh = PairShape<KD, VD>;
+    static_assert(RPT == Sh::RPT && C4 == Sh::C4, "tile shape");
+    const float4 vv = *reinterpret_cast<const float4 *>(&s_v[c4 * 4]);
+    const float4 o = delta_rule<KD, VD, Sh::RG, RPT, C4, Sh::NW>(s, Sp, s_q, s_k, vv, hc, red, wave, lane, c4, rg);
+    float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+    ss = omh_xor_sum_below<C4>(ss);
+    if (rg == 0) {
+        const float rn = 1.f / sqrtf(ss / (float)VD + eps);     // qwen.c:353-357
+        const float4 zz = *reinterpret_cast<const float4 *>(&s_z[c4 * 4]);
+        *reinterpret_cast<float4 *>(core + c4 * 4) = gated(o, rn, gn, zz);
+    }
+}
+
+template <int KD, int VD, int REPMAX>
+__global__ __launch_bounds__((PairShape<KD, VD>::TPB))
+void gdn_decode_paired_kernel(const DecodeArgs args) {
+    using Sh = PairShape<KD, VD>;
+    constexpr int TPB = Sh::TPB, C4 = Sh::C4, NW = Sh::NW;
+    constexpr int NIT = (2 * KD + REPMAX * VD + TPB - 1) / TPB;   // conv channels per thread
+    constexpr int NZ = (REPMAX * VD + TPB - 1) / TPB;             // z values per thread
+
+    const int hk = blockIdx.x;                   // key head
+    const int b = blockIdx.y;                    // sequence
+    const int l = blockIdx.z;                    // layer slot
+    const LayerPtrs &L = args.L[l];
+    const int kh = args.kh, vh = args.vh, K = args.K;
+    const int rep = vh / kh, h0 = hk * rep;      // value heads h0 .. h0+rep-1 (qwen.c:331, 335)
+    const int key_dim = kh * KD, vdim = vh * VD, conv_dim = 2 * key_dim + vdim;
+    const size_t tok = (size_t)l * args.B + b;
+
+    const int tid = threadIdx.x;
+    const int c4 = tid % C4, rg = tid / C4;
+    const int lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
+    float *S0 = L.S + ((size_t)b * vh + h0) * (KD * VD);
+
+    __shared__ __align__(16) float s_q[KD], s_k[KD], s_v[REPMAX * VD], s_z[REPMAX * VD];
+    __shared__ float s_gam[REPMAX], s_beta[REPMAX];
+    __shared__ float4 s_red[2][NW][2][C4];
+
+    // The first two value heads' state tiles (REPMAX >= 2 means rep >= 2)
+    // are requested before anything else: starting every workgroup's HBM
+    // stream at once beats having the prologue's small scattered reads
+    // (which then wait behind the tiles) ready early.
+    float4 sa[Sh::RPT], sb[Sh::RPT];
+    load_head<KD, VD>(sa, S0, rg, c4);
+    if constexpr (REPMAX > 1) load_head<KD, VD>(sb, S0 + KD * VD, rg, c4);
+
+    // (1) Prologue: the conv channels of key head hk (q, k) and of its
+    // value heads (v), z of the value heads, the gate inputs.  This
+    // workgroup owns all of these channels and appends them to the ring.
+    const int ph = L.phase[L.epoch * L.max_seqs + b];
+    const float *qkv = args.qkv + tok * args.ld_qkv;
+    const int nch = 2 * KD + rep * VD;
+    ConvIn<NIT> cin;
+    cin.load([&](int c) {
+                 return c < KD ? hk * KD + c
+                               : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h0 * VD + (c - 2 * KD));
+             },
+             nch, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b);
+    const float *zrow = args.z + tok * args.ld_z + (size_t)h0 * VD;
+    float zin[NZ];
+#pragma unroll
+    for (int it = 0; it < NZ; it++) {
+        const int c = tid + it * TPB;
+        zin[it] = zrow[c < rep * VD ? c : 0];
+    }
+    const int gh = h0 + (tid < rep ? tid : rep - 1);
+    const float ga = args.a[tok * args.ld_ab + gh], gb = args.b[tok * args.ld_ab + gh];
+    const float galog = L.A_log[gh], gdt = L.dt_bias[gh];
+    const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + c4 * 4);
+
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        if (cin.gch[it] < 0) continue;
+        const int c = tid + it * TPB;
+        const float y = cin.conv(it, K, ph);
+        if (c < KD) s_q[c] = y;
+        else if (c < 2 * KD) s_k[c - KD] = y;
+        else s_v[c - 2 * KD] = y;
+        *reinterpret_cast<float4 *>(L.conv_st + ring_at(b, cin.gch[it], conv_dim)) = cin.appended(it, ph);
+    }
+#pragma unroll
+    for (int it = 0; it < NZ; it++) {
+        const int c = tid + it * TPB;
+        if (c < rep * VD) s_z[c] = zin[it];
+    }
+    if (tid < rep) {
+        // gates (qwen.c:337-338)
+        const float g = -expf(galog) * omh_softplus(ga + gdt);
+        s_gam[tid] = expf(g);
+        s_beta[tid] = omh_sigmoid(gb);
+    }
+    omh_lds_barrier();
+    HeadCoef hc;
+    qk_factors<KD>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
+
+    // (3)+(4) value heads in order; the next head's state is in flight while
+    // the current one is reduced and written back.  Heads alternate between
+    // the two reduction buffers, so a wave that runs ahead into the next
+    // head never overwrites sums another wave is still reading.
+    float *core = args.core + tok * vdim + (size_t)h0 * VD;
+    for (int j = 0; j < rep; j += 2) {
+        hc.gam = s_gam[j];
+        hc.beta = s_beta[j];
+        paired_head<KD, VD>(sa, S0 + (size_t)j * KD * VD, core + j * VD, s_q, s_k, s_v + j * VD, s_z + j * VD, hc,
+                            gn, args.eps, s_red[0], wave, lane, c4, rg);
+        if (j + 2 < rep) load_head<KD, VD>(sa, S0 + (size_t)(j + 2) * KD * VD, rg, c4);
+        if (REPMAX > 1 && j + 1 < rep) {
+            hc.gam = s_gam[j + 1];
+            hc.beta = s_beta[j + 1];
+            paired_head<KD, VD>(sb, S0 + (size_t)(j + 1) * KD * VD, core + (j + 1) * VD, s_q, s_k,
+                                s_v + (j + 1) * VD, s_z + (j + 1) * VD, hc, gn, args.eps, s_red[1], wave, lane,
+                                c4, rg);
+            if (j + 3 < rep) load_head<KD, VD>(sb, S0 + (size_t)(j + 3) * KD * VD, rg, c4);
+        }
+    }
+    advance_phase(L, args.B, b, hk == 0, hk == 0 && b == 0, ph, tid, TPB);
+}
+
+// ------------------------------------------------------------- sliced kernel
 template <int KD, int VD, int NCS>
-__global__ __launch_bounds__((DecShape<KD, VD, NCS>::TPB))
+__global__ __launch_bounds__((TileShape<KD, VD / NCS>::TPB))
 void gdn_decode_core_kernel(const DecodeArgs args) {
-    using Sh = DecShape<KD, VD, NCS>;
-    constexpr int TPB = Sh::TPB, CW = Sh::CW, C4 = Sh::C4, RG = Sh::RG, RPT = Sh::RPT, NW = Sh::NW;
+    using Sh = TileShape<KD, VD / NCS>;
+    constexpr int TPB = Sh::TPB, CW = VD / NCS, C4 = Sh::C4, RG = Sh::RG, RPT = Sh::RPT, NW = Sh::NW;
+    static_assert(NCS <= kMaxSlices && VD / 4 <= TPB, "norm epilogue layout");
 
     const int cs = blockIdx.x % NCS;             // column slice
     const int h = blockIdx.x / NCS;              // value head
@@ -116,90 +378,62 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     const int lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
     float *Sp = L.S + ((size_t)b * vh + h) * (KD * VD) + col0;
 
-    __shared__ float s_q[KD], s_k[KD], s_v[CW];
+    __shared__ __align__(16) float s_q[KD], s_k[KD], s_v[CW];
     __shared__ float s_gam, s_beta;
-    __shared__ float4 s_red1[NW][C4], s_red2[NW][C4];
+    __shared__ float4 s_red[NW][2][C4];
     __shared__ int s_last;
 
-    // State loads first: nothing before the delta rule depends on them, so
-    // their latency overlaps the prologue (whose barriers order LDS only).
+    // (1) Prologue inputs first (see ConvIn): the q/k channels of key head
+    // hk (recomputed by every workgroup of the key head, appended by its
+    // first one) and this slice's value channels.
+    constexpr int NIT = (2 * KD + CW + TPB - 1) / TPB;
+    const int ph = L.phase[L.epoch * L.max_seqs + b];
+    const float *qkv = args.qkv + tok * args.ld_qkv;
+    ConvIn<NIT> cin;
+    cin.load([&](int c) {
+                 return c < KD ? hk * KD + c
+                               : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h * VD + col0 + (c - 2 * KD));
+             },
+             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b);
+    const int t4 = tid < VD / 4 ? tid : 0;
+    const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + t4 * 4);
+    const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + t4 * 4);
+    const float ga = args.a[tok * args.ld_ab + h], gb = args.b[tok * args.ld_ab + h];
+    const float galog = L.A_log[h], gdt = L.dt_bias[h];
+
     float4 s[RPT];
 #pragma unroll
     for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream(Sp + (size_t)(rg + RG * m) * VD + c4 * 4);
-    float4 zz = f4_zero(), gn = f4_zero();
-    if (tid < VD / 4) {
-        zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + tid * 4);
-        gn = *reinterpret_cast<const float4 *>(L.gnorm + tid * 4);
-    }
+    __builtin_amdgcn_sched_barrier(0);           // keep prologue arithmetic after the state requests
 
-    // (1) conv + SiLU (op order as qwen.c:311-319) for the q/k channels of
-    // key head hk and this slice's value channels.
-    const int ph = L.phase[L.epoch * L.max_seqs + b];
-    const float *qkv = args.qkv + tok * args.ld_qkv;
-    float *ring = L.conv_st + (size_t)b * conv_dim * kConvRing;
     const bool own_qk = (h % rep == 0) && cs == 0;
-    for (int c = tid; c < 2 * KD + CW; c += TPB) {
-        int gch;
-        float *dst;
-        bool own;
-        if (c < KD) { gch = hk * KD + c; dst = &s_q[c]; own = own_qk; }
-        else if (c < 2 * KD) { gch = key_dim + hk * KD + (c - KD); dst = &s_k[c - KD]; own = own_qk; }
-        else { gch = 2 * key_dim + h * VD + col0 + (c - 2 * KD); dst = &s_v[c - 2 * KD]; own = true; }
-        const float x = qkv[gch];
-        const float4 rv = *reinterpret_cast<const float4 *>(ring + (size_t)gch * kConvRing);
-        const float rr[kConvRing] = {rv.x, rv.y, rv.z, rv.w};
-        const float *w = L.conv_w + (size_t)gch * K;
-        float acc = 0.f;
-        for (int j = 0; j < K - 1; j++) acc += w[j] * rr[ring_slot(ph, K, j)];
-        acc += w[K - 1] * x;
-        if (own) ring[(size_t)gch * kConvRing + (ph & (kConvRing - 1))] = x;
-        *dst = omh_silu(acc);
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        if (cin.gch[it] < 0) continue;
+        const int c = tid + it * TPB;
+        const float y = cin.conv(it, K, ph);
+        bool own = true;
+        if (c < KD) { s_q[c] = y; own = own_qk; }
+        else if (c < 2 * KD) { s_k[c - KD] = y; own = own_qk; }
+        else s_v[c - 2 * KD] = y;
+        if (own) *reinterpret_cast<float4 *>(L.conv_st + ring_at(b, cin.gch[it], conv_dim)) = cin.appended(it, ph);
     }
     if (tid == 0) {
         // gates (qwen.c:337-338)
-        const float g = -expf(L.A_log[h]) * omh_softplus(args.a[tok * args.ld_ab + h] + L.dt_bias[h]);
+        const float g = -expf(galog) * omh_softplus(ga + gdt);
         s_gam = expf(g);
-        s_beta = omh_sigmoid(args.b[tok * args.ld_ab + h]);
-        if (h == 0 && cs == 0) L.phase[(1 - L.epoch) * L.max_seqs + b] = (ph + 1) & (kConvRing - 1);
-    }
-    if (h == 0 && cs == 0 && b == 0) {
-        // sequences outside this launch keep their phase in the other buffer
-        for (int bb = args.B + tid; bb < L.max_seqs; bb += TPB)
-            L.phase[(1 - L.epoch) * L.max_seqs + bb] = L.phase[L.epoch * L.max_seqs + bb];
+        s_beta = omh_sigmoid(gb);
     }
     omh_lds_barrier();
-    // L2 norm of q and k (eps 1e-6), then q *= kd^-1/2 (qwen.c:153-157, 326-329)
-    if (wave == 0) {
-        float sq = 0.f, sk = 0.f;
-        for (int i = lane; i < KD; i += OMH_WAVE) { sq += s_q[i] * s_q[i]; sk += s_k[i] * s_k[i]; }
-        sq = omh_xor_sum_below<OMH_WAVE>(sq);
-        sk = omh_xor_sum_below<OMH_WAVE>(sk);
-        const float rq = 1.f / sqrtf(sq + 1e-6f), rk = 1.f / sqrtf(sk + 1e-6f);
-        const float scale = 1.f / sqrtf((float)KD);
-        for (int i = lane; i < KD; i += OMH_WAVE) { s_q[i] = (s_q[i] * rq) * scale; s_k[i] *= rk; }
-    }
-    omh_lds_barrier();
+    HeadCoef hc;
+    qk_factors<KD>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
+    hc.gam = s_gam;
+    hc.beta = s_beta;
 
     // (3) delta rule on this slice of value head h (qwen.c:339-352)
-    const float gam = s_gam, beta = s_beta;
-    float4 kv = f4_zero();
-#pragma unroll
-    for (int m = 0; m < RPT; m++) {
-        s[m] = f4_scale(s[m], gam);
-        kv = f4_fma(s[m], s_k[rg + RG * m], kv);
-    }
-    kv = colsum<C4, NW>(kv, s_red1, wave, lane, c4);
     const float4 vv = *reinterpret_cast<const float4 *>(&s_v[c4 * 4]);
-    const float4 delta = f4_scale(f4_sub(vv, kv), beta);
-    float4 o = f4_zero();
-#pragma unroll
-    for (int m = 0; m < RPT; m++) {
-        const int i = rg + RG * m;
-        s[m] = f4_fma(delta, s_k[i], s[m]);
-        o = f4_fma(s[m], s_q[i], o);
-        omh_st_stream(Sp + (size_t)i * VD + c4 * 4, s[m]);
-    }
-    o = colsum<C4, NW>(o, s_red2, wave, lane, c4);
+    const float4 o = delta_rule<KD, VD, RG, RPT, C4, NW>(s, Sp, s_q, s_k, vv, hc, s_red, wave, lane, c4, rg);
+    advance_phase(L, args.B, b, h == 0 && cs == 0, h == 0 && cs == 0 && b == 0, ph, tid, TPB);
 
     // (4) gated RMSNorm over the head's vd columns (qwen.c:353-357)
     float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
@@ -252,30 +486,45 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
 }
 
 template <int KD, int VD, int NCS>
-hipError_t launch_one(const DecodeArgs &a, hipStream_t st) {
+hipError_t launch_sliced(const DecodeArgs &a, hipStream_t st) {
     dim3 grid(a.vh * NCS, a.B, a.nl);
-    hipLaunchKernelGGL((gdn_decode_core_kernel<KD, VD, NCS>), grid, dim3(DecShape<KD, VD, NCS>::TPB), 0, st, a);
+    hipLaunchKernelGGL((gdn_decode_core_kernel<KD, VD, NCS>), grid, dim3(TileShape<KD, VD / NCS>::TPB), 0, st, a);
     return hipGetLastError();
 }
 
 template <int KD, int VD>
-hipError_t launch_ncs(const DecodeArgs &a, int ncs, hipStream_t st) {
-    switch (ncs) {
-        case 1: if constexpr (dec_valid<KD, VD, 1>()) return launch_one<KD, VD, 1>(a, st); break;
-        case 2: if constexpr (dec_valid<KD, VD, 2>()) return launch_one<KD, VD, 2>(a, st); break;
-        case 4: if constexpr (dec_valid<KD, VD, 4>()) return launch_one<KD, VD, 4>(a, st); break;
-        case 8: if constexpr (dec_valid<KD, VD, 8>()) return launch_one<KD, VD, 8>(a, st); break;
+hipError_t launch_kd_vd(const DecodeArgs &a, int variant, hipStream_t st) {
+    switch (variant) {
+        case kDecodePaired: {
+            const int rep = a.vh / a.kh;
+            const dim3 grid(a.kh, a.B, a.nl), block(PairShape<KD, VD>::TPB);
+            if (rep == 1) hipLaunchKernelGGL((gdn_decode_paired_kernel<KD, VD, 1>), grid, block, 0, st, a);
+            else if (rep == 2) hipLaunchKernelGGL((gdn_decode_paired_kernel<KD, VD, 2>), grid, block, 0, st, a);
+            else if (rep <= 4) hipLaunchKernelGGL((gdn_decode_paired_kernel<KD, VD, 4>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((gdn_decode_paired_kernel<KD, VD, kMaxRep>), grid, block, 0, st, a);
+            return hipGetLastError();
+        }
+        case 1: if constexpr (slice_valid(KD, VD, 1)) return launch_sliced<KD, VD, 1>(a, st); break;
+        case 2: if constexpr (slice_valid(KD, VD, 2)) return launch_sliced<KD, VD, 2>(a, st); break;
+        case 4: if constexpr (slice_valid(KD, VD, 4)) return launch_sliced<KD, VD, 4>(a, st); break;
+        case 8: if constexpr (slice_valid(KD, VD, 8)) return launch_sliced<KD, VD, 8>(a, st); break;
         default: break;
     }
     return hipErrorInvalidValue;
 }
 
-// One workgroup per value head is fastest on MI355X at every measured size:
-// splitting columns multiplies the per-workgroup prologue and adds the
-// exchange round trips, which cost more than the extra memory parallelism
-// gains (30-layer B=1 step: 25.3 us at NCS=1 vs 36.1 us at NCS=4).
-int default_ncs(int kd, int vd) {
+// Launch-size rule: the paired kernel once the launch has enough key-head
+// workgroups to cover the chip (30 layers x 1 sequence: 24.8 us paired vs
+// 28.4 us one workgroup per head on MI355X); below that one workgroup per
+// value head.  Column slices do not pay on MI355X even for one layer at
+// B = 1 (7.4 us at NCS = 1, 8.1 / 8.2 / 9.0 us at NCS = 2 / 4 / 8): the
+// step is latency-bound there and the cross-slice exchange adds a round
+// trip.  They stay available through the variant argument.
+int choose_variant(const DecodeArgs &a, int kd, int vd) {
     (void)kd; (void)vd;
+    const long pair_wgs = (long)a.nl * a.B * a.kh;
+    const int rep = a.vh / a.kh;
+    if (pair_wgs >= 256 && rep <= kMaxRep) return kDecodePaired;
     return 1;
 }
 
@@ -286,14 +535,15 @@ bool decode_core_supported(int kd, int vd, int rep, int K) {
     return (kd == vd && (kd == 16 || kd == 32 || kd == 64 || kd == 128)) || (kd == 32 && vd == 16);
 }
 
-hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int ncs, hipStream_t st) {
+hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, hipStream_t st) {
     if (!decode_core_supported(kd, vd, a.vh / a.kh, a.K)) return hipErrorInvalidValue;
-    if (ncs <= 0) ncs = default_ncs(kd, vd);
-    if (kd == 16 && vd == 16) return launch_ncs<16, 16>(a, ncs, st);
-    if (kd == 32 && vd == 32) return launch_ncs<32, 32>(a, ncs, st);
-    if (kd == 64 && vd == 64) return launch_ncs<64, 64>(a, ncs, st);
-    if (kd == 128 && vd == 128) return launch_ncs<128, 128>(a, ncs, st);
-    if (kd == 32 && vd == 16) return launch_ncs<32, 16>(a, ncs, st);
+    if (variant == 0) variant = choose_variant(a, kd, vd);
+    if (variant == kDecodePaired && a.vh / a.kh > kMaxRep) return hipErrorInvalidValue;
+    if (kd == 16 && vd == 16) return launch_kd_vd<16, 16>(a, variant, st);
+    if (kd == 32 && vd == 32) return launch_kd_vd<32, 32>(a, variant, st);
+    if (kd == 64 && vd == 64) return launch_kd_vd<64, 64>(a, variant, st);
+    if (kd == 128 && vd == 128) return launch_kd_vd<128, 128>(a, variant, st);
+    if (kd == 32 && vd == 16) return launch_kd_vd<32, 16>(a, variant, st);
     return hipErrorInvalidValue;
 }
 

@@ -75,13 +75,12 @@ void prefill_prep_kernel(const PrefillArgs a) {
     if (tid < D) {
         const int gch = gch0 + tid;
         float w[kConvRing], h[kConvRing - 1];
-        for (int j = 0; j < K; j++) w[j] = a.L.conv_w[(size_t)gch * K + j];
+        const float4 wv = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)gch * kConvRing);
+        for (int j = 0; j < K; j++) w[j] = f4_get(wv, j);
         if (t0 == 0) {
             const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
-            const float4 rv = *reinterpret_cast<const float4 *>(
-                a.L.conv_st + ((size_t)a.seq * conv_dim + gch) * kConvRing);
-            const float rr[kConvRing] = {rv.x, rv.y, rv.z, rv.w};
-            for (int j = 0; j < K - 1; j++) h[j] = rr[ring_slot(ph, K, j)];
+            const float4 rv = *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, gch, conv_dim));
+            for (int j = 0; j < K - 1; j++) h[j] = f4_get(rv, ring_slot(ph, K, j));
         } else {
             for (int j = 0; j < K - 1; j++) h[j] = a.qkv[(size_t)(t0 - (K - 1) + j) * a.ld_qkv + gch];
         }
@@ -133,7 +132,10 @@ void prefill_prep_kernel(const PrefillArgs a) {
 
 // ---------------------------------------------------------------- P5 commit
 // New conv history = last K-1 entries of [old history, x_0 .. x_{T-1}],
-// written in ring order for phase (p + T) mod ring size.
+// written in ring order for phase (p + T) mod ring size.  Every block reads
+// the phase from phase[epoch]; the new one goes to phase[1 - epoch] (block 0
+// also carries the other sequences' phases over) and the host flips the
+// layer's epoch after the launch, as for decode launches.
 __global__ __launch_bounds__(256)
 void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
     const int c = blockIdx.x * 256 + threadIdx.x;
@@ -141,17 +143,22 @@ void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
     const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
     const int nph = (ph + T) & (kConvRing - 1);
     if (c < conv_dim) {
-        float *ring = a.L.conv_st + ((size_t)a.seq * conv_dim + c) * kConvRing;
-        const float4 rv = *reinterpret_cast<const float4 *>(ring);
-        const float rr[kConvRing] = {rv.x, rv.y, rv.z, rv.w};
-        float nh[kConvRing - 1];
+        float4 *ring = reinterpret_cast<float4 *>(a.L.conv_st + ring_at(a.seq, c, conv_dim));
+        const float4 old = *ring;
+        float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int j = 0; j < K - 1; j++) {
             const int idx = T + j;               // index into [old history (K-1), x_0 ..]
-            nh[j] = idx < K - 1 ? rr[ring_slot(ph, K, idx)] : a.qkv[(size_t)(idx - (K - 1)) * a.ld_qkv + c];
+            const float v = idx < K - 1 ? f4_get(old, ring_slot(ph, K, idx))
+                                        : a.qkv[(size_t)(idx - (K - 1)) * a.ld_qkv + c];
+            f4_set(e, ring_slot(nph, K, j), v);
         }
-        for (int j = 0; j < K - 1; j++) ring[ring_slot(nph, K, j)] = nh[j];
+        *ring = e;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.L.phase[a.L.epoch * a.L.max_seqs + a.seq] = nph;
+    if (blockIdx.x == 0) {
+        int *nxt = a.L.phase + (1 - a.L.epoch) * a.L.max_seqs;
+        const int *cur = a.L.phase + a.L.epoch * a.L.max_seqs;
+        for (int s = threadIdx.x; s < a.L.max_seqs; s += 256) nxt[s] = s == a.seq ? nph : cur[s];
+    }
 }
 
 // ---------------------------------------------------------------- P4 norm

@@ -116,12 +116,17 @@ LayerPtrs ptrs(const DevLayer &L) {
     return p;
 }
 
-// Column slices per value head for decode: OMH_DECODE_NCS (1, 2, 4 or 8)
-// overrides the kernel's default; read per call so it can be changed at run
-// time for tuning and tests.
-int decode_ncs() {
-    const char *e = getenv("OMH_DECODE_NCS");
-    return e ? atoi(e) : 0;
+// Decode kernel override for tuning and tests, read per call:
+// OMH_DECODE_KERNEL=paired, or =sliced with OMH_DECODE_NCS (1, 2, 4 or 8)
+// column slices per value head.  Unset: chosen by launch size.
+int decode_variant() {
+    const char *k = getenv("OMH_DECODE_KERNEL");
+    if (k && strcmp(k, "paired") == 0) return kDecodePaired;
+    if (k && strcmp(k, "sliced") == 0) {
+        const char *e = getenv("OMH_DECODE_NCS");
+        return e ? atoi(e) : 1;
+    }
+    return 0;
 }
 
 // Core decode on device pointers for layers lis[0..nl), B sequences each.
@@ -164,7 +169,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
         A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
         A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
         for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
-        HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_ncs(), st));
+        HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_variant(), st));
         for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
     }
     return OMH_OK;
@@ -217,6 +222,7 @@ int prefill_core(int li, int seq, int T, const float *qkv, int64_t ld_qkv, const
     if (int rc = ensure(g_pre, prefill_scratch_bytes(D, d.kh, d.vh, T))) return rc;
     prefill_bind_scratch(A, D, g_pre.p);
     HIP_OK(launch_prefill_core(A, D, st));
+    L.epoch ^= 1;                      // the conv commit wrote the other phase buffer
     return OMH_OK;
 }
 
@@ -293,7 +299,13 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
     const int K = d->conv_k, D = d->hidden, vh = d->vh;
     int rc = OMH_OK;
 #define UP(dst, n, src) do { if ((rc = upload(&(dst), (size_t)(n), (src))) != OMH_OK) { free_layer(L); return rc; } } while (0)
-    UP(L.conv_w, (size_t)L.conv_dim * K, w->conv_w);
+    {
+        // device layout [conv_dim][kConvRing]: taps 0..K-1, zero padded
+        std::vector<float> cw((size_t)L.conv_dim * kConvRing, 0.f);
+        for (int c = 0; c < L.conv_dim; c++)
+            for (int j = 0; j < K; j++) cw[(size_t)c * kConvRing + j] = w->conv_w[(size_t)c * K + j];
+        UP(L.conv_w, cw.size(), cw.data());
+    }
     UP(L.A_log, vh, w->A_log);
     UP(L.dt_bias, vh, w->dt_bias);
     UP(L.gnorm, d->vd, w->gnorm);
@@ -396,7 +408,7 @@ int omh_gdn_state_get(int li, int seq, float *conv, float *S) {
         HIP_OK(hipMemcpy(&ph, L.phase + (size_t)L.epoch * L.max_seqs + seq, sizeof(int), hipMemcpyDeviceToHost));
         for (int c = 0; c < L.conv_dim; c++)
             for (int j = 0; j < K - 1; j++)
-                conv[(size_t)c * (K - 1) + j] = ring[(size_t)c * kConvRing + ring_slot(ph, K, j)];
+                conv[(size_t)c * (K - 1) + j] = ring[ring_at(0, c, L.conv_dim) + ring_slot(ph, K, j)];
     }
     if (S) HIP_OK(hipMemcpy(S, L.S + seq * sn, sn * sizeof(float), hipMemcpyDeviceToHost));
     return OMH_OK;
@@ -414,7 +426,7 @@ int omh_gdn_state_set(int li, int seq, const float *conv, const float *S) {
         std::vector<float> ring(cn, 0.f);       // written at phase 0
         for (int c = 0; c < L.conv_dim; c++)
             for (int j = 0; j < K - 1; j++)
-                ring[(size_t)c * kConvRing + ring_slot(0, K, j)] = conv[(size_t)c * (K - 1) + j];
+                ring[ring_at(0, c, L.conv_dim) + ring_slot(0, K, j)] = conv[(size_t)c * (K - 1) + j];
         const int zero = 0;
         HIP_OK(hipMemcpy(L.conv_st + seq * cn, ring.data(), cn * sizeof(float), hipMemcpyHostToDevice));
         HIP_OK(hipMemcpy(L.phase + (size_t)L.epoch * L.max_seqs + seq, &zero, sizeof(int), hipMemcpyHostToDevice));

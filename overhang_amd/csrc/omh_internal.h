@@ -9,12 +9,25 @@ namespace omh {
 // Conv history ring: every channel keeps kConvRing slots; at phase p the
 // K-1 history values, oldest first, sit in slots (p + kConvRing+1 - K + j)
 // mod kConvRing and slot p mod kConvRing is free.  Consuming a token writes
-// it into the free slot and advances p.  Readers never touch the free slot,
-// so any number of workgroups may read a channel while its owner appends.
+// it into the free slot and advances p.  A channel's slots are one 16-byte
+// entry ([seq][conv_dim][kConvRing]); its owner rewrites the whole entry
+// with only the free slot changed, so a concurrent reader of the entry sees
+// the history slots it uses unchanged, and every write covers whole lines.
 constexpr int kConvRing = 4;          // supports conv kernels K = 2..4
 
 __host__ __device__ inline int ring_slot(int p, int K, int j) {
     return (p + kConvRing + 1 - K + j) & (kConvRing - 1);
+}
+// Offset of channel ch's ring entry for sequence seq.
+__host__ __device__ inline size_t ring_at(int seq, int ch, int conv_dim) {
+    return ((size_t)seq * conv_dim + ch) * kConvRing;
+}
+// Element j (0..3) of a float4.
+__host__ __device__ inline float f4_get(const float4 &v, int j) {
+    return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
+}
+__host__ __device__ inline void f4_set(float4 &v, int j, float x) {
+    if (j == 0) v.x = x; else if (j == 1) v.y = x; else if (j == 2) v.z = x; else v.w = x;
 }
 
 // Device pointers of one layer's core weights and state.  The per-sequence
@@ -22,7 +35,7 @@ __host__ __device__ inline int ring_slot(int p, int K, int j) {
 // reads phase[epoch][b] and writes phase[1-epoch][b], and the host flips
 // the layer's epoch after enqueueing it.
 struct LayerPtrs {
-    const float *conv_w;   // [conv_dim][K]
+    const float *conv_w;   // [conv_dim][kConvRing], taps 0..K-1 then zeros
     const float *A_log;    // [vh]
     const float *dt_bias;  // [vh]
     const float *gnorm;    // [vd]
@@ -91,8 +104,11 @@ bool prefill_supported(int kd, int vd, int rep, int K);
 hipError_t launch_prefill_core(const PrefillArgs &a, int D, hipStream_t st);
 
 // Returns hipSuccess, or hipErrorInvalidValue for an unsupported shape.
-// ncs = column slices per value head (0: the kernel's default for kd, vd).
-hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int ncs, hipStream_t st);
+// variant: 0 = chosen by launch size; kDecodePaired = one workgroup per key
+// head streaming its value heads; 1, 2, 4, 8 = one workgroup per column
+// slice of a value head, with that many slices.
+constexpr int kDecodePaired = -1;
+hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int variant, hipStream_t st);
 bool decode_core_supported(int kd, int vd, int rep, int K);
 
 }  // namespace omh

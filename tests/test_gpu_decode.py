@@ -22,8 +22,22 @@ def new_li():
     return _next_li[0]
 
 
+# every decode kernel: chosen by launch size, paired heads, one slice per head
+VARIANTS = [{}, {"OMH_DECODE_KERNEL": "paired"}, {"OMH_DECODE_KERNEL": "sliced", "OMH_DECODE_NCS": "1"}]
+VARIANT_IDS = ["auto", "paired", "sliced1"]
+
+
+@pytest.fixture(params=VARIANTS, ids=VARIANT_IDS)
+def variant(request, monkeypatch):
+    for k in ("OMH_DECODE_KERNEL", "OMH_DECODE_NCS"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in request.param.items():
+        monkeypatch.setenv(k, v)
+    return request.param
+
+
 @pytest.mark.parametrize("name", fixtures.CORE_FIXTURES)
-def test_decode_core_matches_reference_golden(name):
+def test_decode_core_matches_reference_golden(name, variant):
     d, w, inp, (conv, S), exp = fixtures.load(name)
     L = gdn.GdnLayer(new_li(), d, w)
     L.set_state(0, conv, S)
@@ -38,7 +52,7 @@ def test_decode_core_matches_reference_golden(name):
 
 
 @pytest.mark.parametrize("name", fixtures.LAYER_FIXTURES)
-def test_decode_layer_matches_reference_golden(name):
+def test_decode_layer_matches_reference_golden(name, variant):
     d, w, inp, (conv, S), exp = fixtures.load(name)
     L = gdn.GdnLayer(new_li(), d, w, int8=exp["int8"])
     L.set_state(0, conv, S)
@@ -51,7 +65,7 @@ def test_decode_layer_matches_reference_golden(name):
     L.free()
 
 
-def test_decode_core_35b_shape_batched_vs_oracle():
+def test_decode_core_35b_shape_batched_vs_oracle(variant):
     """Qwen3.6-35B-A3B GDN shape, 3 sequences with distinct states, 4 tokens."""
     d = Q35B
     w = synth.layer_weights(d, 31, gnorm_std=0.1, projections=False)
@@ -73,7 +87,7 @@ def test_decode_core_35b_shape_batched_vs_oracle():
     L.free()
 
 
-def test_multi_layer_dev_call_equals_per_layer_calls():
+def test_multi_layer_dev_call_equals_per_layer_calls(variant):
     from overhang_amd import hip
     d = CFG1
     nl, B = 5, 2
@@ -154,6 +168,7 @@ def test_argument_errors_are_reported():
 @pytest.mark.parametrize("ncs", [1, 2, 4, 8])
 def test_column_slices_agree_with_oracle(ncs, monkeypatch):
     """Every column-slice count (incl. the cross-slice gated-norm epilogue)."""
+    monkeypatch.setenv("OMH_DECODE_KERNEL", "sliced")
     monkeypatch.setenv("OMH_DECODE_NCS", str(ncs))
     d = GdnDims(2, 4, 128, 128, 4, 0)
     w = synth.layer_weights(d, 70 + ncs, gnorm_std=0.2, projections=False)
@@ -172,7 +187,7 @@ def test_column_slices_agree_with_oracle(ncs, monkeypatch):
     L.free()
 
 
-def test_varying_batch_keeps_each_sequence_history():
+def test_varying_batch_keeps_each_sequence_history(variant):
     """Calls with B = 3, 1, 2, 3, 1 on one layer: sequences left out of a call
     keep their conv history and phase; each matches its own oracle run."""
     d = CFG1
@@ -201,7 +216,7 @@ def test_varying_batch_keeps_each_sequence_history():
     L.free()
 
 
-def test_state_set_mid_stream_restarts_history():
+def test_state_set_mid_stream_restarts_history(variant):
     """state_set after some decode steps (ring phase != 0) re-bases the ring."""
     d = CFG1
     w = synth.layer_weights(d, 90, projections=False)
@@ -219,4 +234,47 @@ def test_state_set_mid_stream_restarts_history():
                                    conv0, S0)
     assert_close(got, ref)
     assert np.array_equal(L.get_state(0)[0], cref)
+    L.free()
+
+
+@pytest.mark.parametrize("rep", [1, 2, 3, 4, 8])
+def test_paired_kernel_every_rep(rep, monkeypatch):
+    """The paired kernel streams rep value heads per key head with a two-deep
+    prefetch: odd and even rep, rep = 1 (no prefetch) and the maximum."""
+    monkeypatch.setenv("OMH_DECODE_KERNEL", "paired")
+    d = GdnDims(2, 2 * rep, 64, 64, 4, 0)
+    seed = 110 + rep
+    w = synth.layer_weights(d, seed, gnorm_std=0.2, projections=False)
+    B, T = 2, 3
+    inp = synth.core_inputs(d, T, seed, B=B)
+    conv0, S0 = synth.states(d, seed, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    got = np.stack([L.decode_core(inp["qkv"][:, t], inp["z"][:, t], inp["a"][:, t], inp["b"][:, t])
+                    for t in range(T)], axis=1)
+    for s in range(B):
+        ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"][s], inp["z"][s], inp["a"][s], inp["b"][s],
+                                          conv0[s], S0[s])
+        conv, S = L.get_state(s)
+        assert_close(got[s], ref, what=f"rep={rep} seq {s} core")
+        assert_close(S, Sref, what=f"rep={rep} seq {s} S")
+        assert np.array_equal(conv, cref)
+    L.free()
+
+
+def test_paired_kernel_rejects_rep_above_limit(monkeypatch):
+    monkeypatch.setenv("OMH_DECODE_KERNEL", "paired")
+    d = GdnDims(1, 16, 16, 16, 4, 0)
+    w = synth.layer_weights(d, 120, projections=False)
+    L = gdn.GdnLayer(new_li(), d, w)
+    inp = synth.core_inputs(d, 1, 120)
+    with pytest.raises(gdn.OmhError) as e:
+        L.decode_core(inp["qkv"], inp["z"], inp["a"], inp["b"])
+    assert e.value.code == gdn.OMH_ERR_DEVICE
+    monkeypatch.delenv("OMH_DECODE_KERNEL")
+    core = L.decode_core(inp["qkv"], inp["z"], inp["a"], inp["b"])    # auto: sliced
+    ref, _, _ = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"],
+                                np.zeros((d.conv_dim, 3), np.float32), np.zeros((16, 16, 16), np.float32))
+    assert_close(core, ref)
     L.free()
