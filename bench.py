@@ -330,11 +330,11 @@ def main():
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = probe = None
+    pre = None
     if a.part == "all":
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
-        probe = copy_probe(hip, 1 << 29, 20, 3)
-        log(f"copy probe: {probe['GBs']:.0f} GB/s (D2D copy of 512 MiB)")
+    probe = copy_probe(hip, 1 << 29, 20, 3)
+    log(f"copy probe: {probe['GBs']:.0f} GB/s (D2D copy of 512 MiB)")
     cpu = None
     if not a.no_cpu:
         log("cpu baseline (oracle, OpenMP) ...")
