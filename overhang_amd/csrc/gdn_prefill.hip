@@ -11,11 +11,11 @@
 //     S <- e^{gc_last} S + (K * e^{gc_last - gc})^T v_new
 // Only exp of differences of cumulative decays are formed, never exp(-gc).
 //
-// Five launches, all on the caller's stream:
-//   P1 prep    conv + SiLU, q/k L2 norm (+ q scale), gates        HBM-bound
-//   P5 commit  conv history ring -> last K-1 inputs, new phase     tiny
-//   P2 chunk   per (value head, chunk): KK^T, QK^T, X, W, U on fp32 MFMA,
-//              written as per-lane fragment panels for P3          MFMA-bound
+// Four launches, all on the caller's stream:
+//   P1 wy      per (value head, chunk): conv + SiLU, q/k L2 norm, gates,
+//              KK^T, QK^T, X, W, U on fp32 MFMA, written as per-lane
+//              fragment panels for P3                              MFMA-bound
+//   P2 commit  conv history ring -> last K-1 inputs, new phase     tiny
 //   P3 scan    per (value head, 16-column block): the chunk recurrence,
 //              sequential over chunks, on fp32 MFMA                MFMA-bound
 //   P4 norm    gated RMSNorm of the head outputs                   HBM-bound
@@ -41,96 +41,26 @@ __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
 }
 __device__ __forceinline__ v4f v4zero() { v4f z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
-// Scan work split for head dim D: NWV waves per workgroup, each owning KT
-// kd tiles of S and TT of the chunk's 4 token tiles.
+// Scan work split for head dim D: NWV = D/16 waves per workgroup; wave w
+// owns row tile w (16 kd rows) of the workgroup's 128 x 16 slice of S.  The
+// eight per-chunk reductions (v_new and o for the chunk's 4 token tiles)
+// are jobs j = 0..7 (kind j / 4, token tile j % 4), job j on wave j % NWV.
+// Panels, per lane, in MFMA fragment order (the WY kernel writes them):
+//   W, Q e^gc   per (head, chunk, wave w): f = tt*4 + s -> row 16tt + l%16, col 16w + 4g + s
+//   (K e^{gl-gc})^T  same index: f = tt*4 + s -> row 16tt + 4g + s, col 16w + l%16
+//   Aqk         per (head, chunk, token tile mt): f = kt*4 + s -> row 16mt + l%16, col 16kt + 4g + s
+//   U           per (head, chunk, column block cb, mt): f = r -> row 16mt + 4g + r, col 16cb + l%16
+// (g = l / 16); each group of four consecutive f is one float4 per lane.
 template <int D>
 struct ScanShape {
-    static constexpr int NWV = D / 16 < 4 ? D / 16 : 4;
-    static constexpr int KT = D / 16 / NWV;
-    static constexpr int TT = 4 / NWV;
-    static constexpr int NFW = 16 * KT;        // W / Q fragments per lane per chunk
-    static constexpr int NFK = 16 * KT;        // K^T fragments
-    static constexpr int NFA = 16 * TT;        // Aqk fragments
-    static constexpr int NFU = 4 * TT;         // U values per column block
-    static_assert(NWV * KT * 16 == D && NWV * TT == 4, "scan split");
+    static constexpr int NWV = D / 16;
+    static constexpr int JPW = NWV >= 8 ? 1 : 8 / NWV;    // reduction jobs per wave
+    static_assert(NWV >= 1 && NWV <= 8, "scan split");
 };
+// float4 index of panel group f4 of lane l in block `blk` (4 groups per block)
+__device__ __forceinline__ size_t pan4(size_t blk, int f4, int l) { return ((blk * 4 + f4) * OMH_WAVE + l) * 4; }
 
-// ---------------------------------------------------------------- P1 prep
-// grid (2*kh + vh, Tp/C); thread = channel of one q, k or v head.
-template <int D>
-__global__ __launch_bounds__((D < 64 ? 64 : D))
-void prefill_prep_kernel(const PrefillArgs a) {
-    constexpr int NT = D < 64 ? 64 : D;
-    constexpr int NW = NT / OMH_WAVE;
-    const int grp = blockIdx.x, t0 = blockIdx.y * C;
-    const int tid = threadIdx.x, lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
-    const int kh = a.kh, vh = a.vh, K = a.K;
-    const int key_dim = kh * D, conv_dim = 2 * key_dim + vh * D;
-    int kind, head, gch0;
-    if (grp < kh) { kind = 0; head = grp; gch0 = grp * D; }
-    else if (grp < 2 * kh) { kind = 1; head = grp - kh; gch0 = key_dim + head * D; }
-    else { kind = 2; head = grp - 2 * kh; gch0 = 2 * key_dim + head * D; }
-
-    __shared__ float s_y[C][D + 1];
-    if (tid < D) {
-        const int gch = gch0 + tid;
-        float w[kConvRing], h[kConvRing - 1];
-        const float4 wv = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)gch * kConvRing);
-        for (int j = 0; j < K; j++) w[j] = f4_get(wv, j);
-        if (t0 == 0) {
-            const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
-            const float4 rv = *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, gch, conv_dim));
-            for (int j = 0; j < K - 1; j++) h[j] = f4_get(rv, ring_slot(ph, K, j));
-        } else {
-            for (int j = 0; j < K - 1; j++) h[j] = a.qkv[(size_t)(t0 - (K - 1) + j) * a.ld_qkv + gch];
-        }
-        float *vout = a.v + ((size_t)head * a.Tp + t0) * D + tid;
-        for (int t = 0; t < C; t++) {
-            const int tt = t0 + t;
-            float y = 0.f;
-            if (tt < a.T) {
-                const float x = a.qkv[(size_t)tt * a.ld_qkv + gch];
-                float acc = 0.f;
-                for (int j = 0; j < K - 1; j++) acc += w[j] * h[j];   // qwen.c:315-316
-                acc += w[K - 1] * x;
-                for (int j = 0; j < K - 2; j++) h[j] = h[j + 1];
-                h[K - 2] = x;
-                y = omh_silu(acc);
-            }
-            if (kind == 2) vout[(size_t)t * D] = y;
-            else s_y[t][tid] = y;
-        }
-    }
-    if (kind == 2) {
-        if (tid < C) {                            // gates (qwen.c:337-338)
-            const int tt = t0 + tid;
-            float g = 0.f, be = 0.f;
-            if (tt < a.T) {
-                g = -expf(a.L.A_log[head]) * omh_softplus(a.a[(size_t)tt * a.ld_ab + head] + a.L.dt_bias[head]);
-                be = omh_sigmoid(a.b[(size_t)tt * a.ld_ab + head]);
-            }
-            a.g[(size_t)head * a.Tp + tt] = g;
-            a.beta[(size_t)head * a.Tp + tt] = be;
-        }
-        return;
-    }
-    __syncthreads();
-    // per-token L2 norm over the head's D channels (qwen.c:153-157, 327-329)
-    float *out = (kind == 0 ? a.qn : a.kn) + ((size_t)head * a.Tp + t0) * D;
-    const float scale = kind == 0 ? 1.f / sqrtf((float)D) : 1.f;
-    for (int t = wave; t < C; t += NW) {
-        float ss = 0.f;
-        for (int i = lane; i < D; i += OMH_WAVE) ss += s_y[t][i] * s_y[t][i];
-        ss = omh_xor_sum_below<OMH_WAVE>(ss);
-        const float r = 1.f / sqrtf(ss + 1e-6f);
-        for (int i = lane; i < D; i += OMH_WAVE) {
-            const float q = s_y[t][i] * r;
-            out[(size_t)t * D + i] = kind == 0 ? q * scale : q;
-        }
-    }
-}
-
-// ---------------------------------------------------------------- P5 commit
+// ---------------------------------------------------------------- P2 commit
 // New conv history = last K-1 entries of [old history, x_0 .. x_{T-1}],
 // written in ring order for phase (p + T) mod ring size.  Every block reads
 // the phase from phase[epoch]; the new one goes to phase[1 - epoch] (block 0
@@ -194,190 +124,426 @@ __device__ __forceinline__ size_t panel_idx(size_t base4, int f, int l) {
     return ((base4 + (size_t)(f >> 2)) * OMH_WAVE + l) * 4 + (f & 3);
 }
 
-// ---------------------------------------------------------------- P2 chunk
+// ---------------------------------------------------------------- P1 WY
+// One workgroup per (value head h, chunk c): the chunk's conv + SiLU and
+// L2 norms straight from mixed_qkv, the gates, then on fp32 MFMA
+//   G = K K^T, P = Q K^T (lower 16x16 tiles), L = strict_lower(beta_i G e^{gc_i-gc_j}),
+//   Aqk = lower_incl(P e^{gc_i-gc_j}), X = (I + L)^-1 (blocked: four 16x16
+//   diagonal inverses by forward substitution in parallel, then the
+//   off-diagonal blocks level by level, X_ij = -D_i sum_k L_ik X_kj),
+//   W = X (K beta e^gc), U = X (V beta),
+// and the operand panels the scan reads.  Threads exchange data through
+// LDS only, so every barrier orders LDS alone: the next item's prefetched
+// inputs and this item's panel stores stay in flight across them.
 template <int D>
-__global__ __launch_bounds__(256)
-void prefill_chunk_kernel(const PrefillArgs a) {
-    using SS = ScanShape<D>;
-    constexpr int NWV = SS::NWV, KT = SS::KT, TT = SS::TT;
-    constexpr int PD = D + 4, PC = C + 4;        // padded LDS row lengths
-    const int h = blockIdx.x, c = blockIdx.y;
-    const int vh = a.vh, rep = vh / a.kh, hk = h / rep;
-    const int t0 = c * C;
+struct WyShape {
+    static constexpr int NW = D / 16 < 4 ? 4 : D / 16;   // waves
+    static constexpr int NT = NW * OMH_WAVE;
+    static constexpr int PD = D + 4, PC = C + 4;         // padded LDS rows
+    static constexpr int NCT = D / 16;                   // 16-column tiles of D
+    static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 4 * C) * sizeof(float);
+};
+
+// conv1d (K taps, history oldest..newest, then the input; op order as
+// engines/qwen.c:311-319) + SiLU over NS consecutive tokens, written down an
+// LDS column with row stride PD; tokens at or past nvalid are zero.
+template <int KK, int PD, int NS>
+__device__ __forceinline__ void conv_tokens_impl(const float (&xin)[NS], const float (&hist0)[kConvRing - 1],
+                                                 float4 wv, float *dst, int nvalid) {
+    const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+    float h[kConvRing - 1];
+#pragma unroll
+    for (int j = 0; j < kConvRing - 1; j++) h[j] = hist0[j];
+#pragma unroll
+    for (int t = 0; t < NS; t++) {
+        const float x = xin[t];
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < KK - 1; j++) acc += w[j] * h[j];
+        acc += w[KK - 1] * x;
+#pragma unroll
+        for (int j = 0; j + 1 < KK - 1; j++) h[j] = h[j + 1];
+        h[KK - 2] = x;
+        dst[t * PD] = t < nvalid ? omh_silu_fast(acc) : 0.f;
+    }
+}
+
+// The lower 16x16 tiles of a 64x64 matrix, in order (0,0) (1,0) (1,1) (2,0) ...
+__device__ __forceinline__ void lower_tile(int it, int &i, int &j) {
+    i = it < 1 ? 0 : (it < 3 ? 1 : (it < 6 ? 2 : 3));
+    j = it - i * (i + 1) / 2;
+}
+
+// Work item m -> (value head, chunk), XCD-aware: with N items and a grid
+// that is a multiple of 8, the items a given XCD processes together are
+// consecutive (the value heads of one key head, then the next key head, for
+// one chunk), so the q/k inputs they share are read once per XCD L2.
+__device__ __forceinline__ void wy_item(int m, int N, int kh, int rep, int &h, int &hk, int &c) {
+    const int mm = N % 8 == 0 ? (m % 8) * (N / 8) + m / 8 : m;
+    const int j = mm % rep;
+    hk = (mm / rep) % kh;
+    c = mm / (rep * kh);
+    h = hk * rep + j;
+}
+
+// Inputs of one work item held in registers (prefetched during the
+// previous item).  The conv work of an item is 3D channels x C tokens,
+// split into units of (channel, NSEG-token segment) dealt round-robin over
+// all threads (NU units each), so every wave does an equal share; a unit's
+// K-1 history is the inputs before its segment (the ring for the first
+// segment of chunk 0).  The gate wave also holds the gate inputs of its token.
+template <int D>
+struct WyIn {
+    static constexpr int NSEG = 16;
+    static constexpr int NUNITS = 3 * D * (C / NSEG);
+    static constexpr int NU = (NUNITS + WyShape<D>::NT - 1) / WyShape<D>::NT;
+    float xin[NU][NSEG];
+    float4 hv[NU];        // the K-1 inputs before the segment, in .x .y .z
+    float4 wv[NU];
+    float ga, gb, galog, gdt;
+
+    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_lane,
+                                         int lane) {
+        const int kh = a.kh, vh = a.vh, K = a.K, T = a.T, t0 = c * C;
+        const int key_dim = kh * D, conv_dim = 2 * key_dim + vh * D;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const int unit = tid + u * WyShape<D>::NT;
+            if (unit >= NUNITS) continue;
+            const int ch = unit % (3 * D), seg = unit / (3 * D);
+            const int part = ch / D, cc = ch % D;
+            const int gch = part == 0 ? hk * D + cc : (part == 1 ? key_dim + hk * D + cc : 2 * key_dim + h * D + cc);
+            const int ts = t0 + seg * NSEG;
+#pragma unroll
+            for (int t = 0; t < NSEG; t++) xin[u][t] = a.qkv[(size_t)min(ts + t, T - 1) * a.ld_qkv + gch];   // past T: unused
+            wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)gch * kConvRing);
+            // Branch-free: the first segment of chunk 0 takes its history from
+            // the ring at conv time instead (rows clamped to a valid range here).
+            const float *col = a.qkv + gch;
+            const int r0 = ts - (K - 1);
+            hv[u].x = col[(size_t)min(max(r0, 0), T - 1) * a.ld_qkv];
+            hv[u].y = col[(size_t)min(max(r0 + (K > 2 ? 1 : 0), 0), T - 1) * a.ld_qkv];
+            hv[u].z = col[(size_t)min(max(r0 + (K > 3 ? 2 : 0), 0), T - 1) * a.ld_qkv];
+            hv[u].w = 0.f;
+        }
+        if (gate_lane) {
+            const int tt = min(t0 + lane, T - 1);
+            ga = a.a[(size_t)tt * a.ld_ab + h];
+            gb = a.b[(size_t)tt * a.ld_ab + h];
+            galog = a.L.A_log[h];
+            gdt = a.L.dt_bias[h];
+        }
+    }
+};
+
+template <int D>
+__global__ __launch_bounds__(WyShape<D>::NT)
+void prefill_wy_kernel(const PrefillArgs a) {
+    using WS = WyShape<D>;
+    constexpr int NW = WS::NW, NT = WS::NT, PD = WS::PD, PC = WS::PC, NCT = WS::NCT;
+    constexpr int NWV = ScanShape<D>::NWV;
+
+    const int kh = a.kh, rep = a.vh / kh, K = a.K, T = a.T;
+    const int nitems = a.vh * a.nc;
     const int tid = threadIdx.x, lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
     const int l16 = lane % 16, g4 = lane / 16;
+    const bool gate_wave = wave == NW - 1;
 
     extern __shared__ float smem[];
-    float *Ks = smem;                            // [C][PD]
-    float *Qs = Ks + C * PD;                     // [C][PD]
-    float *Vs = Qs + C * PD;                     // [C][PD]
-    float *Xs = Vs + C * PD;                     // [C][PC]  L, then X = (I+L)^-1
-    float *As = Xs + C * PC;                     // [C][PC]  Aqk
-    float *gcs = As + C * PC;                    // [C]
-    float *bs = gcs + C;                         // [C]
+    float *Qs = smem;                            // [C][PD] q~ -> q^; later W
+    float *Ks = Qs + C * PD;                     // [C][PD]
+    float *Vs = Ks + C * PD;                     // [C][PD]
+    float *Ls = Vs + C * PD;                     // [C][PC] L
+    float *Xs = Ls + C * PC;                     // [C][PC] diagonal blocks of (I + L)^-1
+    float *As = Xs + C * PC;                     // [C][PC] Aqk
+    float *gcs = As + C * PC;                    // [C] cumulative log decay
+    float *bs = gcs + C;                         // [C] beta
+    float *ws = bs + C;                          // [C] beta e^gc
+    float *egl = ws + C;                         // [C] e^{gc_last - gc}
 
-    // 1. stage K, Q (key head hk), V (value head h), g, beta
-    {
-        const float *kp = a.kn + ((size_t)hk * a.Tp + t0) * D;
-        const float *qp = a.qn + ((size_t)hk * a.Tp + t0) * D;
-        const float *vp = a.v + ((size_t)h * a.Tp + t0) * D;
-        for (int e = tid; e < C * D / 4; e += 256) {
-            const int r = e / (D / 4), c4 = e % (D / 4);
-            const float4 kk = *reinterpret_cast<const float4 *>(kp + (size_t)e * 4);
-            const float4 qq = *reinterpret_cast<const float4 *>(qp + (size_t)e * 4);
-            const float4 vv = *reinterpret_cast<const float4 *>(vp + (size_t)e * 4);
-            float *kd = Ks + r * PD + c4 * 4, *qd = Qs + r * PD + c4 * 4, *vd = Vs + r * PD + c4 * 4;
-            kd[0] = kk.x; kd[1] = kk.y; kd[2] = kk.z; kd[3] = kk.w;
-            qd[0] = qq.x; qd[1] = qq.y; qd[2] = qq.z; qd[3] = qq.w;
-            vd[0] = vv.x; vd[1] = vv.y; vd[2] = vv.z; vd[3] = vv.w;
+    int m = blockIdx.x;
+    WyIn<D> in;
+    if (m < nitems) {
+        int h, hk, c;
+        wy_item(m, nitems, kh, rep, h, hk, c);
+        in.load(a, h, hk, c, tid, gate_wave, lane);
+    }
+    for (; m < nitems; m += gridDim.x) {
+        int h, hk, c;
+        wy_item(m, nitems, kh, rep, h, hk, c);
+        const int t0 = c * C;
+        const size_t hc = (size_t)h * a.nc + c;
+
+        // 1. conv + SiLU of the q, k channels of key head hk and the v
+        // channels of head h; tokens past T are zero.  Gates on the gate wave
+        // (qwen.c:337-338, zero past T) with an inclusive prefix sum of g.
+#pragma unroll
+        for (int u = 0; u < WyIn<D>::NU; u++) {
+            const int unit = tid + u * NT;
+            if (unit >= WyIn<D>::NUNITS) continue;
+            const int ch = unit % (3 * D), seg = unit / (3 * D);
+            const int part = ch / D, cc = ch % D;
+            constexpr int NS = WyIn<D>::NSEG;
+            float *dst = (part == 0 ? Qs : (part == 1 ? Ks : Vs)) + seg * NS * PD + cc;
+            const int nvalid = T - t0 - seg * NS;
+            float hist[kConvRing - 1];
+            if (t0 + seg * NS == 0) {
+                const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
+                const int gch = part == 0 ? hk * D + cc : (part == 1 ? kh * D + hk * D + cc : 2 * kh * D + h * D + cc);
+                const float4 rv = *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, gch, (2 * kh + a.vh) * D));
+#pragma unroll
+                for (int jj = 0; jj < kConvRing - 1; jj++) hist[jj] = jj < K - 1 ? f4_get(rv, ring_slot(ph, K, jj)) : 0.f;
+            } else {
+                hist[0] = in.hv[u].x; hist[1] = in.hv[u].y; hist[2] = in.hv[u].z;
+            }
+            if (K == 4) conv_tokens_impl<4, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
+            else if (K == 3) conv_tokens_impl<3, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
+            else conv_tokens_impl<2, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
         }
-        if (wave == 0) {
-            // inclusive prefix sum of g over the chunk (one lane per token)
-            float x = a.g[(size_t)h * a.Tp + t0 + lane];
+        if (gate_wave) {
+            float g = 0.f, be = 0.f;
+            if (t0 + lane < T) {
+                g = -expf(in.galog) * omh_softplus(in.ga + in.gdt);
+                be = omh_sigmoid(in.gb);
+            }
+            float x = g;
 #pragma unroll
             for (int off = 1; off < OMH_WAVE; off <<= 1) {
                 const float y = __shfl_up(x, off, OMH_WAVE);
                 if (lane >= off) x += y;
             }
+            const float gl = __shfl(x, C - 1, OMH_WAVE);
             gcs[lane] = x;
-            bs[lane] = a.beta[(size_t)h * a.Tp + t0 + lane];
-            if (lane == C - 1) a.glast[(size_t)h * a.nc + c] = expf(x);
+            bs[lane] = be;
+            ws[lane] = be * expf(x);
+            egl[lane] = expf(gl - x);
+            if (lane == C - 1) a.glast[hc] = expf(x);
         }
-    }
-    __syncthreads();
+        // prefetch the next item's inputs; they land during this item's math
+        if (m + (int)gridDim.x < nitems) {
+            int h2, hk2, c2;
+            wy_item(m + gridDim.x, nitems, kh, rep, h2, hk2, c2);
+            in.load(a, h2, hk2, c2, tid, gate_wave, lane);
+        }
+        omh_lds_barrier();
 
-    // 2. G = K K^T and QK = Q K^T, lower tiles only; wave w owns row tile w
-    {
-        v4f G[4], Q[4];
+        // 2. L2 norm per token over the head's D channels (eps 1e-6), q also
+        // scaled by D^-1/2 (qwen.c:153-157, 326-329)
+        {
+            // TPR consecutive lanes per row, each over D/TPR columns
+            constexpr int TPR = NT / (2 * C) >= 4 ? 4 : 2;
+            constexpr int EPT = D / TPR;
+            static_assert(EPT % 4 == 0 && NT / TPR >= 2 * C / 2, "norm layout");
+            for (int r = tid / TPR; r < 2 * C; r += NT / TPR) {
+                float *row = (r < C ? Qs + r * PD : Ks + (r - C) * PD) + (tid % TPR) * EPT;
+                float4 v[EPT / 4];
+                float ss = 0.f;
 #pragma unroll
-        for (int n = 0; n < 4; n++) { G[n] = v4zero(); Q[n] = v4zero(); }
-        const int m0 = wave * 16;
-        for (int k0 = 0; k0 < D; k0 += 4) {
-            const float ak = Ks[(m0 + l16) * PD + k0 + g4];
-            const float aq = Qs[(m0 + l16) * PD + k0 + g4];
+                for (int i = 0; i < EPT / 4; i++) {
+                    v[i] = *reinterpret_cast<const float4 *>(row + 4 * i);
+                    ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+                }
+                ss = omh_group_sum<TPR>(ss);
+                const float rr = 1.f / sqrtf(ss + 1e-6f);
+                const float sc = 1.f / sqrtf((float)D);
 #pragma unroll
-            for (int n = 0; n < 4; n++) {
-                if (n <= wave) {
-                    const float bk = Ks[(n * 16 + l16) * PD + k0 + g4];
-                    G[n] = mfma4(ak, bk, G[n]);
-                    Q[n] = mfma4(aq, bk, Q[n]);
+                for (int i = 0; i < EPT / 4; i++) {
+                    float4 y = f4_scale(v[i], rr);
+                    if (r < C) y = f4_scale(y, sc);
+                    *reinterpret_cast<float4 *>(row + 4 * i) = y;
                 }
             }
         }
-        // masks and decays; write full rows of the row tile
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
+        omh_lds_barrier();
+
+        // 3. G = K K^T (products 0-9) and P = Q K^T (10-19) on the lower
+        // tiles, dealt round-robin over the waves; lane group g4 sums the
+        // contiguous k range [g4 D/4, (g4+1) D/4), so operands load as float4.
+        for (int p = wave; p < 20; p += NW) {
+            int ti, tj;
+            lower_tile(p % 10, ti, tj);
+            const bool isP = p >= 10;
+            v4f acc = v4zero(), acc2 = v4zero();
+            const float *aa = (isP ? Qs : Ks) + (16 * ti + l16) * PD + g4 * (D / 4);
+            const float *kb = Ks + (16 * tj + l16) * PD + g4 * (D / 4);
+#pragma unroll 2
+            for (int s4 = 0; s4 < D / 16; s4++) {
+                const float4 A = *reinterpret_cast<const float4 *>(aa + 4 * s4);
+                const float4 B = *reinterpret_cast<const float4 *>(kb + 4 * s4);
+                acc = mfma4(A.x, B.x, acc);
+                acc2 = mfma4(A.y, B.y, acc2);
+                acc = mfma4(A.z, B.z, acc);
+                acc2 = mfma4(A.w, B.w, acc2);
+            }
+            acc += acc2;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int i = m0 + 4 * g4 + r, j = n * 16 + l16;
-                float lv = 0.f, av = 0.f;
-                if (j <= i) {
-                    const float dec = expf(gcs[i] - gcs[j]);
-                    av = Q[n][r] * dec;
-                    if (j < i) lv = bs[i] * G[n][r] * dec;
+                const int row = 16 * ti + 4 * g4 + r, col = 16 * tj + l16;
+                const float dec = col <= row ? expf(gcs[row] - gcs[col]) : 0.f;
+                if (isP) As[row * PC + col] = col <= row ? acc[r] * dec : 0.f;
+                else Ls[row * PC + col] = col < row ? bs[row] * acc[r] * dec : 0.f;
+            }
+        }
+        for (int e = tid; e < C * C; e += NT) {  // upper tiles: zero (never multiplied)
+            const int row = e / C, col = e % C;
+            if (col / 16 > row / 16) { Ls[row * PC + col] = 0.f; As[row * PC + col] = 0.f; }
+        }
+        omh_lds_barrier();
+
+        // 4. waves 0-3: diagonal blocks D_b = (I + L_bb)^-1 by forward
+        // substitution, lane jj < 16 keeping column jj (X[i][jj] = -sum_{m<i}
+        // L[i][m] X[m][jj] below the diagonal).  Meanwhile the other waves
+        // (all waves, after, when there are only four) write the panels that
+        // need no inverse: Q e^gc, (K e^{gl - gc})^T and Aqk, a float4 per lane.
+        if (wave < 4) {
+            const int b0 = 16 * wave;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float acc = 0.f;
+#pragma unroll
+                for (int mm = 0; mm < i; mm++) acc += Ls[(b0 + i) * PC + b0 + mm] * x[mm];
+                x[i] = lane < i ? -acc : (lane == i ? 1.f : 0.f);
+            }
+            if (lane < 16)
+#pragma unroll
+                for (int i = 0; i < 16; i++) Xs[(b0 + i) * PC + b0 + lane] = x[i];
+        }
+        {
+            constexpr int PW = NW > 4 ? NW - 4 : NW;         // panel-writing waves
+            const int pw_t = NW > 4 ? tid - 4 * OMH_WAVE : tid;
+            if (pw_t >= 0) {
+                // Q/K panels: NWV scan waves x 4 token tiles x 64 lanes
+                for (int e = pw_t; e < NWV * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
+                    const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
+                    const int ll16 = l % 16, lg = l / 16;
+                    const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
+                    const float4 vq = f4_scale(*reinterpret_cast<const float4 *>(Qs + rq * PD + cq), expf(gcs[rq]));
+                    const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
+                    const float4 vk = make_float4(Ks[rk * PD + ck] * egl[rk], Ks[(rk + 1) * PD + ck] * egl[rk + 1],
+                                                  Ks[(rk + 2) * PD + ck] * egl[rk + 2], Ks[(rk + 3) * PD + ck] * egl[rk + 3]);
+                    *reinterpret_cast<float4 *>(a.pq + pan4(hc * NWV + w, tt, l)) = vq;
+                    *reinterpret_cast<float4 *>(a.pk + pan4(hc * NWV + w, tt, l)) = vk;
                 }
-                Xs[i * PC + j] = lv;
-                As[i * PC + j] = av;
+                for (int e = pw_t; e < 16 * OMH_WAVE; e += PW * OMH_WAVE) {
+                    const int l = e % OMH_WAVE, kt = (e / OMH_WAVE) % 4, mt = e / (4 * OMH_WAVE);
+                    const int row = 16 * mt + l % 16, col = 16 * kt + 4 * (l / 16);
+                    *reinterpret_cast<float4 *>(a.pa + pan4(hc * 4 + mt, kt, l)) =
+                        *reinterpret_cast<const float4 *>(As + row * PC + col);
+                }
             }
         }
-    }
-    __syncthreads();
+        omh_lds_barrier();
 
-    const size_t hc = (size_t)h * a.nc + c;
-    if (wave == 0) {
-        // 3a. X = (I + L)^-1 by forward substitution; lane j keeps column j
-        // of X: X[i][j] = -sum_{m<i} L[i][m] X[m][j] for j < i, X[j][j] = 1.
-        float xc[C];
+        // 5. W and U by blocked forward substitution on (I + L) [W | U] =
+        // [K beta e^gc | V beta]: row tile i = D_i (RHS_i - sum_{k<i} L_ik R_k),
+        // column tile by column tile, the tiles kept in registers in MFMA D
+        // layout (a D-layout tile feeds the B operand directly: at k-step s
+        // lane group g supplies row 4g+s).  Each wave takes the W and the U
+        // tile of one column (two independent chains).  U goes straight to
+        // its panel (the scan's D layout); W is staged in Qs.
+        for (int q = wave; q < 2 * NCT; q += 2 * NW) {
+            const int tn = q % NCT;
+            const bool two = q + NW < 2 * NCT;           // this wave also has the U tile of column tn
+            const bool firstU = q >= NCT;
+            v4f R0[4], R1[4];
 #pragma unroll
-        for (int i = 0; i < C; i++) {
-            float acc = 0.f;
+            for (int i = 0; i < 4; i++) {
+                v4f acc0, acc1;
 #pragma unroll
-            for (int m = 0; m < i; m++) acc += Xs[i * PC + m] * xc[m];
-            xc[i] = lane < i ? -acc : (lane == i ? 1.f : 0.f);
-        }
+                for (int r = 0; r < 4; r++) {
+                    const int row = 16 * i + 4 * g4 + r;
+                    acc0[r] = firstU ? Vs[row * PD + 16 * tn + l16] * bs[row] : Ks[row * PD + 16 * tn + l16] * ws[row];
+                    acc1[r] = two ? Vs[row * PD + 16 * tn + l16] * bs[row] : 0.f;
+                }
 #pragma unroll
-        for (int i = 0; i < C; i++) Xs[i * PC + lane] = xc[i];
-    } else {
-        // 3b. panels that do not need X: Q*e^gc, (K*e^{gl-gc})^T, Aqk
-        const float gl = gcs[C - 1];
-        for (int e = tid - OMH_WAVE; e < NWV * OMH_WAVE * SS::NFW; e += 256 - OMH_WAVE) {
-            const int f = e % SS::NFW, l = (e / SS::NFW) % OMH_WAVE, w = e / (SS::NFW * OMH_WAVE);
-            const int ll16 = l % 16, lg = l / 16;
-            // W/Q order: f = (tt*KT + kt)*4 + s -> row 16tt + l%16, col 16(w*KT+kt) + 4g + s
-            {
-                const int s = f & 3, kt = (f >> 2) % KT, tt = (f >> 2) / KT;
-                const int row = tt * 16 + ll16, col = 16 * (w * KT + kt) + 4 * lg + s;
-                a.pq[panel_idx((hc * NWV + w) * (SS::NFW / 4), f, l)] = Qs[row * PD + col] * expf(gcs[row]);
+                for (int k = 0; k < i; k++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        const float nl = -Ls[(16 * i + l16) * PC + 16 * k + 4 * g4 + s];
+                        acc0 = mfma4(nl, R0[k][s], acc0);
+                        acc1 = mfma4(nl, R1[k][s], acc1);
+                    }
+                R0[i] = v4zero();
+                R1[i] = v4zero();
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    const float dv = Xs[(16 * i + l16) * PC + 16 * i + 4 * g4 + s];
+                    R0[i] = mfma4(dv, acc0[s], R0[i]);
+                    R1[i] = mfma4(dv, acc1[s], R1[i]);
+                }
             }
-            // K order: f = (kt*4 + tt)*4 + s -> row (token) 16tt + 4g + s, col 16(w*KT+kt) + l%16
-            {
-                const int s = f & 3, tt = (f >> 2) & 3, kt = f >> 4;
-                const int row = tt * 16 + 4 * lg + s, col = 16 * (w * KT + kt) + ll16;
-                a.pk[panel_idx((hc * NWV + w) * (SS::NFK / 4), f, l)] = Ks[row * PD + col] * expf(gl - gcs[row]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // U panel of column block tn, token tile i (the D layout of R)
+                float *up = a.pu + pan4(hc * NCT + tn, i, lane);
+                if (firstU) {
+                    *reinterpret_cast<v4f *>(up) = R0[i];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) Qs[(16 * i + 4 * g4 + r) * PD + 16 * tn + l16] = R0[i][r];
+                    if (two) *reinterpret_cast<v4f *>(up) = R1[i];
+                }
             }
         }
-        for (int e = tid - OMH_WAVE; e < NWV * OMH_WAVE * SS::NFA; e += 256 - OMH_WAVE) {
-            // A order: f = u*16 + kt*4 + s -> row 16(w*TT+u) + l%16, col 16kt + 4g + s
-            const int f = e % SS::NFA, l = (e / SS::NFA) % OMH_WAVE, w = e / (SS::NFA * OMH_WAVE);
-            const int s = f & 3, kt = (f >> 2) & 3, u = f >> 4;
-            const int row = 16 * (w * TT + u) + l % 16, col = 16 * kt + 4 * (l / 16) + s;
-            a.pa[panel_idx((hc * NWV + w) * (SS::NFA / 4), f, l)] = As[row * PC + col];
-        }
-    }
-    __syncthreads();
+        omh_lds_barrier();
 
-    // 4. W = X (K * beta * e^gc), U = X (V * beta); wave w owns token tile w
-    constexpr int NT16 = D / 16;
-    v4f Wt[NT16], Ut[NT16];
-#pragma unroll
-    for (int n = 0; n < NT16; n++) { Wt[n] = v4zero(); Ut[n] = v4zero(); }
-    {
-        const int m0 = wave * 16;
-        for (int k0 = 0; k0 < m0 + 16; k0 += 4) {            // X is lower triangular
-            const int kk = k0 + g4;
-            const float ax = Xs[(m0 + l16) * PC + kk];
-            const float sb = bs[kk], sw = bs[kk] * expf(gcs[kk]);
-#pragma unroll
-            for (int n = 0; n < NT16; n++) {
-                Wt[n] = mfma4(ax, Ks[kk * PD + n * 16 + l16] * sw, Wt[n]);
-                Ut[n] = mfma4(ax, Vs[kk * PD + n * 16 + l16] * sb, Ut[n]);
-            }
+        // 6. W panel (the Q panel's order)
+        for (int e = tid; e < NWV * 4 * OMH_WAVE; e += NT) {
+            const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
+            const int row = tt * 16 + l % 16, col = 16 * w + 4 * (l / 16);
+            *reinterpret_cast<float4 *>(a.pw + pan4(hc * NWV + w, tt, l)) =
+                *reinterpret_cast<const float4 *>(Qs + row * PD + col);
         }
-    }
-    __syncthreads();
-    // stage W (in Qs) and U (in Ks) row-major
-#pragma unroll
-    for (int n = 0; n < NT16; n++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = wave * 16 + 4 * g4 + r, j = n * 16 + l16;
-            Qs[i * PD + j] = Wt[n][r];
-            Ks[i * PD + j] = Ut[n][r];
-        }
-    __syncthreads();
-    // 5. W panel (same order as the Q panel) and U panel (D layout per column block)
-    for (int e = tid; e < NWV * OMH_WAVE * SS::NFW; e += 256) {
-        const int f = e % SS::NFW, l = (e / SS::NFW) % OMH_WAVE, w = e / (SS::NFW * OMH_WAVE);
-        const int s = f & 3, kt = (f >> 2) % KT, tt = (f >> 2) / KT;
-        const int row = tt * 16 + l % 16, col = 16 * (w * KT + kt) + 4 * (l / 16) + s;
-        a.pw[panel_idx((hc * NWV + w) * (SS::NFW / 4), f, l)] = Qs[row * PD + col];
-    }
-    for (int e = tid; e < NT16 * NWV * OMH_WAVE * SS::NFU; e += 256) {
-        // U order per column block cb: f = u*4 + r -> row 16(w*TT+u) + 4g + r, col 16cb + l%16
-        const int f = e % SS::NFU, l = (e / SS::NFU) % OMH_WAVE;
-        const int w = (e / (SS::NFU * OMH_WAVE)) % NWV, cb = e / (SS::NFU * OMH_WAVE * NWV);
-        const int r = f & 3, u = f >> 2;
-        const int row = 16 * (w * TT + u) + 4 * (l / 16) + r, col = 16 * cb + l % 16;
-        a.pu[panel_idx(((hc * NT16 + cb) * NWV + w) * (SS::NFU / 4), f, l)] = Ks[row * PD + col];
+        omh_lds_barrier();                       // LDS is reused by the next item
     }
 }
 
 // ---------------------------------------------------------------- P3 scan
+// One chunk's operands for one scan wave, in MFMA fragment order.
+template <int D>
+struct ScanIn {
+    static constexpr int JPW = ScanShape<D>::JPW;
+    float Wf[16], Qf[16], Kf[16], Af[JPW][16], Uf[JPW][4];
+    float eg;
+
+    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int cb, int c, int w, int lane) {
+        constexpr int NWV = ScanShape<D>::NWV, NCB = D / 16;
+        const size_t hc = (size_t)h * a.nc + c;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            const float4 x = *reinterpret_cast<const float4 *>(a.pw + pan4(hc * NWV + w, tt, lane));
+            const float4 y = *reinterpret_cast<const float4 *>(a.pq + pan4(hc * NWV + w, tt, lane));
+            const float4 z = *reinterpret_cast<const float4 *>(a.pk + pan4(hc * NWV + w, tt, lane));
+            Wf[4 * tt] = x.x; Wf[4 * tt + 1] = x.y; Wf[4 * tt + 2] = x.z; Wf[4 * tt + 3] = x.w;
+            Qf[4 * tt] = y.x; Qf[4 * tt + 1] = y.y; Qf[4 * tt + 2] = y.z; Qf[4 * tt + 3] = y.w;
+            Kf[4 * tt] = z.x; Kf[4 * tt + 1] = z.y; Kf[4 * tt + 2] = z.z; Kf[4 * tt + 3] = z.w;
+        }
+#pragma unroll
+        for (int jj = 0; jj < JPW; jj++) {
+            const int mt = (w + jj * NWV) % 4;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const float4 x = *reinterpret_cast<const float4 *>(a.pa + pan4(hc * 4 + mt, kt, lane));
+                Af[jj][4 * kt] = x.x; Af[jj][4 * kt + 1] = x.y; Af[jj][4 * kt + 2] = x.z; Af[jj][4 * kt + 3] = x.w;
+            }
+            const float4 u = *reinterpret_cast<const float4 *>(a.pu + pan4(hc * NCB + cb, mt, lane));
+            Uf[jj][0] = u.x; Uf[jj][1] = u.y; Uf[jj][2] = u.z; Uf[jj][3] = u.w;
+        }
+        eg = a.glast[hc];
+    }
+};
+
+// Per (value head, 16-column block of S): the chunk recurrence, S held in
+// registers (MFMA D layout) for the whole sequence, one 16-row tile per
+// wave.  The next chunk's operands are in flight while the current one is
+// processed (two register sets), and the workgroup barriers order LDS only,
+// so they do not wait for those loads or for the output stores.
 template <int D>
 __global__ __launch_bounds__((ScanShape<D>::NWV * OMH_WAVE), 1)
 void prefill_scan_kernel(const PrefillArgs a) {
     using SS = ScanShape<D>;
-    constexpr int NWV = SS::NWV, KT = SS::KT, TT = SS::TT;
+    constexpr int NWV = SS::NWV, JPW = SS::JPW;
     constexpr int NCB = D / 16;
     const int vh = a.vh;
     // XCD-aware: the NCB column blocks of a head share one XCD (and its L2)
@@ -394,125 +560,115 @@ void prefill_scan_kernel(const PrefillArgs a) {
     __shared__ v4f s_o[NWV][4][OMH_WAVE];        // (Q e^gc) S partials
     __shared__ v4f s_vn[4][OMH_WAVE];            // v_new tiles (D layout)
 
-    // S rows 16(w*KT + kt) + 4g + r, column 16cb + l%16
+    // S rows 16w + 4g + r, column 16cb + l%16
     float *Sbase = a.L.S + ((size_t)a.seq * vh + h) * (D * D);
-    v4f S[KT];
+    v4f S;
 #pragma unroll
-    for (int kt = 0; kt < KT; kt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            S[kt][r] = Sbase[(size_t)(16 * (w * KT + kt) + 4 * g4 + r) * D + 16 * cb + l16];
+    for (int r = 0; r < 4; r++) S[r] = Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16];
 
     const size_t vdim = (size_t)vh * D;
-    for (int c = 0; c < a.nc; c++) {
-        const size_t hc = (size_t)h * a.nc + c;
-        float Wf[SS::NFW], Qf[SS::NFW], Kf[SS::NFK], Af[SS::NFA], Uf[SS::NFU];
-        {
-            const float4 *pw = reinterpret_cast<const float4 *>(a.pw) + (hc * NWV + w) * (SS::NFW / 4) * OMH_WAVE + lane;
-            const float4 *pq = reinterpret_cast<const float4 *>(a.pq) + (hc * NWV + w) * (SS::NFW / 4) * OMH_WAVE + lane;
-            const float4 *pk = reinterpret_cast<const float4 *>(a.pk) + (hc * NWV + w) * (SS::NFK / 4) * OMH_WAVE + lane;
-            const float4 *pa = reinterpret_cast<const float4 *>(a.pa) + (hc * NWV + w) * (SS::NFA / 4) * OMH_WAVE + lane;
-            const float4 *pu = reinterpret_cast<const float4 *>(a.pu) + ((hc * NCB + cb) * NWV + w) * (SS::NFU / 4) * OMH_WAVE + lane;
-#pragma unroll
-            for (int i = 0; i < SS::NFW / 4; i++) {
-                const float4 x = pw[i * OMH_WAVE], y = pq[i * OMH_WAVE];
-                Wf[4 * i] = x.x; Wf[4 * i + 1] = x.y; Wf[4 * i + 2] = x.z; Wf[4 * i + 3] = x.w;
-                Qf[4 * i] = y.x; Qf[4 * i + 1] = y.y; Qf[4 * i + 2] = y.z; Qf[4 * i + 3] = y.w;
-            }
-#pragma unroll
-            for (int i = 0; i < SS::NFK / 4; i++) {
-                const float4 x = pk[i * OMH_WAVE];
-                Kf[4 * i] = x.x; Kf[4 * i + 1] = x.y; Kf[4 * i + 2] = x.z; Kf[4 * i + 3] = x.w;
-            }
-#pragma unroll
-            for (int i = 0; i < SS::NFA / 4; i++) {
-                const float4 x = pa[i * OMH_WAVE];
-                Af[4 * i] = x.x; Af[4 * i + 1] = x.y; Af[4 * i + 2] = x.z; Af[4 * i + 3] = x.w;
-            }
-#pragma unroll
-            for (int i = 0; i < SS::NFU / 4; i++) {
-                const float4 x = pu[i * OMH_WAVE];
-                Uf[4 * i] = x.x; Uf[4 * i + 1] = x.y; Uf[4 * i + 2] = x.z; Uf[4 * i + 3] = x.w;
-            }
-        }
-        const float eg = a.glast[hc];
-
-        // partial W S and (Q e^gc) S over this wave's kd rows, all token tiles
-        v4f P[4], O[4];
+    auto step = [&](const ScanIn<D> &f, int c) {
+        // partial W S and (Q e^gc) S over this wave's 16 kd rows, all token tiles
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
-            P[tt] = v4zero(); O[tt] = v4zero();
+            v4f P = v4zero(), O = v4zero();
 #pragma unroll
-            for (int kt = 0; kt < KT; kt++)
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    P[tt] = mfma4(Wf[(tt * KT + kt) * 4 + s], S[kt][s], P[tt]);
-                    O[tt] = mfma4(Qf[(tt * KT + kt) * 4 + s], S[kt][s], O[tt]);
-                }
-            s_p[w][tt][lane] = P[tt];
-            s_o[w][tt][lane] = O[tt];
+            for (int s = 0; s < 4; s++) {
+                P = mfma4(f.Wf[tt * 4 + s], S[s], P);
+                O = mfma4(f.Qf[tt * 4 + s], S[s], O);
+            }
+            s_p[w][tt][lane] = P;
+            s_o[w][tt][lane] = O;
         }
-        __syncthreads();
-        // reduce over waves for the owned token tiles; v_new = U - W S
-        v4f Oa[TT];
+        omh_lds_barrier();
+        // reductions over the waves: v_new = U - W S (kind 0), o (kind 1)
+        v4f Oa[JPW];
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            const int mt = w * TT + u;
-            v4f p = s_p[0][mt][lane], o = s_o[0][mt][lane];
+        for (int jj = 0; jj < JPW; jj++) {
+            const int job = w + jj * NWV, mt = job % 4;
+            if (job < 4) {
+                v4f p = s_p[0][mt][lane];
 #pragma unroll
-            for (int ww = 1; ww < NWV; ww++) { p += s_p[ww][mt][lane]; o += s_o[ww][mt][lane]; }
-            v4f vn;
+                for (int ww = 1; ww < NWV; ww++) p += s_p[ww][mt][lane];
+                v4f vn;
 #pragma unroll
-            for (int r = 0; r < 4; r++) vn[r] = Uf[u * 4 + r] - p[r];
-            s_vn[mt][lane] = vn;
-            Oa[u] = o;
+                for (int r = 0; r < 4; r++) vn[r] = f.Uf[jj][r] - p[r];
+                s_vn[mt][lane] = vn;
+            } else {
+                v4f o = s_o[0][mt][lane];
+#pragma unroll
+                for (int ww = 1; ww < NWV; ww++) o += s_o[ww][mt][lane];
+                Oa[jj] = o;
+            }
         }
-        __syncthreads();
+        omh_lds_barrier();
         v4f VN[4];
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) VN[tt] = s_vn[tt][lane];
-        // o += Aqk v_new (causal: key tiles <= query tile)
+        // o += Aqk v_new (causal: key tiles <= query tile), then the raw
+        // output rows 16mt + 4g + r of this chunk
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            const int mt = w * TT + u;
+        for (int jj = 0; jj < JPW; jj++) {
+            const int job = w + jj * NWV, mt = job % 4;
+            if (job >= 4) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-                if (kt <= mt)
+                for (int kt = 0; kt < 4; kt++)
+                    if (kt <= mt)
 #pragma unroll
-                    for (int s = 0; s < 4; s++) Oa[u] = mfma4(Af[u * 16 + kt * 4 + s], VN[kt][s], Oa[u]);
-            // raw output rows 16mt + 4g + r of this chunk
+                        for (int s = 0; s < 4; s++) Oa[jj] = mfma4(f.Af[jj][kt * 4 + s], VN[kt][s], Oa[jj]);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = c * C + 16 * mt + 4 * g4 + r;
-                if (t < a.T) a.core[(size_t)t * vdim + (size_t)h * D + 16 * cb + l16] = Oa[u][r];
+                for (int r = 0; r < 4; r++) {
+                    const int t = c * C + 16 * mt + 4 * g4 + r;
+                    if (t < a.T) a.core[(size_t)t * vdim + (size_t)h * D + 16 * cb + l16] = Oa[jj][r];
+                }
             }
         }
         // S <- e^{gl} S + (K e^{gl-gc})^T v_new
+        S *= f.eg;
 #pragma unroll
-        for (int kt = 0; kt < KT; kt++) {
-            S[kt] *= eg;
+        for (int tt = 0; tt < 4; tt++)
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int s = 0; s < 4; s++) S[kt] = mfma4(Kf[(kt * 4 + tt) * 4 + s], VN[tt][s], S[kt]);
+            for (int s = 0; s < 4; s++) S = mfma4(f.Kf[tt * 4 + s], VN[tt][s], S);
+    };
+
+    const int nc = a.nc;
+    ScanIn<D> f0, f1;
+    f0.load(a, h, cb, 0, w, lane);
+    for (int c = 0; c < nc; c += 2) {
+        f1.load(a, h, cb, min(c + 1, nc - 1), w, lane);
+        step(f0, c);
+        if (c + 1 < nc) {
+            f0.load(a, h, cb, min(c + 2, nc - 1), w, lane);
+            step(f1, c + 1);
         }
     }
 #pragma unroll
-    for (int kt = 0; kt < KT; kt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            Sbase[(size_t)(16 * (w * KT + kt) + 4 * g4 + r) * D + 16 * cb + l16] = S[kt][r];
+    for (int r = 0; r < 4; r++) Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16] = S[r];
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Workgroups of the persistent WY kernel: the device's CU count.
+int wy_grid() {
+    static int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+            cus = 256;
+        return cus - cus % 8;
+    }();
+    return n;
+}
+
 template <int D>
 hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     const int conv_dim = 2 * a.kh * D + a.vh * D;
-    hipLaunchKernelGGL((prefill_prep_kernel<D>), dim3(2 * a.kh + a.vh, a.nc), dim3(D < 64 ? 64 : D), 0, st, a);
+    // the WY kernel reads the ring for chunk 0 before the commit rewrites it
+    // persistent: one workgroup per CU (the LDS footprint allows one), a
+    // multiple of 8 so the XCD-aware item order holds
+    const int nitems = a.vh * a.nc;
+    const int grid = nitems < wy_grid() ? nitems : wy_grid();
+    hipLaunchKernelGGL((prefill_wy_kernel<D>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     hipLaunchKernelGGL(prefill_conv_commit_kernel, dim3((conv_dim + 255) / 256), dim3(256), 0, st, a, conv_dim);
-    const size_t lds = (size_t)(3 * C * (D + 4) + 2 * C * (C + 4) + 2 * C) * sizeof(float);
-    hipLaunchKernelGGL((prefill_chunk_kernel<D>), dim3(a.vh, a.nc), dim3(256), lds, st, a);
     hipLaunchKernelGGL((prefill_scan_kernel<D>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
     constexpr int RPB = 256 / (D / 4);
     const size_t rows = (size_t)a.T * a.vh;
@@ -522,20 +678,16 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
 
 template <int D>
 bool set_lds_limit() {
-    const size_t lds = (size_t)(3 * C * (D + 4) + 2 * C * (C + 4) + 2 * C) * sizeof(float);
-    return hipFuncSetAttribute((const void *)prefill_chunk_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)lds) == hipSuccess;
+    return hipFuncSetAttribute((const void *)prefill_wy_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)WyShape<D>::LDS) == hipSuccess;
 }
 
 }  // namespace
 
 size_t prefill_scratch_bytes(int D, int kh, int vh, int T) {
+    (void)kh;
     const size_t Tp = (size_t)((T + C - 1) / C) * C, nc = Tp / C;
     size_t n = 0;
-    n += 2 * align256((size_t)kh * Tp * D * 4);            // qn, kn
-    n += align256((size_t)vh * Tp * D * 4);                // v
-    n += 2 * align256((size_t)vh * Tp * 4);                // g, beta
-    n += align256((size_t)vh * Tp * 4);                    // gc (reserved)
     n += align256((size_t)vh * nc * 4);                    // glast
     n += 3 * align256((size_t)vh * Tp * D * 4);            // pw, pq, pk
     n += align256((size_t)vh * nc * C * C * 4);            // pa
@@ -547,12 +699,6 @@ void prefill_bind_scratch(PrefillArgs &a, int D, void *base) {
     const size_t Tp = (size_t)a.Tp, nc = (size_t)a.nc;
     char *p = static_cast<char *>(base);
     auto take = [&](size_t bytes) { float *r = reinterpret_cast<float *>(p); p += align256(bytes); return r; };
-    a.qn = take((size_t)a.kh * Tp * D * 4);
-    a.kn = take((size_t)a.kh * Tp * D * 4);
-    a.v = take((size_t)a.vh * Tp * D * 4);
-    a.g = take((size_t)a.vh * Tp * 4);
-    a.beta = take((size_t)a.vh * Tp * 4);
-    a.gc = take((size_t)a.vh * Tp * 4);
     a.glast = take((size_t)a.vh * nc * 4);
     a.pw = take((size_t)a.vh * Tp * D * 4);
     a.pq = take((size_t)a.vh * Tp * D * 4);

@@ -10,6 +10,9 @@
 __device__ __forceinline__ float omh_sigmoid(float z) { return 1.f / (1.f + expf(-z)); }
 __device__ __forceinline__ float omh_silu(float z) { return z * omh_sigmoid(z); }
 __device__ __forceinline__ float omh_softplus(float z) { return z > 20.f ? z : log1pf(expf(z)); }
+// SiLU with the hardware exp2 and reciprocal (a few ulp; used where it is
+// evaluated for every channel of every token of a prefill chunk).
+__device__ __forceinline__ float omh_silu_fast(float z) { return z * __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
 
 // Workgroup barrier that orders LDS only: outstanding global loads stay in
 // flight across it (a plain __syncthreads also drains them).  Correct
@@ -32,6 +35,18 @@ template <int HI>
 __device__ __forceinline__ float omh_xor_sum_below(float v) {
 #pragma unroll
     for (int off = 1; off < HI; off <<= 1) v += __shfl_xor(v, off, OMH_WAVE);
+    return v;
+}
+
+// Sum over aligned groups of N = 1, 2 or 4 consecutive lanes (DPP quad
+// permutes: no LDS round trip).
+template <int N>
+__device__ __forceinline__ float omh_group_sum(float v) {
+    static_assert(N == 1 || N == 2 || N == 4, "lane group");
+    if constexpr (N >= 2)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    if constexpr (N >= 4)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
     return v;
 }
 

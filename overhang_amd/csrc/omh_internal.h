@@ -94,8 +94,7 @@ struct PrefillArgs {
     int kh, vh, K;
     float eps;
     // scratch (device), sized by prefill_scratch_bytes()
-    float *qn, *kn, *v, *g, *beta;       // head-major P1 outputs
-    float *gc, *glast;                   // cumulative log-decay [vh][Tp], exp(g_last) [vh][nc]
+    float *glast;                        // exp(cumulative log-decay at chunk end) [vh][nc]
     float *pw, *pq, *pk, *pa, *pu;       // per-chunk operand panels for the scan
 };
 size_t prefill_scratch_bytes(int D, int kh, int vh, int T);
