@@ -7,17 +7,18 @@
 //     L  = strict_lower(beta_i k_i.k_j exp(gc_i - gc_j)),   X = (I + L)^-1
 //     W  = X (K * beta * e^gc),   U = X (V * beta)
 //     Aqk = lower_incl_diag(q_i.k_j exp(gc_i - gc_j))
-//     v_new = U - W S;   o = (Q * e^gc) S + Aqk v_new
+//     v_new = U - W S;   o = (Q * e^gc) S + Aqk v_new   (S = the chunk's starting state)
 //     S <- e^{gc_last} S + (K * e^{gc_last - gc})^T v_new
 // Only exp of differences of cumulative decays are formed, never exp(-gc).
 //
 // Four launches, all on the caller's stream:
 //   P1 wy      per (value head, chunk): conv + SiLU, q/k L2 norm, gates,
-//              KK^T, QK^T, X, W, U on fp32 MFMA, written as per-lane
-//              fragment panels for P3                              MFMA-bound
+//              KK^T, QK^T, (I+L)^-1 blocks, W, U on fp32 MFMA, written as
+//              per-lane fragment panels                            MFMA-bound
 //   P2 commit  conv history ring -> last K-1 inputs, new phase     tiny
-//   P3 scan    per (value head, 16-column block): the chunk recurrence,
-//              sequential over chunks, on fp32 MFMA                MFMA-bound
+//   P3 scan    per (value head, 16-column block of S): the chunk
+//              recurrence and the raw outputs, sequential over chunks, on
+//              fp32 MFMA                                           MFMA-bound
 //   P4 norm    gated RMSNorm of the head outputs                   HBM-bound
 //
 // MFMA conventions (v_mfma_f32_16x16x4_f32, lane l, g = l / 16):
@@ -41,24 +42,29 @@ __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
 }
 __device__ __forceinline__ v4f v4zero() { v4f z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
-// Scan work split for head dim D: NWV = D/16 waves per workgroup; wave w
-// owns row tile w (16 kd rows) of the workgroup's 128 x 16 slice of S.  The
-// eight per-chunk reductions (v_new and o for the chunk's 4 token tiles)
-// are jobs j = 0..7 (kind j / 4, token tile j % 4), job j on wave j % NWV.
+// Scan work split for head dim D: eight waves per workgroup, which owns a
+// D x 16 column slice of S; wave w < NST = D/16 holds row tile w (16 kd
+// rows) in registers.  Per chunk, waves 0-3 form v_new of token tile w
+// (W S over all of kd) and waves 4-7 the output of token tile w - 4.
 // Panels, per lane, in MFMA fragment order (the WY kernel writes them):
-//   W, Q e^gc   per (head, chunk, wave w): f = tt*4 + s -> row 16tt + l%16, col 16w + 4g + s
-//   (K e^{gl-gc})^T  same index: f = tt*4 + s -> row 16tt + 4g + s, col 16w + l%16
+//   W, Q e^gc   per (head, chunk, token tile j): f = kt*4 + s -> row 16j + l%16, col 16kt + 4g + s
+//   (K e^{gl-gc})^T  per (head, chunk, row tile w): f = tt*4 + s -> row 16tt + 4g + s, col 16w + l%16
 //   Aqk         per (head, chunk, token tile mt): f = kt*4 + s -> row 16mt + l%16, col 16kt + 4g + s
 //   U           per (head, chunk, column block cb, mt): f = r -> row 16mt + 4g + r, col 16cb + l%16
 // (g = l / 16); each group of four consecutive f is one float4 per lane.
 template <int D>
 struct ScanShape {
-    static constexpr int NWV = D / 16;
-    static constexpr int JPW = NWV >= 8 ? 1 : 8 / NWV;    // reduction jobs per wave
-    static_assert(NWV >= 1 && NWV <= 8, "scan split");
+    static constexpr int NST = D / 16;          // S row tiles
+    static constexpr int NWV = 8;
+    static_assert(NST >= 1 && NST <= NWV, "scan split");
 };
 // float4 index of panel group f4 of lane l in block `blk` (4 groups per block)
 __device__ __forceinline__ size_t pan4(size_t blk, int f4, int l) { return ((blk * 4 + f4) * OMH_WAVE + l) * 4; }
+// W / Q e^gc panels: group kt of token tile j (NST groups per tile)
+template <int D>
+__device__ __forceinline__ size_t panj(size_t hc, int j, int kt, int l) {
+    return (((hc * 4 + j) * (D / 16) + kt) * OMH_WAVE + l) * 4;
+}
 
 // ---------------------------------------------------------------- P2 commit
 // New conv history = last K-1 entries of [old history, x_0 .. x_{T-1}],
@@ -116,12 +122,6 @@ void prefill_gated_norm_kernel(const PrefillArgs a) {
     y.z = o.z * rn * gn.z * omh_silu(zz.z);
     y.w = o.w * rn * gn.w * omh_silu(zz.w);
     *reinterpret_cast<float4 *>(op) = y;
-}
-
-// Panel addressing: frag f of lane l of wave w, in float4 groups so that a
-// wave's consecutive lanes read consecutive 16 B.
-__device__ __forceinline__ size_t panel_idx(size_t base4, int f, int l) {
-    return ((base4 + (size_t)(f >> 2)) * OMH_WAVE + l) * 4 + (f & 3);
 }
 
 // ---------------------------------------------------------------- P1 WY
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(WyShape<D>::NT)
 void prefill_wy_kernel(const PrefillArgs a) {
     using WS = WyShape<D>;
     constexpr int NW = WS::NW, NT = WS::NT, PD = WS::PD, PC = WS::PC, NCT = WS::NCT;
-    constexpr int NWV = ScanShape<D>::NWV;
+    constexpr int NST = ScanShape<D>::NST;
 
     const int kh = a.kh, rep = a.vh / kh, K = a.K, T = a.T;
     const int nitems = a.vh * a.nc;
@@ -413,8 +413,8 @@ void prefill_wy_kernel(const PrefillArgs a) {
             constexpr int PW = NW > 4 ? NW - 4 : NW;         // panel-writing waves
             const int pw_t = NW > 4 ? tid - 4 * OMH_WAVE : tid;
             if (pw_t >= 0) {
-                // Q/K panels: NWV scan waves x 4 token tiles x 64 lanes
-                for (int e = pw_t; e < NWV * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
+                // Q/K panels: NST kd tiles x 4 token tiles x 64 lanes
+                for (int e = pw_t; e < NST * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
                     const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
                     const int ll16 = l % 16, lg = l / 16;
                     const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
@@ -422,8 +422,8 @@ void prefill_wy_kernel(const PrefillArgs a) {
                     const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
                     const float4 vk = make_float4(Ks[rk * PD + ck] * egl[rk], Ks[(rk + 1) * PD + ck] * egl[rk + 1],
                                                   Ks[(rk + 2) * PD + ck] * egl[rk + 2], Ks[(rk + 3) * PD + ck] * egl[rk + 3]);
-                    *reinterpret_cast<float4 *>(a.pq + pan4(hc * NWV + w, tt, l)) = vq;
-                    *reinterpret_cast<float4 *>(a.pk + pan4(hc * NWV + w, tt, l)) = vk;
+                    *reinterpret_cast<float4 *>(a.pq + panj<D>(hc, tt, w, l)) = vq;
+                    *reinterpret_cast<float4 *>(a.pk + pan4(hc * NST + w, tt, l)) = vk;
                 }
                 for (int e = pw_t; e < 16 * OMH_WAVE; e += PW * OMH_WAVE) {
                     const int l = e % OMH_WAVE, kt = (e / OMH_WAVE) % 4, mt = e / (4 * OMH_WAVE);
@@ -489,10 +489,10 @@ void prefill_wy_kernel(const PrefillArgs a) {
         omh_lds_barrier();
 
         // 6. W panel (the Q panel's order)
-        for (int e = tid; e < NWV * 4 * OMH_WAVE; e += NT) {
+        for (int e = tid; e < NST * 4 * OMH_WAVE; e += NT) {
             const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
             const int row = tt * 16 + l % 16, col = 16 * w + 4 * (l / 16);
-            *reinterpret_cast<float4 *>(a.pw + pan4(hc * NWV + w, tt, l)) =
+            *reinterpret_cast<float4 *>(a.pw + panj<D>(hc, tt, w, l)) =
                 *reinterpret_cast<const float4 *>(Qs + row * PD + col);
         }
         omh_lds_barrier();                       // LDS is reused by the next item
@@ -500,50 +500,121 @@ void prefill_wy_kernel(const PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- P3 scan
-// One chunk's operands for one scan wave, in MFMA fragment order.
-template <int D>
+// One chunk's operands for one scan wave, in MFMA fragment order: for a
+// v_new wave (V = true) the W and U tiles of its token tile, for an output
+// wave the Q e^gc and Aqk tiles; for both the (K e^{gl-gc})^T row tile of
+// the S tile the wave holds, and e^{gl}.
+template <int D, bool V>
 struct ScanIn {
-    static constexpr int JPW = ScanShape<D>::JPW;
-    float Wf[16], Qf[16], Kf[16], Af[JPW][16], Uf[JPW][4];
-    float eg;
+    static constexpr int NST = ScanShape<D>::NST;
+    static constexpr int NX = V ? 4 : 16;
+    float Mf[4 * NST];   // W or Q e^gc, token tile w % 4
+    float Xf[NX];        // U tile (D layout) or Aqk row tile
+    float Kf[16];        // (K e^{gl-gc})^T of row tile w
+    float eg;            // e^{gl}
 
-    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int cb, int c, int w, int lane) {
-        constexpr int NWV = ScanShape<D>::NWV, NCB = D / 16;
+    // eg comes through a buffer load (a vector load at a uniform offset): a
+    // scalar load would share lgkmcnt with the LDS reads and hold them up.
+    __device__ __forceinline__ void load(const PrefillArgs &a, __amdgpu_buffer_rsrc_t grs, int h, int cb, int c, int w,
+                                         int lane) {
+        constexpr int NCB = D / 16;
         const size_t hc = (size_t)h * a.nc + c;
+        const int j = w & 3;
+        const float *mp = (V ? a.pw : a.pq) + panj<D>(hc, j, 0, lane);
+#pragma unroll
+        for (int kt = 0; kt < NST; kt++) {
+            const float4 x = *reinterpret_cast<const float4 *>(mp + kt * OMH_WAVE * 4);
+            Mf[4 * kt] = x.x; Mf[4 * kt + 1] = x.y; Mf[4 * kt + 2] = x.z; Mf[4 * kt + 3] = x.w;
+        }
+        const float *xp = V ? a.pu + pan4(hc * NCB + cb, j, lane) : a.pa + pan4(hc * 4 + j, 0, lane);
+#pragma unroll
+        for (int kt = 0; kt < NX / 4; kt++) {
+            const float4 x = *reinterpret_cast<const float4 *>(xp + kt * OMH_WAVE * 4);
+            Xf[4 * kt] = x.x; Xf[4 * kt + 1] = x.y; Xf[4 * kt + 2] = x.z; Xf[4 * kt + 3] = x.w;
+        }
+        const float *kp = a.pk + pan4(hc * NST + (w < NST ? w : NST - 1), 0, lane);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
-            const float4 x = *reinterpret_cast<const float4 *>(a.pw + pan4(hc * NWV + w, tt, lane));
-            const float4 y = *reinterpret_cast<const float4 *>(a.pq + pan4(hc * NWV + w, tt, lane));
-            const float4 z = *reinterpret_cast<const float4 *>(a.pk + pan4(hc * NWV + w, tt, lane));
-            Wf[4 * tt] = x.x; Wf[4 * tt + 1] = x.y; Wf[4 * tt + 2] = x.z; Wf[4 * tt + 3] = x.w;
-            Qf[4 * tt] = y.x; Qf[4 * tt + 1] = y.y; Qf[4 * tt + 2] = y.z; Qf[4 * tt + 3] = y.w;
-            Kf[4 * tt] = z.x; Kf[4 * tt + 1] = z.y; Kf[4 * tt + 2] = z.z; Kf[4 * tt + 3] = z.w;
+            const float4 x = *reinterpret_cast<const float4 *>(kp + tt * OMH_WAVE * 4);
+            Kf[4 * tt] = x.x; Kf[4 * tt + 1] = x.y; Kf[4 * tt + 2] = x.z; Kf[4 * tt + 3] = x.w;
         }
-#pragma unroll
-        for (int jj = 0; jj < JPW; jj++) {
-            const int mt = (w + jj * NWV) % 4;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                const float4 x = *reinterpret_cast<const float4 *>(a.pa + pan4(hc * 4 + mt, kt, lane));
-                Af[jj][4 * kt] = x.x; Af[jj][4 * kt + 1] = x.y; Af[jj][4 * kt + 2] = x.z; Af[jj][4 * kt + 3] = x.w;
-            }
-            const float4 u = *reinterpret_cast<const float4 *>(a.pu + pan4(hc * NCB + cb, mt, lane));
-            Uf[jj][0] = u.x; Uf[jj][1] = u.y; Uf[jj][2] = u.z; Uf[jj][3] = u.w;
-        }
-        eg = a.glast[hc];
+        eg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(grs, 0, (int)(hc * 4), 0));
     }
 };
 
+// LDS of one scan workgroup
+template <int D>
+struct ScanLds {
+    v4f S[2][ScanShape<D>::NST][OMH_WAVE];   // S row tiles at the start of a chunk, by chunk parity
+    v4f V[4][OMH_WAVE];                      // v_new token tiles
+};
+
+// S <- e^{gl} S + (K e^{gl-gc})^T v_new for the wave's row tile (two chains)
+template <int D, bool V>
+__device__ __forceinline__ void scan_update_s(const ScanIn<D, V> &f, const v4f (&VN)[4], v4f &S) {
+    v4f S2 = v4zero();
+    S *= f.eg;
+#pragma unroll
+    for (int tt = 0; tt < 4; tt += 2)
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            S = mfma4(f.Kf[tt * 4 + s], VN[tt][s], S);
+            S2 = mfma4(f.Kf[(tt + 1) * 4 + s], VN[tt + 1][s], S2);
+        }
+    S += S2;
+}
+
+// (token tile) x S over all of kd: the B operand of k-step (kt, s) is
+// register s of S row tile kt (D layout), read from LDS; two chains
+template <int D, bool V>
+__device__ __forceinline__ void scan_times_s(const ScanIn<D, V> &f, const v4f (&Ss)[ScanShape<D>::NST][OMH_WAVE], int lane,
+                                             v4f &P0, v4f &P1) {
+#pragma unroll
+    for (int kt = 0; kt < ScanShape<D>::NST; kt++) {
+        const v4f sf = Ss[kt][lane];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            if (kt & 1) P1 = mfma4(f.Mf[kt * 4 + s], sf[s], P1);
+            else P0 = mfma4(f.Mf[kt * 4 + s], sf[s], P0);
+        }
+    }
+}
+
+// Instruction order for a product over NST row tiles with the next chunk's
+// NL loads spread over its MFMAs (the L1 return path is then busy while
+// the matrix cores are, instead of every wave queueing its loads at once).
+template <int NST, int NL>
+__device__ __forceinline__ void scan_interleave() {
+    constexpr int PER = (NL + NST - 1) / NST;
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);        // first S tiles
+#pragma unroll
+    for (int kt = 0; kt < NST; kt++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);    // 4 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // loads
+        if (kt + 2 < NST) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+}
+
 // Per (value head, 16-column block of S): the chunk recurrence, S held in
-// registers (MFMA D layout) for the whole sequence, one 16-row tile per
-// wave.  The next chunk's operands are in flight while the current one is
-// processed (two register sets), and the workgroup barriers order LDS only,
-// so they do not wait for those loads or for the output stores.
+// registers (MFMA D layout, one 16-row tile per wave w < D/16) for the whole
+// sequence.  Per chunk c, between two barriers:
+//   1. every S row tile is in LDS (S[c & 1]); waves 0-3 each form v_new =
+//      U - W S for one token tile, contracting over all of kd, into V;
+//   2. every wave reads the four v_new tiles and updates its S tile,
+//      S <- e^{gl} S + (K e^{gl-gc})^T v_new, writing it to S[(c + 1) & 1];
+//      waves 4-7 then form the output of one token tile from the old S
+//      (still in S[c & 1]): o = (Q e^gc) S + Aqk v_new over all key tiles
+//      (the panel's tiles above the diagonal are zero).
+// No partial sums cross waves; the S tiles alternate between chunks, so an
+// output wave can still read chunk c's S while chunk c + 1's is written.
+// The two roles run separate loops with the same barriers.  Each loads the
+// next chunk's operands (a second register set) during its own products;
+// an output tile is stored after those loads, so waiting for operands never
+// waits for stores.
 template <int D>
 __global__ __launch_bounds__((ScanShape<D>::NWV * OMH_WAVE), 1)
 void prefill_scan_kernel(const PrefillArgs a) {
-    using SS = ScanShape<D>;
-    constexpr int NWV = SS::NWV, JPW = SS::JPW;
+    constexpr int NST = ScanShape<D>::NST;
     constexpr int NCB = D / 16;
     const int vh = a.vh;
     // XCD-aware: the NCB column blocks of a head share one XCD (and its L2)
@@ -553,97 +624,99 @@ void prefill_scan_kernel(const PrefillArgs a) {
         if (vh % 8 == 0) { h = (n % 8) + 8 * (n / (8 * NCB)); cb = (n / 8) % NCB; }
         else { h = n / NCB; cb = n % NCB; }
     }
-    const int tid = threadIdx.x, lane = tid % OMH_WAVE, w = tid / OMH_WAVE;
+    const int lane = threadIdx.x % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
     const int l16 = lane % 16, g4 = lane / 16;
+    const int j = w & 3;                 // token tile of the wave's job
+    const bool owns = w < NST;           // holds S row tile w
+    const int nc = a.nc;
+    const __amdgpu_buffer_rsrc_t grs =
+        __builtin_amdgcn_make_buffer_rsrc(a.glast, 0, (int)((size_t)vh * nc * sizeof(float)), 0x00020000);
 
-    __shared__ v4f s_p[NWV][4][OMH_WAVE];        // W S partials per wave, token tile
-    __shared__ v4f s_o[NWV][4][OMH_WAVE];        // (Q e^gc) S partials
-    __shared__ v4f s_vn[4][OMH_WAVE];            // v_new tiles (D layout)
+    __shared__ ScanLds<D> sm;
 
     // S rows 16w + 4g + r, column 16cb + l%16
     float *Sbase = a.L.S + ((size_t)a.seq * vh + h) * (D * D);
-    v4f S;
+    v4f S = v4zero();
+    if (owns) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) S[r] = Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16];
+        for (int r = 0; r < 4; r++) S[r] = Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16];
+        sm.S[0][w][lane] = S;
+    }
 
-    const size_t vdim = (size_t)vh * D;
-    auto step = [&](const ScanIn<D> &f, int c) {
-        // partial W S and (Q e^gc) S over this wave's 16 kd rows, all token tiles
+    if (w < 4) {
+        // v_new waves
+        typedef ScanIn<D, true> In;
+        auto step = [&](const In &f, In &fn, int c) {
+            const int pb = c & 1;
+            omh_lds_barrier();                   // S[pb] holds chunk c's S; V is free
+            fn.load(a, grs, h, cb, min(c + 1, nc - 1), w, lane);
+            v4f P0 = v4zero(), P1 = v4zero();
+            scan_times_s<D, true>(f, sm.S[pb], lane, P0, P1);
+            scan_interleave<NST, 4 * NST / 4 + 1 + 4 + 1>();
+            v4f vn;
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            v4f P = v4zero(), O = v4zero();
+            for (int r = 0; r < 4; r++) vn[r] = f.Xf[r] - (P0[r] + P1[r]);
+            sm.V[j][lane] = vn;
+            omh_lds_barrier();                   // V holds chunk c's v_new
+            if (owns) {
+                v4f VN[4];
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                P = mfma4(f.Wf[tt * 4 + s], S[s], P);
-                O = mfma4(f.Qf[tt * 4 + s], S[s], O);
+                for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
+                scan_update_s<D, true>(f, VN, S);
+                sm.S[pb ^ 1][w][lane] = S;
             }
-            s_p[w][tt][lane] = P;
-            s_o[w][tt][lane] = O;
+        };
+        In f0, f1;
+        f0.load(a, grs, h, cb, 0, w, lane);
+        for (int c = 0; c < nc; c += 2) {
+            step(f0, f1, c);
+            if (c + 1 < nc) step(f1, f0, c + 1);
         }
-        omh_lds_barrier();
-        // reductions over the waves: v_new = U - W S (kind 0), o (kind 1)
-        v4f Oa[JPW];
+    } else {
+        // output waves
+        typedef ScanIn<D, false> In;
+        float *obase = a.core + (size_t)h * D + 16 * cb + l16;
+        const size_t vdim = (size_t)vh * D;
+        auto step = [&](const In &f, In &fn, int c) {
+            const int pb = c & 1;
+            omh_lds_barrier();                   // S[pb] holds chunk c's S; V is free
+            omh_lds_barrier();                   // V holds chunk c's v_new
+            v4f VN[4];
 #pragma unroll
-        for (int jj = 0; jj < JPW; jj++) {
-            const int job = w + jj * NWV, mt = job % 4;
-            if (job < 4) {
-                v4f p = s_p[0][mt][lane];
-#pragma unroll
-                for (int ww = 1; ww < NWV; ww++) p += s_p[ww][mt][lane];
-                v4f vn;
-#pragma unroll
-                for (int r = 0; r < 4; r++) vn[r] = f.Uf[jj][r] - p[r];
-                s_vn[mt][lane] = vn;
-            } else {
-                v4f o = s_o[0][mt][lane];
-#pragma unroll
-                for (int ww = 1; ww < NWV; ww++) o += s_o[ww][mt][lane];
-                Oa[jj] = o;
+            for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
+            if (owns) {
+                scan_update_s<D, false>(f, VN, S);
+                sm.S[pb ^ 1][w][lane] = S;
             }
-        }
-        omh_lds_barrier();
-        v4f VN[4];
+            fn.load(a, grs, h, cb, min(c + 1, nc - 1), w, lane);
+            v4f O0 = v4zero(), O1 = v4zero();
+            scan_times_s<D, false>(f, sm.S[pb], lane, O0, O1);
+            scan_interleave<NST, 4 * NST / 4 + 4 + 4 + 1>();
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) VN[tt] = s_vn[tt][lane];
-        // o += Aqk v_new (causal: key tiles <= query tile), then the raw
-        // output rows 16mt + 4g + r of this chunk
+            for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-        for (int jj = 0; jj < JPW; jj++) {
-            const int job = w + jj * NWV, mt = job % 4;
-            if (job >= 4) {
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++)
-                    if (kt <= mt)
-#pragma unroll
-                        for (int s = 0; s < 4; s++) Oa[jj] = mfma4(f.Af[jj][kt * 4 + s], VN[kt][s], Oa[jj]);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int t = c * C + 16 * mt + 4 * g4 + r;
-                    if (t < a.T) a.core[(size_t)t * vdim + (size_t)h * D + 16 * cb + l16] = Oa[jj][r];
+                for (int s = 0; s < 4; s++) {
+                    if (kt & 1) O1 = mfma4(f.Xf[kt * 4 + s], VN[kt][s], O1);
+                    else O0 = mfma4(f.Xf[kt * 4 + s], VN[kt][s], O0);
                 }
+            const v4f o = O0 + O1;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = c * C + 16 * j + 4 * g4 + r;
+                if (t < a.T) obase[(size_t)t * vdim] = o[r];
             }
-        }
-        // S <- e^{gl} S + (K e^{gl-gc})^T v_new
-        S *= f.eg;
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int s = 0; s < 4; s++) S = mfma4(f.Kf[tt * 4 + s], VN[tt][s], S);
-    };
-
-    const int nc = a.nc;
-    ScanIn<D> f0, f1;
-    f0.load(a, h, cb, 0, w, lane);
-    for (int c = 0; c < nc; c += 2) {
-        f1.load(a, h, cb, min(c + 1, nc - 1), w, lane);
-        step(f0, c);
-        if (c + 1 < nc) {
-            f0.load(a, h, cb, min(c + 2, nc - 1), w, lane);
-            step(f1, c + 1);
+        };
+        In f0, f1;
+        f0.load(a, grs, h, cb, 0, w, lane);
+        for (int c = 0; c < nc; c += 2) {
+            step(f0, f1, c);
+            if (c + 1 < nc) step(f1, f0, c + 1);
         }
     }
+    if (owns)
 #pragma unroll
-    for (int r = 0; r < 4; r++) Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16] = S[r];
+        for (int r = 0; r < 4; r++) Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16] = S[r];
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -662,11 +735,11 @@ int wy_grid() {
 template <int D>
 hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     const int conv_dim = 2 * a.kh * D + a.vh * D;
-    // the WY kernel reads the ring for chunk 0 before the commit rewrites it
     // persistent: one workgroup per CU (the LDS footprint allows one), a
     // multiple of 8 so the XCD-aware item order holds
     const int nitems = a.vh * a.nc;
     const int grid = nitems < wy_grid() ? nitems : wy_grid();
+    // the WY kernel reads the ring for chunk 0 before the commit rewrites it
     hipLaunchKernelGGL((prefill_wy_kernel<D>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     hipLaunchKernelGGL(prefill_conv_commit_kernel, dim3((conv_dim + 255) / 256), dim3(256), 0, st, a, conv_dim);
     hipLaunchKernelGGL((prefill_scan_kernel<D>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);

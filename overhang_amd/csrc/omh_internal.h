@@ -95,7 +95,7 @@ struct PrefillArgs {
     float eps;
     // scratch (device), sized by prefill_scratch_bytes()
     float *glast;                        // exp(cumulative log-decay at chunk end) [vh][nc]
-    float *pw, *pq, *pk, *pa, *pu;       // per-chunk operand panels for the scan
+    float *pw, *pq, *pk, *pa, *pu;       // per-chunk operand panels (WY kernel -> scan)
 };
 size_t prefill_scratch_bytes(int D, int kh, int vh, int T);
 void prefill_bind_scratch(PrefillArgs &a, int D, void *base);
