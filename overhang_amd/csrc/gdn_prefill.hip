@@ -204,8 +204,8 @@ struct WyIn {
 
     __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_lane,
                                          int lane) {
-        const int kh = a.kh, vh = a.vh, K = a.K, T = a.T, t0 = c * C;
-        const int key_dim = kh * D, conv_dim = 2 * key_dim + vh * D;
+        const int kh = a.kh, K = a.K, T = a.T, t0 = c * C;
+        const int key_dim = kh * D;
 #pragma unroll
         for (int u = 0; u < NU; u++) {
             const int unit = tid + u * WyShape<D>::NT;
@@ -503,7 +503,8 @@ void prefill_wy_kernel(const PrefillArgs a) {
 // One chunk's operands for one scan wave, in MFMA fragment order: for a
 // v_new wave (V = true) the W and U tiles of its token tile, for an output
 // wave the Q e^gc and Aqk tiles; for both the (K e^{gl-gc})^T row tile of
-// the S tile the wave holds, and e^{gl}.
+// the S tile the wave holds, and e^{gl}.  Loaded in parts (load_m, load_x,
+// load_k) so each part can be spread over a different product.
 template <int D, bool V>
 struct ScanIn {
     static constexpr int NST = ScanShape<D>::NST;
@@ -513,25 +514,25 @@ struct ScanIn {
     float Kf[16];        // (K e^{gl-gc})^T of row tile w
     float eg;            // e^{gl}
 
-    // eg comes through a buffer load (a vector load at a uniform offset): a
-    // scalar load would share lgkmcnt with the LDS reads and hold them up.
-    __device__ __forceinline__ void load(const PrefillArgs &a, __amdgpu_buffer_rsrc_t grs, int h, int cb, int c, int w,
-                                         int lane) {
-        constexpr int NCB = D / 16;
-        const size_t hc = (size_t)h * a.nc + c;
-        const int j = w & 3;
-        const float *mp = (V ? a.pw : a.pq) + panj<D>(hc, j, 0, lane);
+    __device__ __forceinline__ void load_m(const PrefillArgs &a, size_t hc, int w, int lane) {
+        const float *mp = (V ? a.pw : a.pq) + panj<D>(hc, w & 3, 0, lane);
 #pragma unroll
         for (int kt = 0; kt < NST; kt++) {
             const float4 x = *reinterpret_cast<const float4 *>(mp + kt * OMH_WAVE * 4);
             Mf[4 * kt] = x.x; Mf[4 * kt + 1] = x.y; Mf[4 * kt + 2] = x.z; Mf[4 * kt + 3] = x.w;
         }
-        const float *xp = V ? a.pu + pan4(hc * NCB + cb, j, lane) : a.pa + pan4(hc * 4 + j, 0, lane);
+    }
+    __device__ __forceinline__ void load_x(const PrefillArgs &a, size_t hc, int cb, int w, int lane) {
+        const float *xp = V ? a.pu + pan4(hc * (D / 16) + cb, w & 3, lane) : a.pa + pan4(hc * 4 + (w & 3), 0, lane);
 #pragma unroll
         for (int kt = 0; kt < NX / 4; kt++) {
             const float4 x = *reinterpret_cast<const float4 *>(xp + kt * OMH_WAVE * 4);
             Xf[4 * kt] = x.x; Xf[4 * kt + 1] = x.y; Xf[4 * kt + 2] = x.z; Xf[4 * kt + 3] = x.w;
         }
+    }
+    // eg comes through a buffer load (a vector load at a uniform offset): a
+    // scalar load would share lgkmcnt with the LDS reads and hold them up.
+    __device__ __forceinline__ void load_k(const PrefillArgs &a, __amdgpu_buffer_rsrc_t grs, size_t hc, int w, int lane) {
         const float *kp = a.pk + pan4(hc * NST + (w < NST ? w : NST - 1), 0, lane);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
@@ -545,7 +546,7 @@ struct ScanIn {
 // LDS of one scan workgroup
 template <int D>
 struct ScanLds {
-    v4f S[2][ScanShape<D>::NST][OMH_WAVE];   // S row tiles at the start of a chunk, by chunk parity
+    v4f S[ScanShape<D>::NST][OMH_WAVE];      // S row tiles at the start of the chunk
     v4f V[4][OMH_WAVE];                      // v_new token tiles
 };
 
@@ -580,11 +581,12 @@ __device__ __forceinline__ void scan_times_s(const ScanIn<D, V> &f, const v4f (&
     }
 }
 
-// Instruction order for a product over NST row tiles with the next chunk's
-// NL loads spread over its MFMAs (the L1 return path is then busy while
-// the matrix cores are, instead of every wave queueing its loads at once).
+// Instruction order for a product over NST row tiles read from LDS, with NL
+// of the next chunk's loads spread over its MFMAs (the L1 return path then
+// works while the matrix cores do, instead of every wave queueing its loads
+// at once).
 template <int NST, int NL>
-__device__ __forceinline__ void scan_interleave() {
+__device__ __forceinline__ void scan_interleave_s() {
     constexpr int PER = (NL + NST - 1) / NST;
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);        // first S tiles
 #pragma unroll
@@ -594,23 +596,32 @@ __device__ __forceinline__ void scan_interleave() {
         if (kt + 2 < NST) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 }
+// NM MFMAs (operands in registers) with NL loads spread over them
+template <int NM, int NL>
+__device__ __forceinline__ void scan_interleave_r() {
+    constexpr int PER = (NM + NL - 1) / NL;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+}
 
 // Per (value head, 16-column block of S): the chunk recurrence, S held in
 // registers (MFMA D layout, one 16-row tile per wave w < D/16) for the whole
-// sequence.  Per chunk c, between two barriers:
-//   1. every S row tile is in LDS (S[c & 1]); waves 0-3 each form v_new =
-//      U - W S for one token tile, contracting over all of kd, into V;
-//   2. every wave reads the four v_new tiles and updates its S tile,
-//      S <- e^{gl} S + (K e^{gl-gc})^T v_new, writing it to S[(c + 1) & 1];
-//      waves 4-7 then form the output of one token tile from the old S
-//      (still in S[c & 1]): o = (Q e^gc) S + Aqk v_new over all key tiles
-//      (the panel's tiles above the diagonal are zero).
-// No partial sums cross waves; the S tiles alternate between chunks, so an
-// output wave can still read chunk c's S while chunk c + 1's is written.
-// The two roles run separate loops with the same barriers.  Each loads the
-// next chunk's operands (a second register set) during its own products;
-// an output tile is stored after those loads, so waiting for operands never
-// waits for stores.
+// sequence.  Per chunk, two barriers:
+//   B1: every S row tile of the chunk is in LDS.  Waves 0-3 each form
+//       v_new = U - W S for one token tile (contracting over all of kd) into
+//       LDS; waves 4-7 each form (Q e^gc) S for one token tile.
+//   B2: v_new is in LDS.  Every wave updates its S tile,
+//       S <- e^{gl} S + (K e^{gl-gc})^T v_new, and writes it to LDS for the
+//       next chunk; waves 4-7 add Aqk v_new over all key tiles (the panel's
+//       tiles above the diagonal are zero) to finish their output tile,
+//       which they store after the next B1.
+// Each matrix core then has 64 MFMAs before B2 (W S and Q S) and 48 after.
+// The two roles run separate loops with the same barriers; each loads the
+// next chunk's operands into a second register set, spread over its own
+// products.
 template <int D>
 __global__ __launch_bounds__((ScanShape<D>::NWV * OMH_WAVE), 1)
 void prefill_scan_kernel(const PrefillArgs a) {
@@ -630,6 +641,7 @@ void prefill_scan_kernel(const PrefillArgs a) {
     const int j = w & 3;                 // token tile of the wave's job
     const bool owns = w < NST;           // holds S row tile w
     const int nc = a.nc;
+    const size_t hc0 = (size_t)h * nc;
     const __amdgpu_buffer_rsrc_t grs =
         __builtin_amdgcn_make_buffer_rsrc(a.glast, 0, (int)((size_t)vh * nc * sizeof(float)), 0x00020000);
 
@@ -641,34 +653,39 @@ void prefill_scan_kernel(const PrefillArgs a) {
     if (owns) {
 #pragma unroll
         for (int r = 0; r < 4; r++) S[r] = Sbase[(size_t)(16 * w + 4 * g4 + r) * D + 16 * cb + l16];
-        sm.S[0][w][lane] = S;
+        sm.S[w][lane] = S;
     }
 
     if (w < 4) {
         // v_new waves
         typedef ScanIn<D, true> In;
         auto step = [&](const In &f, In &fn, int c) {
-            const int pb = c & 1;
-            omh_lds_barrier();                   // S[pb] holds chunk c's S; V is free
-            fn.load(a, grs, h, cb, min(c + 1, nc - 1), w, lane);
+            const size_t hn = hc0 + min(c + 1, nc - 1);
+            omh_lds_barrier();                   // B1: S tiles of chunk c
+            fn.load_m(a, hn, w, lane);
             v4f P0 = v4zero(), P1 = v4zero();
-            scan_times_s<D, true>(f, sm.S[pb], lane, P0, P1);
-            scan_interleave<NST, 4 * NST / 4 + 1 + 4 + 1>();
+            scan_times_s<D, true>(f, sm.S, lane, P0, P1);
+            scan_interleave_s<NST, NST>();
             v4f vn;
 #pragma unroll
             for (int r = 0; r < 4; r++) vn[r] = f.Xf[r] - (P0[r] + P1[r]);
             sm.V[j][lane] = vn;
-            omh_lds_barrier();                   // V holds chunk c's v_new
+            omh_lds_barrier();                   // B2: v_new of chunk c
+            fn.load_x(a, hn, cb, w, lane);
+            fn.load_k(a, grs, hn, w, lane);
             if (owns) {
                 v4f VN[4];
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
                 scan_update_s<D, true>(f, VN, S);
-                sm.S[pb ^ 1][w][lane] = S;
+                scan_interleave_r<16, 6>();
+                sm.S[w][lane] = S;
             }
         };
         In f0, f1;
-        f0.load(a, grs, h, cb, 0, w, lane);
+        f0.load_m(a, hc0, w, lane);
+        f0.load_x(a, hc0, cb, w, lane);
+        f0.load_k(a, grs, hc0, w, lane);
         for (int c = 0; c < nc; c += 2) {
             step(f0, f1, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
@@ -678,21 +695,32 @@ void prefill_scan_kernel(const PrefillArgs a) {
         typedef ScanIn<D, false> In;
         float *obase = a.core + (size_t)h * D + 16 * cb + l16;
         const size_t vdim = (size_t)vh * D;
+        v4f o = v4zero();
+        auto store = [&](int c) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int t = c * C + 16 * j + 4 * g4 + r;
+                if (t < a.T) obase[(size_t)t * vdim] = o[r];
+            }
+        };
         auto step = [&](const In &f, In &fn, int c) {
-            const int pb = c & 1;
-            omh_lds_barrier();                   // S[pb] holds chunk c's S; V is free
-            omh_lds_barrier();                   // V holds chunk c's v_new
+            const size_t hn = hc0 + min(c + 1, nc - 1);
+            omh_lds_barrier();                   // B1: S tiles of chunk c
+            if (c > 0) store(c - 1);
+            fn.load_m(a, hn, w, lane);
+            fn.load_x(a, hn, cb, w, lane);
+            v4f O0 = v4zero(), O1 = v4zero();
+            scan_times_s<D, false>(f, sm.S, lane, O0, O1);
+            scan_interleave_s<NST, NST + 4>();
+            omh_lds_barrier();                   // B2: v_new of chunk c
+            fn.load_k(a, grs, hn, w, lane);
             v4f VN[4];
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
             if (owns) {
                 scan_update_s<D, false>(f, VN, S);
-                sm.S[pb ^ 1][w][lane] = S;
+                sm.S[w][lane] = S;
             }
-            fn.load(a, grs, h, cb, min(c + 1, nc - 1), w, lane);
-            v4f O0 = v4zero(), O1 = v4zero();
-            scan_times_s<D, false>(f, sm.S[pb], lane, O0, O1);
-            scan_interleave<NST, 4 * NST / 4 + 4 + 4 + 1>();
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
@@ -700,19 +728,18 @@ void prefill_scan_kernel(const PrefillArgs a) {
                     if (kt & 1) O1 = mfma4(f.Xf[kt * 4 + s], VN[kt][s], O1);
                     else O0 = mfma4(f.Xf[kt * 4 + s], VN[kt][s], O0);
                 }
-            const v4f o = O0 + O1;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int t = c * C + 16 * j + 4 * g4 + r;
-                if (t < a.T) obase[(size_t)t * vdim] = o[r];
-            }
+            scan_interleave_r<32, 5>();
+            o = O0 + O1;
         };
         In f0, f1;
-        f0.load(a, grs, h, cb, 0, w, lane);
+        f0.load_m(a, hc0, w, lane);
+        f0.load_x(a, hc0, cb, w, lane);
+        f0.load_k(a, grs, hc0, w, lane);
         for (int c = 0; c < nc; c += 2) {
             step(f0, f1, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
         }
+        store(nc - 1);
     }
     if (owns)
 #pragma unroll

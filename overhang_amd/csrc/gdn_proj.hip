@@ -1,70 +1,314 @@
-// gdn_proj.hip — the layer's dense projections for few tokens (decode).
+// gdn_proj.hip — the layer's dense projections (in_proj and out_proj).
 //
 // y[t][o] = sum_i x[t][i] * W[o][i], with W either fp32 or int8 + per-row
 // scale (the engine's QW twins, engines/qwen.c:34, 94-122, 124-138:
-// dequantisation is acc * scale[o] after the fp32 dot product).  One
-// wavefront owns one output row: it streams the row once from HBM (float4
-// or 4 int8 per lane, fully coalesced) and applies it to the tokens in
-// register tiles of 8, so the weights are read from HBM once per launch.
-// The whole in_proj of a layer ([qkv | z] int8 + [b | a] fp32, or all fp32)
-// is one launch: rows below n_q use the int8 matrix, the rest the fp32 one.
+// dequantisation is acc * scale[o] after the fp32 dot product; the int8
+// values are exact in fp32, so the products are the reference's).  The
+// whole in_proj of a layer ([qkv | z] int8 + [b | a] fp32, or all fp32) is
+// one launch: rows below n_q use the int8 matrix, the rest the fp32 one
+// (n_q is a multiple of 16, so a 16-row tile is one or the other).
+//
+// Both kernels stream each weight row from HBM once per launch (the bound
+// for decode batches), with every lane reading 16 consecutive weights per
+// load (16 B of int8 or 64 B of fp32):
+//   * T <= 4 tokens: GEMV.  A wave takes 8 rows and one k-slice; lane l
+//     covers k = 1024c + 16l + e of it, with the 8 rows' weights in flight
+//     together; the 8 row sums are reduced over the lanes in one butterfly
+//     and the k-slices through LDS.
+//   * T > 4: fp32 MFMA (16x16x4), tokens x rows tiles.  Within a 64-wide
+//     k block, lane (l%16, g) holds x and W at k = 16g + 4j + s for its
+//     token / row l%16, so one 16-byte weight load and four float4 x loads
+//     feed 16 MFMAs (the k order is permuted identically on both operands).
+//     A workgroup is RT row tiles x KS k-slices (RT * KS = 4 waves); the
+//     k-slices are summed through LDS.
 #include "omh_device.h"
 #include "omh_internal.h"
 
 namespace omh {
 namespace {
 
-constexpr int kProjWaves = 4;
-constexpr int kProjTok = 8;
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(kProjWaves * OMH_WAVE)
-void proj_rows_kernel(const ProjArgs p) {
-    const int lane = threadIdx.x % OMH_WAVE;
-    const int o = blockIdx.x * kProjWaves + threadIdx.x / OMH_WAVE;
-    if (o >= p.O) return;
-    const bool q8 = o < p.n_q;
-    const int8_t *qrow = q8 ? p.Q + (size_t)o * p.I : nullptr;
-    const float *wrow = q8 ? nullptr : p.W + (size_t)(o - p.n_q) * p.I;
-    const float sc = q8 ? p.scale[o] : 1.f;
-    for (int t0 = 0; t0 < p.T; t0 += kProjTok) {
-        const int nt = min(kProjTok, p.T - t0);
-        float acc[kProjTok];
+// Weight fragment: 16 consecutive weights of one row, as loaded (int8 or
+// fp32) and as fp32.
+template <bool Q8>
+struct WFrag;
+template <>
+struct WFrag<true> {
+    int4 r;
+    __device__ __forceinline__ void load(const ProjArgs &p, int row, int k) {
+        r = *reinterpret_cast<const int4 *>(p.Q + (size_t)row * p.I + k);
+    }
+    // signed byte s = (u ^ 0x80) - 128 for its unsigned bits u: an
+    // unsigned-byte conversion and an exact subtraction.  (A signed bitfield
+    // extract followed by int->float is folded by this compiler into an SDWA
+    // unsigned conversion of the sign-extended byte, which turns -1 into
+    // 2^32 - 1.)
+    __device__ __forceinline__ void unpack(float (&w)[16]) const {
+        const unsigned v[4] = {(unsigned)r.x ^ 0x80808080u, (unsigned)r.y ^ 0x80808080u,
+                               (unsigned)r.z ^ 0x80808080u, (unsigned)r.w ^ 0x80808080u};
 #pragma unroll
-        for (int t = 0; t < kProjTok; t++) acc[t] = 0.f;
-        for (int i = lane * 4; i < p.I; i += OMH_WAVE * 4) {
-            float4 w;
-            if (q8) {
-                const char4 c = *reinterpret_cast<const char4 *>(qrow + i);
-                w = make_float4((float)c.x, (float)c.y, (float)c.z, (float)c.w);
-            } else {
-                w = *reinterpret_cast<const float4 *>(wrow + i);
-            }
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int t = 0; t < kProjTok; t++) {
-                if (t < nt) {
-                    const float4 xv = *reinterpret_cast<const float4 *>(p.x + (size_t)(t0 + t) * p.ldx + i);
-                    acc[t] = fmaf(xv.x, w.x, acc[t]);
-                    acc[t] = fmaf(xv.y, w.y, acc[t]);
-                    acc[t] = fmaf(xv.z, w.z, acc[t]);
-                    acc[t] = fmaf(xv.w, w.w, acc[t]);
-                }
+            for (int b = 0; b < 4; b++) w[4 * i + b] = (float)((v[i] >> (8 * b)) & 0xFFu) - 128.f;
+    }
+};
+template <>
+struct WFrag<false> {
+    float4 f[4];
+    __device__ __forceinline__ void load(const ProjArgs &p, int row, int k) {
+        const float *src = p.W + (size_t)(row - p.n_q) * p.I + k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) f[i] = *reinterpret_cast<const float4 *>(src + 4 * i);
+    }
+    __device__ __forceinline__ void unpack(float (&w)[16]) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) { w[4 * i] = f[i].x; w[4 * i + 1] = f[i].y; w[4 * i + 2] = f[i].z; w[4 * i + 3] = f[i].w; }
+    }
+};
+
+__device__ __forceinline__ void load_x16(const float *src, float (&x)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 f = *reinterpret_cast<const float4 *>(src + 4 * i);
+        x[4 * i] = f.x; x[4 * i + 1] = f.y; x[4 * i + 2] = f.z; x[4 * i + 3] = f.w;
+    }
+}
+
+// ---------------------------------------------------------------- GEMV
+// A workgroup is 4 waves = RG row groups of kGemvRows rows x KS k-slices;
+// each wave covers its k-slice in chunks of 1024 (16 per lane).
+constexpr int kGemvRows = 8;
+
+// Sum of v[i] over the 64 lanes for 8 values at once, halving the set at
+// each of the first three exchanges: lane L ends with the total of value
+// 4*bit5(L) + 2*bit4(L) + bit3(L).
+__device__ __forceinline__ float sum8_over_lanes(const float (&v)[8], int lane) {
+    float u[4], t[2];
+    const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float send = h5 ? v[i] : v[i + 4];
+        u[i] = (h5 ? v[i + 4] : v[i]) + __shfl_xor(send, 32, OMH_WAVE);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float send = h4 ? u[i] : u[i + 2];
+        t[i] = (h4 ? u[i + 2] : u[i]) + __shfl_xor(send, 16, OMH_WAVE);
+    }
+    float r = (h3 ? t[1] : t[0]) + __shfl_xor(h3 ? t[0] : t[1], 8, OMH_WAVE);
+    r += __shfl_xor(r, 4, OMH_WAVE);
+    r += __shfl_xor(r, 2, OMH_WAVE);
+    r += __shfl_xor(r, 1, OMH_WAVE);
+    return r;
+}
+
+template <int NT, bool Q8, int KS>
+__device__ __forceinline__ void gemv_rows(const ProjArgs &p, int r0, int ks, int lane, float (*red)[NT][OMH_WAVE],
+                                          int rg, bool store) {
+    float acc[kGemvRows][NT];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; i++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[i][t] = 0.f;
+    const int nrow = min(kGemvRows, p.O - r0);
+    const int klen = p.I / KS;
+    for (int kc = ks * klen; kc < (ks + 1) * klen; kc += 16 * OMH_WAVE) {
+        const int k = kc + 16 * lane;
+        if (k < (ks + 1) * klen) {
+            WFrag<Q8> wf[kGemvRows];                 // every row's weights in flight together
+#pragma unroll
+            for (int i = 0; i < kGemvRows; i++) wf[i].load(p, r0 + min(i, nrow - 1), k);
+            float x[NT][16];
+#pragma unroll
+            for (int t = 0; t < NT; t++) load_x16(p.x + (size_t)t * p.ldx + k, x[t]);
+#pragma unroll
+            for (int i = 0; i < kGemvRows; i++) {
+                float w[16];
+                wf[i].unpack(w);
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][t] = fmaf(x[t][e], w[e], acc[i][t]);
             }
         }
+    }
+    // lane L holds row 4*bit5(L) + 2*bit4(L) + bit3(L) after the reduction
+    const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+    float tot[NT];
 #pragma unroll
-        for (int t = 0; t < kProjTok; t++) {
-            const float v = omh_xor_sum_below<OMH_WAVE>(acc[t]);
-            if (lane == 0 && t < nt) p.y[(size_t)(t0 + t) * p.ldy + o] = v * sc;
+    for (int t = 0; t < NT; t++) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = acc[i][t];
+        tot[t] = sum8_over_lanes(v, lane);
+    }
+    if (KS > 1) {
+        if (ks > 0)
+#pragma unroll
+            for (int t = 0; t < NT; t++) red[(ks - 1) * 4 + rg][t][lane] = tot[t];
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int j = 0; j < KS - 1; j++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) tot[t] += red[j * 4 + rg][t][lane];
+    }
+    if (store && (lane & 7) == 0 && myrow < nrow) {
+        const int o = r0 + myrow;
+        const float sc = Q8 ? p.scale[o] : 1.f;
+#pragma unroll
+        for (int t = 0; t < NT; t++) p.y[(size_t)t * p.ldy + o] = tot[t] * sc;
+    }
+}
+
+template <int NT, int KS>
+__global__ __launch_bounds__(4 * OMH_WAVE)
+void proj_gemv_kernel(const ProjArgs p) {
+    constexpr int RG = 4 / KS;
+    __shared__ float red[KS > 1 ? (KS - 1) * 4 : 1][NT][OMH_WAVE];
+    const int lane = threadIdx.x % OMH_WAVE;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
+    const int rg = wv % RG, ks = wv / RG;
+    // a row group past the end works on the last group instead (the
+    // workgroup stays together for the k-slice reduction) and stores nothing
+    const int rs = (blockIdx.x * RG + rg) * kGemvRows;
+    const int r0 = min(rs, ((p.O - 1) / kGemvRows) * kGemvRows);
+    if (r0 < p.n_q) gemv_rows<NT, true, KS>(p, r0, ks, lane, red, rg, rs < p.O);
+    else gemv_rows<NT, false, KS>(p, r0, ks, lane, red, rg, rs < p.O);
+}
+
+// ---------------------------------------------------------------- MFMA
+constexpr int kMfmaTok = 64;            // tokens per workgroup (4 tiles of 16)
+
+// One wave: a 16-row tile x TT token tiles over k in [kbeg, kbeg + klen).
+// PF weight blocks (64 wide) are in flight ahead of use (HBM latency), and
+// the next block's x is loaded while the current one is multiplied.
+template <bool Q8>
+__device__ __forceinline__ void mfma_tiles(const ProjArgs &p, int r0, int t0, int TT, int kbeg, int klen, int lane,
+                                           v4f (&acc)[4]) {
+    constexpr int PF = Q8 ? 8 : 2;
+    const int l16 = lane % 16, g = lane / 16;
+    const int row = min(r0 + l16, p.O - 1);
+    const float *xr[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++) xr[tt] = p.x + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * p.ldx + 16 * g + kbeg;
+    const int nb = klen / 64;
+    const int kw = kbeg + 16 * g;
+    WFrag<Q8> wq[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++)
+        if (i < nb) wq[i].load(p, row, kw + 64 * i);
+    float xa[4][16], xb[4][16];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+        if (tt < TT) load_x16(xr[tt], xa[tt]);
+    for (int b0 = 0; b0 < nb; b0 += 2 * PF) {
+#pragma unroll
+        for (int i = 0; i < 2 * PF; i++) {
+            const int b = b0 + i;
+            if (b < nb) {
+                float (&xc)[4][16] = (i & 1) ? xb : xa;
+                float (&xn)[4][16] = (i & 1) ? xa : xb;
+                float w[16];
+                wq[i % PF].unpack(w);
+                if (b + PF < nb) wq[i % PF].load(p, row, kw + 64 * (b + PF));
+                if (b + 1 < nb)
+#pragma unroll
+                    for (int tt = 0; tt < 4; tt++)
+                        if (tt < TT) load_x16(xr[tt] + 64 * (b + 1), xn[tt]);
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+                    if (tt < TT)
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[tt][e], w[e], acc[tt], 0, 0, 0);
+            }
         }
     }
 }
 
+template <int RT>
+__global__ __launch_bounds__(4 * OMH_WAVE)
+void proj_mfma_kernel(const ProjArgs p) {
+    constexpr int KS = 4 / RT;
+    __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RT][4][OMH_WAVE];
+    const int lane = threadIdx.x % OMH_WAVE;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
+    const int rt = wv % RT, ks = wv / RT;
+    const int r0 = (blockIdx.x * RT + rt) * 16;
+    const int t0 = blockIdx.y * kMfmaTok;
+    const int TT = (min(kMfmaTok, p.T - t0) + 15) / 16;
+    const int klen = p.I / KS, kbeg = ks * klen;
+    v4f acc[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++) acc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (r0 < p.O) {
+        if (r0 < p.n_q) mfma_tiles<true>(p, r0, t0, TT, kbeg, klen, lane, acc);
+        else mfma_tiles<false>(p, r0, t0, TT, kbeg, klen, lane, acc);
+    }
+    if (KS > 1) {
+        if (ks > 0)
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) s_red[ks - 1][rt][tt][lane] = acc[tt];
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int j = 0; j < KS - 1; j++)
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) acc[tt] += s_red[j][rt][tt][lane];
+    }
+    if (r0 >= p.O) return;
+    const int l16 = lane % 16, g = lane / 16;
+    const int o = r0 + l16;
+    if (o >= p.O) return;
+    const float sc = r0 < p.n_q ? p.scale[o] : 1.f;
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int t = t0 + 16 * tt + 4 * g + r;
+            if (tt < TT && t < p.T) p.y[(size_t)t * p.ldy + o] = acc[tt][r] * sc;
+        }
+}
+
 }  // namespace
+
+bool proj_supported(int I, int n_q) { return I >= 64 && I % 64 == 0 && n_q % 16 == 0; }
 
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
     if (p.O <= 0 || p.T <= 0) return hipSuccess;
-    if (p.I % 4 != 0) return hipErrorInvalidValue;
-    dim3 grid((p.O + kProjWaves - 1) / kProjWaves);
-    hipLaunchKernelGGL(proj_rows_kernel, grid, dim3(kProjWaves * OMH_WAVE), 0, st, p);
+    if (!proj_supported(p.I, p.n_q)) return hipErrorInvalidValue;
+    if (p.T <= 4) {
+        // k-slices: as many 1024-wide chunks as there are, up to 4 per row group
+        const int ks = p.I >= 4096 ? 4 : (p.I >= 2048 ? 2 : 1);
+        const int rows_per_wg = (4 / ks) * kGemvRows;
+        const dim3 grid((p.O + rows_per_wg - 1) / rows_per_wg), blk(4 * OMH_WAVE);
+#define OMH_GEMV(NT)                                                                        \
+    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4>), grid, blk, 0, st, p);       \
+    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2>), grid, blk, 0, st, p);  \
+    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1>), grid, blk, 0, st, p);
+        switch (p.T) {
+        case 1: OMH_GEMV(1) break;
+        case 2: OMH_GEMV(2) break;
+        case 3: OMH_GEMV(3) break;
+        default: OMH_GEMV(4) break;
+        }
+#undef OMH_GEMV
+        return hipGetLastError();
+    }
+    // fewest row tiles per workgroup that still gives >= 256 workgroups,
+    // with each k-slice a whole number of 64-wide blocks
+    const int tb = (p.T + kMfmaTok - 1) / kMfmaTok;
+    const int tiles = (p.O + 15) / 16;
+    int rt = 4;
+    if ((tiles + 3) / 4 * tb < 256) rt = 2;
+    if ((tiles + 1) / 2 * tb < 256) rt = 1;
+    while (rt < 4 && p.I % (64 * (4 / rt)) != 0) rt *= 2;
+    const dim3 grid((tiles + rt - 1) / rt, tb), blk(4 * OMH_WAVE);
+    if (rt == 4) hipLaunchKernelGGL(proj_mfma_kernel<4>, grid, blk, 0, st, p);
+    else if (rt == 2) hipLaunchKernelGGL(proj_mfma_kernel<2>, grid, blk, 0, st, p);
+    else hipLaunchKernelGGL(proj_mfma_kernel<1>, grid, blk, 0, st, p);
     return hipGetLastError();
 }
 

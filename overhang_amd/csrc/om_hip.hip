@@ -326,8 +326,11 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
     }
     const bool any_proj = w->W_qkv || w->Q_qkv;
     if (any_proj) {
-        if (D < 4 || D % 4 || L.vdim % 4) { free_layer(L); return fail(OMH_ERR_SHAPE, "layer_init: hidden and vh*vd must be multiples of 4"); }
         const bool q8 = w->Q_qkv != nullptr;
+        if (!proj_supported(D, q8 ? L.conv_dim + L.vdim : 0) || !proj_supported(L.vdim, w->Q_out ? D : 0)) {
+            free_layer(L);
+            return fail(OMH_ERR_SHAPE, "layer_init: projections need hidden and vh*vd multiples of 64 (got %d, %d)", D, L.vdim);
+        }
         if (q8 && (!w->Q_z || !w->S_qkv || !w->S_z)) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: int8 in_proj needs Q_qkv, Q_z and their scales"); }
         if (!q8 && (!w->W_qkv || !w->W_z)) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: fp32 in_proj needs W_qkv and W_z"); }
         if (!w->W_b || !w->W_a) { free_layer(L); return fail(OMH_ERR_ARG, "layer_init: W_b and W_a are required"); }

@@ -77,6 +77,8 @@ struct ProjArgs {
     int64_t ldx, ldy;
     int T, I, O, n_q;
 };
+// hidden size I and int8 row count n_q the projection kernels take
+bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
 
 // Chunked prefill of T tokens of one sequence (kd == vd == D).

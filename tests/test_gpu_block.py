@@ -1,0 +1,98 @@
+"""GPU parity of the whole GDN block (in_proj -> core -> out_proj) through the C-ABI.
+
+The reference runs one token of one sequence per deltanet_step call
+(overhang engines/qwen.c:301-364), with the projections as matvec /
+matmul_q (qwen.c:70-77, 94-122).  Batched decode (B sequences, one token
+each) and prefill (T tokens) must equal that per-token, per-sequence
+recurrence (the CPU oracle) for every batch size, which covers both
+projection kernels (register GEMV for up to 4 tokens, fp32 MFMA above) and
+partial token tiles.  Tolerance: tests/tol.py."""
+import numpy as np
+import pytest
+
+import oracle
+from overhang_amd import gdn, synth
+from overhang_amd.dims import CFG1, TINY, Q35B
+from tests.tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+_next_li = [800]
+
+
+def new_li():
+    _next_li[0] += 1
+    return _next_li[0]
+
+
+def _x(d, seed, shape):
+    return synth.normal(seed, synth.S_X, shape + (d.hidden,), 0.0, 1.0)
+
+
+@pytest.mark.parametrize("dims,int8", [(CFG1, False), (TINY, True)], ids=["cfg1-f32", "tiny-int8"])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 5, 17, 64])
+def test_batched_decode_block_matches_oracle(dims, int8, B):
+    d = dims
+    seed = 9000 + B + 100 * int8
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=int8)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    T = 2
+    x = _x(d, seed, (T, B))
+    got = np.stack([L.decode(x[t]) for t in range(T)], axis=1)       # [B][T][D]
+    for s in sorted({0, B // 2, B - 1}):
+        ref, cref, Sref = oracle.layer_seq(d, w, x[:, s], conv0[s], S0[s], int8=int8)
+        conv, S = L.get_state(s)
+        assert_close(got[s], ref, what=f"B={B} seq {s} out")
+        assert_close(S, Sref, what=f"B={B} seq {s} S")
+        assert_close(conv, cref, atol=1e-5, rtol=1e-5, what=f"B={B} seq {s} conv")
+    L.free()
+
+
+@pytest.mark.parametrize("T", [5, 64, 65, 200])
+def test_prefill_block_matches_oracle(T):
+    d = CFG1
+    seed = 9500 + T
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed)
+    for int8 in (False, True):
+        L = gdn.GdnLayer(new_li(), d, w, int8=int8)
+        L.set_state(0, conv0, S0)
+        x = _x(d, seed, (T,))
+        out = L.prefill(0, x)
+        ref, cref, Sref = oracle.layer_seq(d, w, x, conv0, S0, int8=int8)
+        conv, S = L.get_state(0)
+        assert_close(out, ref, what=f"T={T} int8={int8} out")
+        assert_close(S, Sref, what=f"T={T} int8={int8} S")
+        L.free()
+
+
+def test_35b_int8_block_batch64():
+    """Qwen3.6-35B-A3B GDN block with int8 in/out projections (config 5
+    shape): 64 sequences, one token each, three sequences checked."""
+    d = Q35B
+    B = 64
+    w = synth.layer_weights(d, 77, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, 77, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    x = _x(d, 77, (B,))
+    got = L.decode(x)
+    for s in (0, 31, 63):
+        ref, cref, Sref = oracle.layer_seq(d, w, x[s:s + 1], conv0[s], S0[s], int8=True)
+        conv, S = L.get_state(s)
+        assert_close(got[s:s + 1], ref, what=f"seq {s} out")
+        assert_close(S, Sref, what=f"seq {s} S")
+    L.free()
+
+
+def test_projection_shape_limits_are_reported():
+    from overhang_amd.dims import GdnDims
+    d = GdnDims(kh=2, vh=4, kd=16, vd=16, K=4, hidden=96)       # hidden not a multiple of 64
+    w = synth.layer_weights(d, 1)
+    with pytest.raises(gdn.OmhError) as e:
+        gdn.GdnLayer(new_li(), d, w)
+    assert e.value.code == gdn.OMH_ERR_SHAPE
