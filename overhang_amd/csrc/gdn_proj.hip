@@ -179,84 +179,92 @@ void proj_gemv_kernel(const ProjArgs p) {
 }
 
 // ---------------------------------------------------------------- MFMA
-constexpr int kMfmaTok = 64;            // tokens per workgroup (4 tiles of 16)
+constexpr int kMfmaTok = 64;            // tokens per workgroup (up to 4 tiles of 16)
 
-// One wave: a 16-row tile x TT token tiles over k in [kbeg, kbeg + klen).
-// PF weight blocks (64 wide) are in flight ahead of use (HBM latency), and
-// the next block's x is loaded while the current one is multiplied.
-template <bool Q8>
-__device__ __forceinline__ void mfma_tiles(const ProjArgs &p, int r0, int t0, int TT, int kbeg, int klen, int lane,
+// One wave: a 16-row tile x TT token tiles over k in [kbeg, kbeg + klen),
+// nb = klen / 64 blocks, PF | nb.  The weights come in batches of PF blocks
+// whose loads are all issued before the batch's x loads: the load counter
+// completes in order, so waiting for an x fragment also waits for every
+// weight load issued before it, and batching pays the HBM latency once per
+// batch instead of once per step.  The x fragments (one per (block, token
+// tile) step) are loaded XD steps ahead into NX = XD + 1 rotating 16-float
+// buffers (L2 latency); the batch's step count PF * TT is a multiple of NX,
+// so every buffer index is known at compile time.  Loads are unconditional
+// (indices clamped at the end) so the wait counts are exact.
+template <int TT, bool Q8, int PF>
+__device__ __forceinline__ void mfma_tiles(const ProjArgs &p, int r0, int t0, int kbeg, int klen, int lane,
                                            v4f (&acc)[4]) {
-    constexpr int PF = Q8 ? 8 : 2;
+    constexpr int NS = PF * TT;                          // steps per batch
+    constexpr int NX = NS % 4 == 0 ? 4 : (NS % 2 == 0 ? 2 : 1);
+    constexpr int XD = NX - 1 > 0 ? NX - 1 : 0;          // prefetch distance in steps
     const int l16 = lane % 16, g = lane / 16;
     const int row = min(r0 + l16, p.O - 1);
-    const float *xr[4];
+    const float *xr[TT];
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++) xr[tt] = p.x + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * p.ldx + 16 * g + kbeg;
+    for (int tt = 0; tt < TT; tt++) xr[tt] = p.x + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * p.ldx + 16 * g + kbeg;
     const int nb = klen / 64;
     const int kw = kbeg + 16 * g;
-    WFrag<Q8> wq[PF];
+    // x of global step q (block q / TT, token tile q % TT), clamped to the last step
+    auto load_step = [&](int q, float (&dst)[16]) {
+        const int b = min(q / TT, nb - 1);
+        load_x16(xr[q % TT] + 64 * b, dst);
+    };
+    float xs[NX][16];
+    for (int b0 = 0; b0 < nb; b0 += PF) {
+        WFrag<Q8> wq[PF];
 #pragma unroll
-    for (int i = 0; i < PF; i++)
-        if (i < nb) wq[i].load(p, row, kw + 64 * i);
-    float xa[4][16], xb[4][16];
+        for (int i = 0; i < PF; i++) wq[i].load(p, row, kw + 64 * (b0 + i));
+        if (b0 == 0)
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++)
-        if (tt < TT) load_x16(xr[tt], xa[tt]);
-    for (int b0 = 0; b0 < nb; b0 += 2 * PF) {
+            for (int q = 0; q < XD; q++) load_step(q, xs[q]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 2 * PF; i++) {
-            const int b = b0 + i;
-            if (b < nb) {
-                float (&xc)[4][16] = (i & 1) ? xb : xa;
-                float (&xn)[4][16] = (i & 1) ? xa : xb;
-                float w[16];
-                wq[i % PF].unpack(w);
-                if (b + PF < nb) wq[i % PF].load(p, row, kw + 64 * (b + PF));
-                if (b + 1 < nb)
+        for (int i = 0; i < PF; i++) {
+            float w[16];
+            wq[i].unpack(w);
 #pragma unroll
-                    for (int tt = 0; tt < 4; tt++)
-                        if (tt < TT) load_x16(xr[tt] + 64 * (b + 1), xn[tt]);
+            for (int tt = 0; tt < TT; tt++) {
+                const int st = i * TT + tt;                     // step within the batch
+                const int q = b0 * TT + st;                     // global step
+                if (NX == 1) load_step(q, xs[0]);
+                else load_step(q + XD, xs[(st + XD) % NX]);
+                __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of the products
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++)
-                    if (tt < TT)
-#pragma unroll
-                        for (int e = 0; e < 16; e++)
-                            acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xc[tt][e], w[e], acc[tt], 0, 0, 0);
+                for (int e = 0; e < 16; e++)
+                    acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[st % NX][e], w[e], acc[tt], 0, 0, 0);
             }
         }
     }
 }
 
-template <int RT>
+template <int RT, int TT, int PF>
 __global__ __launch_bounds__(4 * OMH_WAVE)
 void proj_mfma_kernel(const ProjArgs p) {
     constexpr int KS = 4 / RT;
-    __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RT][4][OMH_WAVE];
+    __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RT][TT][OMH_WAVE];
     const int lane = threadIdx.x % OMH_WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
     const int rt = wv % RT, ks = wv / RT;
     const int r0 = (blockIdx.x * RT + rt) * 16;
     const int t0 = blockIdx.y * kMfmaTok;
-    const int TT = (min(kMfmaTok, p.T - t0) + 15) / 16;
     const int klen = p.I / KS, kbeg = ks * klen;
     v4f acc[4];
 #pragma unroll
     for (int tt = 0; tt < 4; tt++) acc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
     if (r0 < p.O) {
-        if (r0 < p.n_q) mfma_tiles<true>(p, r0, t0, TT, kbeg, klen, lane, acc);
-        else mfma_tiles<false>(p, r0, t0, TT, kbeg, klen, lane, acc);
+        if (r0 < p.n_q) mfma_tiles<TT, true, PF>(p, r0, t0, kbeg, klen, lane, acc);
+        else mfma_tiles<TT, false, (PF > 2 ? 2 : PF)>(p, r0, t0, kbeg, klen, lane, acc);
     }
     if (KS > 1) {
         if (ks > 0)
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) s_red[ks - 1][rt][tt][lane] = acc[tt];
+            for (int tt = 0; tt < TT; tt++) s_red[ks - 1][rt][tt][lane] = acc[tt];
         __syncthreads();
         if (ks > 0) return;
 #pragma unroll
         for (int j = 0; j < KS - 1; j++)
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++) acc[tt] += s_red[j][rt][tt][lane];
+            for (int tt = 0; tt < TT; tt++) acc[tt] += s_red[j][rt][tt][lane];
     }
     if (r0 >= p.O) return;
     const int l16 = lane % 16, g = lane / 16;
@@ -264,12 +272,34 @@ void proj_mfma_kernel(const ProjArgs p) {
     if (o >= p.O) return;
     const float sc = r0 < p.n_q ? p.scale[o] : 1.f;
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++)
+    for (int tt = 0; tt < TT; tt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int t = t0 + 16 * tt + 4 * g + r;
-            if (tt < TT && t < p.T) p.y[(size_t)t * p.ldy + o] = acc[tt][r] * sc;
+            if (t < p.T) p.y[(size_t)t * p.ldy + o] = acc[tt][r] * sc;
         }
+}
+
+template <int RT, int PF>
+void launch_mfma_tt(const ProjArgs &p, dim3 grid, hipStream_t st) {
+    // token tiles per workgroup: all tiles when every workgroup sees one
+    // token block, else 4 (the last block's missing tokens are clamped)
+    const int tt = grid.y > 1 ? 4 : (p.T + 15) / 16;
+    const dim3 blk(4 * OMH_WAVE);
+    switch (tt) {
+    case 1: hipLaunchKernelGGL((proj_mfma_kernel<RT, 1, PF>), grid, blk, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((proj_mfma_kernel<RT, 2, PF>), grid, blk, 0, st, p); break;
+    case 3: hipLaunchKernelGGL((proj_mfma_kernel<RT, 3, PF>), grid, blk, 0, st, p); break;
+    default: hipLaunchKernelGGL((proj_mfma_kernel<RT, 4, PF>), grid, blk, 0, st, p); break;
+    }
+}
+
+template <int RT>
+void launch_mfma_rt(const ProjArgs &p, dim3 grid, hipStream_t st) {
+    const int nb = p.I / (4 / RT) / 64;       // 64-wide blocks per k-slice
+    if (nb % 8 == 0) launch_mfma_tt<RT, 8>(p, grid, st);
+    else if (nb % 2 == 0) launch_mfma_tt<RT, 2>(p, grid, st);
+    else launch_mfma_tt<RT, 1>(p, grid, st);
 }
 
 }  // namespace
@@ -297,18 +327,18 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
 #undef OMH_GEMV
         return hipGetLastError();
     }
-    // fewest row tiles per workgroup that still gives >= 256 workgroups,
-    // with each k-slice a whole number of 64-wide blocks
+    // one row tile per workgroup (k split over its 4 waves) unless that
+    // leaves k-slices narrower than a 64-wide block or far more workgroups
+    // than the device holds at once
     const int tb = (p.T + kMfmaTok - 1) / kMfmaTok;
     const int tiles = (p.O + 15) / 16;
-    int rt = 4;
-    if ((tiles + 3) / 4 * tb < 256) rt = 2;
-    if ((tiles + 1) / 2 * tb < 256) rt = 1;
-    while (rt < 4 && p.I % (64 * (4 / rt)) != 0) rt *= 2;
-    const dim3 grid((tiles + rt - 1) / rt, tb), blk(4 * OMH_WAVE);
-    if (rt == 4) hipLaunchKernelGGL(proj_mfma_kernel<4>, grid, blk, 0, st, p);
-    else if (rt == 2) hipLaunchKernelGGL(proj_mfma_kernel<2>, grid, blk, 0, st, p);
-    else hipLaunchKernelGGL(proj_mfma_kernel<1>, grid, blk, 0, st, p);
+    int rt = 1;
+    if (p.I % 256 != 0 || tiles * tb > 4096) rt = 2;
+    if (p.I % 128 != 0 || tiles * tb > 8192) rt = 4;
+    const dim3 grid((tiles + rt - 1) / rt, tb);
+    if (rt == 4) launch_mfma_rt<4>(p, grid, st);
+    else if (rt == 2) launch_mfma_rt<2>(p, grid, st);
+    else launch_mfma_rt<1>(p, grid, st);
     return hipGetLastError();
 }
 
