@@ -10,10 +10,12 @@ Cache cannot hold them (each step reads and writes 126 MB of state from HBM).
 
 Also reported: the same step launched layer by layer (the order an engine
 runs it), a batch sweep B=1..64 of one-layer launches, the chunked prefill
-of T=4096 tokens at the same head shape (MFMA roofline), a device-to-device
-copy of the decode step's bytes (the HBM bandwidth a plain copy reaches on
-this box), and the CPU oracle (the reference GDN restated in C, OpenMP) on
-the host cores.
+of T=4096 tokens at the same head shape (MFMA roofline), a 32768-token
+prefill continuing from an 8192-token one (config 4), one decode step of the
+whole block with int8 projections for 64 sequences (config 5, HBM roofline),
+a device-to-device copy (the HBM bandwidth a plain copy reaches on this
+box), and the CPU oracle (the reference GDN restated in C, OpenMP) on the
+host cores.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--part all|decode|prefill]
@@ -220,11 +222,89 @@ def bench_prefill(hip, gdn, synth, T, steps, warmup):
            "flops_per_call": fl, "TFLOPs": tf, "peak_TFLOPs": FP32_MFMA_TFLOPS,
            "frac_fp32_mfma": tf / FP32_MFMA_TFLOPS, "frac_attainable": tf / attain,
            "hbm_bytes_alg": by, "recurrent_equiv_GFLOP": 7 * d.vh * T * d.kd * d.vd / 1e9,
-           "note": "one GDN layer core (5 launches: prep, conv commit, chunk, scan, gated norm), "
+           "note": "one GDN layer core (4 launches: WY/chunk (conv, norms, gates, triangular solve, "
+                   "panels), conv-history commit, scan, gated norm), "
                    "kh=16 vh=32 kd=vd=128, fp32 I/O and fp32 MFMA, state carried across calls"}
     log(f"prefill T={T}: {1e6 * t:.0f} us/layer, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
         f"({100 * out['frac_fp32_mfma']:.1f}% of fp32 MFMA peak)")
     return out
+
+
+def bench_prefill_warm(hip, gdn, synth, T, warm, steps, warmup):
+    """Config 4: T-token prefill calls continuing from the state left by a
+    warm-up prefill of `warm` tokens, gate logits a ~ N(-2, 1).  Inputs are a
+    seeded 4096-token block repeated (generating T fresh 35B-width rows on the
+    host would dominate the run); every call does the same work."""
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = synth.layer_weights(d, 1, projections=False)
+    L = gdn.GdnLayer(2001, d, w, max_seqs=1)
+    blk = synth.core_inputs(d, 4096, 11, a_mean=-2.0)
+    rep = -(-max(T, warm) // 4096)
+    dev = {k: hip.Buffer.from_numpy(np.tile(v, (rep, 1))) for k, v in blk.items()}
+    core = hip.Buffer(max(T, warm) * d.val_dim * 4)
+    st = hip.Stream()
+    gdn.prefill_core_dev(L.li, 0, warm, dev["qkv"], dev["z"], dev["a"], dev["b"], core, stream=st)
+
+    def one(k):
+        gdn.prefill_core_dev(L.li, 0, T, dev["qkv"], dev["z"], dev["a"], dev["b"], core, stream=st)
+
+    el, durs, _ = time_launches(hip, st, one, steps, warmup)
+    L.free()
+    t = el / steps
+    fl = prefill_flops(d, T)
+    tf = fl / t / 1e12
+    out = {"T": T, "warm_tokens": warm, "chunk": 64, "tok_s": T * steps / el, "us_per_call": 1e6 * t,
+           "flops_per_call": fl, "TFLOPs": tf, "frac_fp32_mfma": tf / FP32_MFMA_TFLOPS,
+           "hbm_bytes_alg": prefill_bytes(d, T),
+           "note": "config 4: one GDN layer core, T-token prefill continuing from the state of a "
+                   f"{warm}-token prefill, a ~ N(-2,1), 35B head shape, fp32"}
+    log(f"prefill warm-append T={T}: {1e6 * t:.0f} us/call, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
+        f"({100 * out['frac_fp32_mfma']:.1f}% of fp32 MFMA peak)")
+    return out
+
+
+def block_bytes(d, B):
+    """Compulsory HBM bytes of one batched decode step of the whole GDN block
+    with int8 projections: in_proj weights ([qkv|z] int8 + per-row scales,
+    [b|a] fp32), out_proj int8 + scales, each sequence's recurrent and conv
+    state read and written, x in and out."""
+    n_q = d.conv_dim + d.val_dim
+    w_in = n_q * d.hidden + 4 * n_q + 2 * d.vh * d.hidden * 4
+    w_out = d.hidden * d.val_dim + 4 * d.hidden
+    state = 2 * (d.state_bytes + 4 * d.conv_dim * (d.K - 1))
+    return w_in + w_out + B * state + 2 * B * d.hidden * 4
+
+
+def bench_block(hip, gdn, synth, B, steps, warmup):
+    """Config 5: one decode step of the whole GDN block (int8 in_proj -> conv ->
+    recurrence -> gated norm -> int8 out_proj) for B independent sequences,
+    each with its own state, rotating over >1 GiB of layer states."""
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = synth.layer_weights(d, 5)
+    per = B * (d.state_bytes + 4 * d.conv_dim * (d.K - 1))
+    nrot = max(2, math.ceil(ROTATE_BYTES / per))
+    lays = [gdn.GdnLayer(3000 + i, d, w, max_seqs=B, int8=True) for i in range(nrot)]
+    x = hip.Buffer.from_numpy(synth.normal(7, synth.S_X, (B, d.hidden), 0.0, 1.0))
+    out = hip.Buffer(B * d.hidden * 4)
+    st = hip.Stream()
+
+    def one(k):
+        gdn.decode_dev(lays[k % nrot].li, B, x, out, stream=st)
+
+    el, durs, _ = time_launches(hip, st, one, steps, warmup)
+    for L in lays:
+        L.free()
+    t = el / steps
+    by = block_bytes(d, B)
+    gbs = by / t / 1e9
+    res = {"B": B, "us_per_step": 1e6 * t, "tok_s": B / t, "alg_bytes": by, "achieved_GBs": gbs,
+           "frac_hbm": gbs / HBM_PEAK_GBS,
+           "note": "config 5: whole GDN block, one token for each of B sequences, int8 [qkv|z] in_proj and "
+                   "out_proj dequantised in-kernel, fp32 b/a rows, 35B shape; tok_s is per layer"}
+    log(f"block B={B}: {1e6 * t:.1f} us/step, {gbs:.0f} GB/s ({100 * res['frac_hbm']:.1f}% of HBM peak)")
+    return res
 
 
 def cpu_prefill_baseline(synth, T=256, budget_s=8.0):
@@ -330,9 +410,11 @@ def main():
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = None
+    pre = warm = block = None
     if a.part == "all":
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
+        warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 5, 1)
+        block = bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)
     probe = copy_probe(hip, 1 << 29, 20, 3)
     log(f"copy probe: {probe['GBs']:.0f} GB/s (D2D copy of 512 MiB)")
     cpu = None
@@ -372,6 +454,8 @@ def main():
         "cpu_baseline": cpu,
         "hbm_copy_probe": probe,
         "prefill_T4096": pre,
+        "prefill_T32768_warm": warm,
+        "block_int8_B64": block,
         "decode_engine_order": engine,
         "decode_batch_sweep": sweep,
     }
