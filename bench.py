@@ -18,7 +18,7 @@ box), and the CPU oracle (the reference GDN restated in C, OpenMP) on the
 host cores.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--part all|decode|prefill]
+                       [--part all|decode|prefill|block]
 """
 from __future__ import annotations
 
@@ -394,8 +394,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=("all", "decode", "prefill"), default="all",
-                    help="decode: the headline only (for profiling); prefill: the T=4096 prefill only")
+    ap.add_argument("--part", choices=("all", "decode", "prefill", "block"), default="all",
+                    help="decode: the headline only (for profiling); prefill: the T=4096 and T=32768 "
+                         "prefills only; block: the config 5 int8 block at B=64 only")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN layer needs no collectives and this build "
@@ -406,7 +407,12 @@ def main():
     log("device: gfx950 ready")
     if a.part == "prefill":
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 3), a.warmup)
-        print(json.dumps({"prefill": pre}), flush=True)
+        warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 3, 1)
+        print(json.dumps({"prefill": pre, "prefill_T32768_warm": warm}), flush=True)
+        return
+    if a.part == "block":
+        print(json.dumps({"block_int8_B64": bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)}),
+              flush=True)
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
