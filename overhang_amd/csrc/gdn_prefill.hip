@@ -620,8 +620,8 @@ __device__ __forceinline__ void scan_interleave_r() {
 //       which they store after the next B1.
 // Each matrix core then has 64 MFMAs before B2 (W S and Q S) and 48 after.
 // The two roles run separate loops with the same barriers; each loads the
-// next chunk's operands into a second register set, spread over its own
-// products.
+// operands of the chunk after next into a third register set (two chunks of
+// lead time for HBM latency), spread over its own products.
 template <int D>
 __global__ __launch_bounds__((ScanShape<D>::NWV * OMH_WAVE), 1)
 void prefill_scan_kernel(const PrefillArgs a) {
@@ -660,7 +660,7 @@ void prefill_scan_kernel(const PrefillArgs a) {
         // v_new waves
         typedef ScanIn<D, true> In;
         auto step = [&](const In &f, In &fn, int c) {
-            const size_t hn = hc0 + min(c + 1, nc - 1);
+            const size_t hn = hc0 + min(c + 2, nc - 1);
             omh_lds_barrier();                   // B1: S tiles of chunk c
             fn.load_m(a, hn, w, lane);
             v4f P0 = v4zero(), P1 = v4zero();
@@ -682,13 +682,17 @@ void prefill_scan_kernel(const PrefillArgs a) {
                 sm.S[w][lane] = S;
             }
         };
-        In f0, f1;
+        In f0, f1, f2;
         f0.load_m(a, hc0, w, lane);
         f0.load_x(a, hc0, cb, w, lane);
         f0.load_k(a, grs, hc0, w, lane);
-        for (int c = 0; c < nc; c += 2) {
-            step(f0, f1, c);
+        f1.load_m(a, hc0 + min(1, nc - 1), w, lane);
+        f1.load_x(a, hc0 + min(1, nc - 1), cb, w, lane);
+        f1.load_k(a, grs, hc0 + min(1, nc - 1), w, lane);
+        for (int c = 0; c < nc; c += 3) {
+            step(f0, f2, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
+            if (c + 2 < nc) step(f2, f1, c + 2);
         }
     } else {
         // output waves
@@ -704,7 +708,7 @@ void prefill_scan_kernel(const PrefillArgs a) {
             }
         };
         auto step = [&](const In &f, In &fn, int c) {
-            const size_t hn = hc0 + min(c + 1, nc - 1);
+            const size_t hn = hc0 + min(c + 2, nc - 1);
             omh_lds_barrier();                   // B1: S tiles of chunk c
             if (c > 0) store(c - 1);
             fn.load_m(a, hn, w, lane);
@@ -731,13 +735,17 @@ void prefill_scan_kernel(const PrefillArgs a) {
             scan_interleave_r<32, 5>();
             o = O0 + O1;
         };
-        In f0, f1;
+        In f0, f1, f2;
         f0.load_m(a, hc0, w, lane);
         f0.load_x(a, hc0, cb, w, lane);
         f0.load_k(a, grs, hc0, w, lane);
-        for (int c = 0; c < nc; c += 2) {
-            step(f0, f1, c);
+        f1.load_m(a, hc0 + min(1, nc - 1), w, lane);
+        f1.load_x(a, hc0 + min(1, nc - 1), cb, w, lane);
+        f1.load_k(a, grs, hc0 + min(1, nc - 1), w, lane);
+        for (int c = 0; c < nc; c += 3) {
+            step(f0, f2, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
+            if (c + 2 < nc) step(f2, f1, c + 2);
         }
         store(nc - 1);
     }
