@@ -47,10 +47,14 @@ __device__ __forceinline__ v4f v4zero() { v4f z = {0.f, 0.f, 0.f, 0.f}; return z
 // rows) in registers.  Per chunk, waves 0-3 form v_new of token tile w
 // (W S over all of kd) and waves 4-7 the output of token tile w - 4.
 // Panels, per lane, in MFMA fragment order (the WY kernel writes them):
-//   W, Q e^gc   per (head, chunk, token tile j): f = kt*4 + s -> row 16j + l%16, col 16kt + 4g + s
-//   (K e^{gl-gc})^T  per (head, chunk, row tile w): f = tt*4 + s -> row 16tt + 4g + s, col 16w + l%16
-//   Aqk         per (head, chunk, token tile mt): f = kt*4 + s -> row 16mt + l%16, col 16kt + 4g + s
-//   U           per (head, chunk, column block cb, mt): f = r -> row 16mt + 4g + r, col 16cb + l%16
+//   W           per (value head, chunk, token tile j): f = kt*4 + s -> row 16j + l%16, col 16kt + 4g + s
+//   q^          per (key head, chunk, token tile j): the same layout
+//   k^T         per (key head, chunk, row tile w): f = tt*4 + s -> row 16tt + 4g + s, col 16w + l%16
+//   Aqk         per (value head, chunk, token tile mt): f = kt*4 + s -> row 16mt + l%16, col 16kt + 4g + s
+//   U           per (value head, chunk, column block cb, mt): f = r -> row 16mt + 4g + r, col 16cb + l%16
+// q^ and k^ are the normalised q, k, shared by the value heads of a key
+// head; their per-value-head token scalings e^gc and e^{gl-gc} go with them
+// as two 64-float vectors per (value head, chunk).
 // (g = l / 16); each group of four consecutive f is one float4 per lane.
 template <int D>
 struct ScanShape {
@@ -60,7 +64,7 @@ struct ScanShape {
 };
 // float4 index of panel group f4 of lane l in block `blk` (4 groups per block)
 __device__ __forceinline__ size_t pan4(size_t blk, int f4, int l) { return ((blk * 4 + f4) * OMH_WAVE + l) * 4; }
-// W / Q e^gc panels: group kt of token tile j (NST groups per tile)
+// W / q^ panels: group kt of token tile j (NST groups per tile)
 template <int D>
 __device__ __forceinline__ size_t panj(size_t hc, int j, int kt, int l) {
     return (((hc * 4 + j) * (D / 16) + kt) * OMH_WAVE + l) * 4;
@@ -141,7 +145,7 @@ struct WyShape {
     static constexpr int NT = NW * OMH_WAVE;
     static constexpr int PD = D + 4, PC = C + 4;         // padded LDS rows
     static constexpr int NCT = D / 16;                   // 16-column tiles of D
-    static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 4 * C) * sizeof(float);
+    static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 3 * C) * sizeof(float);
 };
 
 // conv1d (K taps, history oldest..newest, then the input; op order as
@@ -259,7 +263,6 @@ void prefill_wy_kernel(const PrefillArgs a) {
     float *gcs = As + C * PC;                    // [C] cumulative log decay
     float *bs = gcs + C;                         // [C] beta
     float *ws = bs + C;                          // [C] beta e^gc
-    float *egl = ws + C;                         // [C] e^{gc_last - gc}
 
     int m = blockIdx.x;
     WyIn<D> in;
@@ -313,11 +316,13 @@ void prefill_wy_kernel(const PrefillArgs a) {
                 if (lane >= off) x += y;
             }
             const float gl = __shfl(x, C - 1, OMH_WAVE);
+            const float ex = expf(x), ee = expf(gl - x);
             gcs[lane] = x;
             bs[lane] = be;
-            ws[lane] = be * expf(x);
-            egl[lane] = expf(gl - x);
-            if (lane == C - 1) a.glast[hc] = expf(x);
+            ws[lane] = be * ex;
+            a.pg[hc * C + lane] = ex;
+            a.pe[hc * C + lane] = ee;
+            if (lane == C - 1) a.glast[hc] = ex;
         }
         // prefetch the next item's inputs; they land during this item's math
         if (m + (int)gridDim.x < nitems) {
@@ -394,7 +399,7 @@ void prefill_wy_kernel(const PrefillArgs a) {
         // substitution, lane jj < 16 keeping column jj (X[i][jj] = -sum_{m<i}
         // L[i][m] X[m][jj] below the diagonal).  Meanwhile the other waves
         // (all waves, after, when there are only four) write the panels that
-        // need no inverse: Q e^gc, (K e^{gl - gc})^T and Aqk, a float4 per lane.
+        // need no inverse: q^, k^T (once per key head) and Aqk, a float4 per lane.
         if (wave < 4) {
             const int b0 = 16 * wave;
             float x[16];
@@ -413,17 +418,21 @@ void prefill_wy_kernel(const PrefillArgs a) {
             constexpr int PW = NW > 4 ? NW - 4 : NW;         // panel-writing waves
             const int pw_t = NW > 4 ? tid - 4 * OMH_WAVE : tid;
             if (pw_t >= 0) {
-                // Q/K panels: NST kd tiles x 4 token tiles x 64 lanes
-                for (int e = pw_t; e < NST * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
-                    const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
-                    const int ll16 = l % 16, lg = l / 16;
-                    const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
-                    const float4 vq = f4_scale(*reinterpret_cast<const float4 *>(Qs + rq * PD + cq), expf(gcs[rq]));
-                    const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
-                    const float4 vk = make_float4(Ks[rk * PD + ck] * egl[rk], Ks[(rk + 1) * PD + ck] * egl[rk + 1],
-                                                  Ks[(rk + 2) * PD + ck] * egl[rk + 2], Ks[(rk + 3) * PD + ck] * egl[rk + 3]);
-                    *reinterpret_cast<float4 *>(a.pq + panj<D>(hc, tt, w, l)) = vq;
-                    *reinterpret_cast<float4 *>(a.pk + pan4(hc * NST + w, tt, l)) = vk;
+                // q^ / k^T panels (NST kd tiles x 4 token tiles x 64 lanes),
+                // once per key head: by the item of its first value head
+                if (h % rep == 0) {
+                    const size_t hq = (size_t)hk * a.nc + c;
+                    for (int e = pw_t; e < NST * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
+                        const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
+                        const int ll16 = l % 16, lg = l / 16;
+                        const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
+                        const float4 vq = *reinterpret_cast<const float4 *>(Qs + rq * PD + cq);
+                        const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
+                        const float4 vk = make_float4(Ks[rk * PD + ck], Ks[(rk + 1) * PD + ck], Ks[(rk + 2) * PD + ck],
+                                                      Ks[(rk + 3) * PD + ck]);
+                        *reinterpret_cast<float4 *>(a.pq + panj<D>(hq, tt, w, l)) = vq;
+                        *reinterpret_cast<float4 *>(a.pk + pan4(hq * NST + w, tt, l)) = vk;
+                    }
                 }
                 for (int e = pw_t; e < 16 * OMH_WAVE; e += PW * OMH_WAVE) {
                     const int l = e % OMH_WAVE, kt = (e / OMH_WAVE) % 4, mt = e / (4 * OMH_WAVE);
@@ -501,21 +510,24 @@ void prefill_wy_kernel(const PrefillArgs a) {
 
 // ---------------------------------------------------------------- P3 scan
 // One chunk's operands for one scan wave, in MFMA fragment order: for a
-// v_new wave (V = true) the W and U tiles of its token tile, for an output
-// wave the Q e^gc and Aqk tiles; for both the (K e^{gl-gc})^T row tile of
-// the S tile the wave holds, and e^{gl}.  Loaded in parts (load_m, load_x,
-// load_k) so each part can be spread over a different product.
+// v_new wave (V = true) the W and U tiles of its token tile and e^{gl-gc} of
+// its rows, for an output wave the q^ and Aqk tiles and e^gc of its rows;
+// for both the k^T row tile of the S tile the wave holds, and e^{gl}.
+// Loaded in parts (load_m, load_x, load_k) so each part can be spread over a
+// different product.
 template <int D, bool V>
 struct ScanIn {
     static constexpr int NST = ScanShape<D>::NST;
     static constexpr int NX = V ? 4 : 16;
-    float Mf[4 * NST];   // W or Q e^gc, token tile w % 4
+    float Mf[4 * NST];   // W or q^, token tile w % 4
     float Xf[NX];        // U tile (D layout) or Aqk row tile
-    float Kf[16];        // (K e^{gl-gc})^T of row tile w
+    float Kf[16];        // k^T of row tile w
+    float sc[4];         // e^{gl-gc} (v_new waves) or e^gc (output waves) of rows 4g..4g+3 of token tile w % 4
     float eg;            // e^{gl}
 
-    __device__ __forceinline__ void load_m(const PrefillArgs &a, size_t hc, int w, int lane) {
-        const float *mp = (V ? a.pw : a.pq) + panj<D>(hc, w & 3, 0, lane);
+    // hc: (value head, chunk); hq: (key head, chunk)
+    __device__ __forceinline__ void load_m(const PrefillArgs &a, size_t hc, size_t hq, int w, int lane) {
+        const float *mp = V ? a.pw + panj<D>(hc, w & 3, 0, lane) : a.pq + panj<D>(hq, w & 3, 0, lane);
 #pragma unroll
         for (int kt = 0; kt < NST; kt++) {
             const float4 x = *reinterpret_cast<const float4 *>(mp + kt * OMH_WAVE * 4);
@@ -529,11 +541,14 @@ struct ScanIn {
             const float4 x = *reinterpret_cast<const float4 *>(xp + kt * OMH_WAVE * 4);
             Xf[4 * kt] = x.x; Xf[4 * kt + 1] = x.y; Xf[4 * kt + 2] = x.z; Xf[4 * kt + 3] = x.w;
         }
+        const float4 x = *reinterpret_cast<const float4 *>((V ? a.pe : a.pg) + hc * C + 16 * (w & 3) + 4 * (lane / 16));
+        sc[0] = x.x; sc[1] = x.y; sc[2] = x.z; sc[3] = x.w;
     }
     // eg comes through a buffer load (a vector load at a uniform offset): a
     // scalar load would share lgkmcnt with the LDS reads and hold them up.
-    __device__ __forceinline__ void load_k(const PrefillArgs &a, __amdgpu_buffer_rsrc_t grs, size_t hc, int w, int lane) {
-        const float *kp = a.pk + pan4(hc * NST + (w < NST ? w : NST - 1), 0, lane);
+    __device__ __forceinline__ void load_k(const PrefillArgs &a, __amdgpu_buffer_rsrc_t grs, size_t hc, size_t hq, int w,
+                                           int lane) {
+        const float *kp = a.pk + pan4(hq * NST + (w < NST ? w : NST - 1), 0, lane);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
             const float4 x = *reinterpret_cast<const float4 *>(kp + tt * OMH_WAVE * 4);
@@ -548,6 +563,7 @@ template <int D>
 struct ScanLds {
     v4f S[ScanShape<D>::NST][OMH_WAVE];      // S row tiles at the start of the chunk
     v4f V[4][OMH_WAVE];                      // v_new token tiles
+    v4f Vs[4][OMH_WAVE];                     // the same rows scaled by e^{gl-gc}
 };
 
 // S <- e^{gl} S + (K e^{gl-gc})^T v_new for the wave's row tile (two chains)
@@ -612,9 +628,10 @@ __device__ __forceinline__ void scan_interleave_r() {
 // sequence.  Per chunk, two barriers:
 //   B1: every S row tile of the chunk is in LDS.  Waves 0-3 each form
 //       v_new = U - W S for one token tile (contracting over all of kd) into
-//       LDS; waves 4-7 each form (Q e^gc) S for one token tile.
+//       LDS, once as is and once with its rows scaled by e^{gl-gc}; waves 4-7
+//       each form e^gc (q^ S) for one token tile.
 //   B2: v_new is in LDS.  Every wave updates its S tile,
-//       S <- e^{gl} S + (K e^{gl-gc})^T v_new, and writes it to LDS for the
+//       S <- e^{gl} S + k^T (e^{gl-gc} v_new), and writes it to LDS for the
 //       next chunk; waves 4-7 add Aqk v_new over all key tiles (the panel's
 //       tiles above the diagonal are zero) to finish their output tile,
 //       which they store after the next B1.
@@ -628,13 +645,23 @@ void prefill_scan_kernel(const PrefillArgs a) {
     constexpr int NST = ScanShape<D>::NST;
     constexpr int NCB = D / 16;
     const int vh = a.vh;
-    // XCD-aware: the NCB column blocks of a head share one XCD (and its L2)
+    // XCD-aware: the column blocks of all value heads of a key head share one
+    // XCD (and its L2), so the key head's q^ / k^ panels are fetched once
+    const int rep = vh / a.kh;
     int h, cb;
     {
         const int n = blockIdx.x;
-        if (vh % 8 == 0) { h = (n % 8) + 8 * (n / (8 * NCB)); cb = (n / 8) % NCB; }
-        else { h = n / NCB; cb = n % NCB; }
+        if (a.kh % 8 == 0) {
+            const int x = n % 8, m = n / 8;
+            h = (x + 8 * (m / (rep * NCB))) * rep + (m / NCB) % rep;
+            cb = m % NCB;
+        } else {
+            h = n / NCB;
+            cb = n % NCB;
+        }
     }
+    const int hk = h / rep;
+    const size_t hq0 = (size_t)hk * a.nc;
     const int lane = threadIdx.x % OMH_WAVE;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
     const int l16 = lane % 16, g4 = lane / 16;
@@ -660,35 +687,40 @@ void prefill_scan_kernel(const PrefillArgs a) {
         // v_new waves
         typedef ScanIn<D, true> In;
         auto step = [&](const In &f, In &fn, int c) {
-            const size_t hn = hc0 + min(c + 2, nc - 1);
+            const int cn = min(c + 2, nc - 1);
             omh_lds_barrier();                   // B1: S tiles of chunk c
-            fn.load_m(a, hn, w, lane);
+            fn.load_m(a, hc0 + cn, hq0 + cn, w, lane);
             v4f P0 = v4zero(), P1 = v4zero();
             scan_times_s<D, true>(f, sm.S, lane, P0, P1);
             scan_interleave_s<NST, NST>();
-            v4f vn;
+            v4f vn, vs;
 #pragma unroll
-            for (int r = 0; r < 4; r++) vn[r] = f.Xf[r] - (P0[r] + P1[r]);
+            for (int r = 0; r < 4; r++) {
+                vn[r] = f.Xf[r] - (P0[r] + P1[r]);
+                vs[r] = vn[r] * f.sc[r];
+            }
             sm.V[j][lane] = vn;
+            sm.Vs[j][lane] = vs;
             omh_lds_barrier();                   // B2: v_new of chunk c
-            fn.load_x(a, hn, cb, w, lane);
-            fn.load_k(a, grs, hn, w, lane);
+            fn.load_x(a, hc0 + cn, cb, w, lane);
+            fn.load_k(a, grs, hc0 + cn, hq0 + cn, w, lane);
             if (owns) {
                 v4f VN[4];
 #pragma unroll
-                for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
+                for (int tt = 0; tt < 4; tt++) VN[tt] = sm.Vs[tt][lane];
                 scan_update_s<D, true>(f, VN, S);
-                scan_interleave_r<16, 6>();
+                scan_interleave_r<16, 7>();
                 sm.S[w][lane] = S;
             }
         };
         In f0, f1, f2;
-        f0.load_m(a, hc0, w, lane);
+        const int c1 = min(1, nc - 1);
+        f0.load_m(a, hc0, hq0, w, lane);
         f0.load_x(a, hc0, cb, w, lane);
-        f0.load_k(a, grs, hc0, w, lane);
-        f1.load_m(a, hc0 + min(1, nc - 1), w, lane);
-        f1.load_x(a, hc0 + min(1, nc - 1), cb, w, lane);
-        f1.load_k(a, grs, hc0 + min(1, nc - 1), w, lane);
+        f0.load_k(a, grs, hc0, hq0, w, lane);
+        f1.load_m(a, hc0 + c1, hq0 + c1, w, lane);
+        f1.load_x(a, hc0 + c1, cb, w, lane);
+        f1.load_k(a, grs, hc0 + c1, hq0 + c1, w, lane);
         for (int c = 0; c < nc; c += 3) {
             step(f0, f2, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
@@ -708,23 +740,29 @@ void prefill_scan_kernel(const PrefillArgs a) {
             }
         };
         auto step = [&](const In &f, In &fn, int c) {
-            const size_t hn = hc0 + min(c + 2, nc - 1);
+            const int cn = min(c + 2, nc - 1);
             omh_lds_barrier();                   // B1: S tiles of chunk c
             if (c > 0) store(c - 1);
-            fn.load_m(a, hn, w, lane);
-            fn.load_x(a, hn, cb, w, lane);
+            fn.load_m(a, hc0 + cn, hq0 + cn, w, lane);
+            fn.load_x(a, hc0 + cn, cb, w, lane);
             v4f O0 = v4zero(), O1 = v4zero();
             scan_times_s<D, false>(f, sm.S, lane, O0, O1);
-            scan_interleave_s<NST, NST + 4>();
+            scan_interleave_s<NST, NST + 5>();
+#pragma unroll
+            for (int r = 0; r < 4; r++) O0[r] = (O0[r] + O1[r]) * f.sc[r];
+            O1 = v4zero();
             omh_lds_barrier();                   // B2: v_new of chunk c
-            fn.load_k(a, grs, hn, w, lane);
+            fn.load_k(a, grs, hc0 + cn, hq0 + cn, w, lane);
+            if (owns) {
+                v4f VS[4];
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) VS[tt] = sm.Vs[tt][lane];
+                scan_update_s<D, false>(f, VS, S);
+                sm.S[w][lane] = S;
+            }
             v4f VN[4];
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
-            if (owns) {
-                scan_update_s<D, false>(f, VN, S);
-                sm.S[w][lane] = S;
-            }
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
@@ -736,12 +774,13 @@ void prefill_scan_kernel(const PrefillArgs a) {
             o = O0 + O1;
         };
         In f0, f1, f2;
-        f0.load_m(a, hc0, w, lane);
+        const int c1 = min(1, nc - 1);
+        f0.load_m(a, hc0, hq0, w, lane);
         f0.load_x(a, hc0, cb, w, lane);
-        f0.load_k(a, grs, hc0, w, lane);
-        f1.load_m(a, hc0 + min(1, nc - 1), w, lane);
-        f1.load_x(a, hc0 + min(1, nc - 1), cb, w, lane);
-        f1.load_k(a, grs, hc0 + min(1, nc - 1), w, lane);
+        f0.load_k(a, grs, hc0, hq0, w, lane);
+        f1.load_m(a, hc0 + c1, hq0 + c1, w, lane);
+        f1.load_x(a, hc0 + c1, cb, w, lane);
+        f1.load_k(a, grs, hc0 + c1, hq0 + c1, w, lane);
         for (int c = 0; c < nc; c += 3) {
             step(f0, f2, c);
             if (c + 1 < nc) step(f1, f0, c + 1);
@@ -793,11 +832,12 @@ bool set_lds_limit() {
 }  // namespace
 
 size_t prefill_scratch_bytes(int D, int kh, int vh, int T) {
-    (void)kh;
     const size_t Tp = (size_t)((T + C - 1) / C) * C, nc = Tp / C;
     size_t n = 0;
     n += align256((size_t)vh * nc * 4);                    // glast
-    n += 3 * align256((size_t)vh * Tp * D * 4);            // pw, pq, pk
+    n += 2 * align256((size_t)vh * Tp * 4);                // pg, pe
+    n += align256((size_t)vh * Tp * D * 4);                // pw
+    n += 2 * align256((size_t)kh * Tp * D * 4);            // pq, pk
     n += align256((size_t)vh * nc * C * C * 4);            // pa
     n += align256((size_t)vh * Tp * D * 4);                // pu
     return n;
@@ -808,9 +848,11 @@ void prefill_bind_scratch(PrefillArgs &a, int D, void *base) {
     char *p = static_cast<char *>(base);
     auto take = [&](size_t bytes) { float *r = reinterpret_cast<float *>(p); p += align256(bytes); return r; };
     a.glast = take((size_t)a.vh * nc * 4);
+    a.pg = take((size_t)a.vh * Tp * 4);
+    a.pe = take((size_t)a.vh * Tp * 4);
     a.pw = take((size_t)a.vh * Tp * D * 4);
-    a.pq = take((size_t)a.vh * Tp * D * 4);
-    a.pk = take((size_t)a.vh * Tp * D * 4);
+    a.pq = take((size_t)a.kh * Tp * D * 4);
+    a.pk = take((size_t)a.kh * Tp * D * 4);
     a.pa = take((size_t)a.vh * nc * C * C * 4);
     a.pu = take((size_t)a.vh * Tp * D * 4);
 }

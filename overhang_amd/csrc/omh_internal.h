@@ -97,7 +97,9 @@ struct PrefillArgs {
     float eps;
     // scratch (device), sized by prefill_scratch_bytes()
     float *glast;                        // exp(cumulative log-decay at chunk end) [vh][nc]
-    float *pw, *pq, *pk, *pa, *pu;       // per-chunk operand panels (WY kernel -> scan)
+    float *pg, *pe;                      // e^{gc}, e^{gc_last - gc} per token [vh][nc][C]
+    float *pw, *pa, *pu;                 // per (value head, chunk) operand panels (WY kernel -> scan)
+    float *pq, *pk;                      // q^, k^ per (key head, chunk), shared by its value heads
 };
 size_t prefill_scratch_bytes(int D, int kh, int vh, int T);
 void prefill_bind_scratch(PrefillArgs &a, int D, void *base);
