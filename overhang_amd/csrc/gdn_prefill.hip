@@ -148,27 +148,28 @@ struct WyShape {
     static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 3 * C) * sizeof(float);
 };
 
-// conv1d (K taps, history oldest..newest, then the input; op order as
-// engines/qwen.c:311-319) + SiLU over NS consecutive tokens, written down an
-// LDS column with row stride PD; tokens at or past nvalid are zero.
-template <int KK, int PD, int NS>
-__device__ __forceinline__ void conv_tokens_impl(const float (&xin)[NS], const float (&hist0)[kConvRing - 1],
-                                                 float4 wv, float *dst, int nvalid) {
+// conv1d (KK taps: the history oldest..newest, then the input; op order as
+// engines/qwen.c:311-319) + SiLU over NS consecutive tokens, the outputs
+// replacing the inputs in registers; tokens at or past nvalid are zero.  The
+// history is right-aligned (the last KK-1 entries of hist0).
+template <int KK, int NS>
+__device__ __forceinline__ void conv_tokens_inplace(float (&x)[NS], const float (&hist0)[kConvRing - 1], float4 wv,
+                                                    int nvalid) {
     const float w[4] = {wv.x, wv.y, wv.z, wv.w};
-    float h[kConvRing - 1];
+    float h[KK - 1];
 #pragma unroll
-    for (int j = 0; j < kConvRing - 1; j++) h[j] = hist0[j];
+    for (int j = 0; j < KK - 1; j++) h[j] = hist0[j + (kConvRing - KK)];
 #pragma unroll
     for (int t = 0; t < NS; t++) {
-        const float x = xin[t];
+        const float xt = x[t];
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < KK - 1; j++) acc += w[j] * h[j];
-        acc += w[KK - 1] * x;
+        acc += w[KK - 1] * xt;
 #pragma unroll
         for (int j = 0; j + 1 < KK - 1; j++) h[j] = h[j + 1];
-        h[KK - 2] = x;
-        dst[t * PD] = t < nvalid ? omh_silu_fast(acc) : 0.f;
+        h[KK - 2] = xt;
+        x[t] = t < nvalid ? omh_silu_fast(acc) : 0.f;
     }
 }
 
@@ -190,55 +191,165 @@ __device__ __forceinline__ void wy_item(int m, int N, int kh, int rep, int &h, i
     h = hk * rep + j;
 }
 
-// Inputs of one work item held in registers (prefetched during the
-// previous item).  The conv work of an item is 3D channels x C tokens,
-// split into units of (channel, NSEG-token segment) dealt round-robin over
-// all threads (NU units each), so every wave does an equal share; a unit's
-// K-1 history is the inputs before its segment (the ring for the first
-// segment of chunk 0).  The gate wave also holds the gate inputs of its token.
+// One work item's conv inputs, held in registers: loaded during the item
+// before (load), turned into conv + SiLU outputs in place while that item's
+// products run (compute), written to LDS when the item starts (store).  The
+// conv work of an item is 3D channels x C tokens, split into units of
+// (channel, NSEG-token segment) dealt round-robin over all threads (NU units
+// each), so every wave does an equal share; a unit's K-1 history is the
+// inputs before its segment (the ring for the first segment of chunk 0).
+// The gate wave also carries the gates of its token.
 template <int D>
 struct WyIn {
     static constexpr int NSEG = 16;
     static constexpr int NUNITS = 3 * D * (C / NSEG);
     static constexpr int NU = (NUNITS + WyShape<D>::NT - 1) / WyShape<D>::NT;
-    float xin[NU][NSEG];
-    float4 hv[NU];        // the K-1 inputs before the segment, in .x .y .z
+    // with 3D a multiple of the wave size a unit's part (q, k or v) and
+    // segment are the same over a wave, so its row addresses are scalar
+    static constexpr bool UNIFORM = (3 * D) % OMH_WAVE == 0;
+    float x[NU][NSEG];    // inputs of the segment, then its conv + SiLU outputs
+    float hv[NU][3];      // the K-1 inputs before the segment
     float4 wv[NU];
-    float ga, gb, galog, gdt;
+    float ga, gb;         // gate inputs of the gate wave's token; then gc and beta
 
-    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_lane,
-                                         int lane) {
-        const int kh = a.kh, K = a.K, T = a.T, t0 = c * C;
-        const int key_dim = kh * D;
+    __device__ __forceinline__ static void unit_of(int unit, int &part, int &seg, int &cc) {
+        const int ch = unit % (3 * D);
+        seg = unit / (3 * D);
+        part = ch / D;
+        cc = ch % D;
+        if (UNIFORM) {
+            seg = __builtin_amdgcn_readfirstlane(seg);
+            part = __builtin_amdgcn_readfirstlane(part);
+        }
+    }
+    __device__ __forceinline__ static int channel(const PrefillArgs &a, int part, int h, int hk) {
+        return part == 0 ? hk * D : (part == 1 ? a.kh * D + hk * D : 2 * a.kh * D + h * D);
+    }
+
+    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_wave, int lane) {
+        const int T = a.T, t0 = c * C;
 #pragma unroll
         for (int u = 0; u < NU; u++) {
             const int unit = tid + u * WyShape<D>::NT;
             if (unit >= NUNITS) continue;
-            const int ch = unit % (3 * D), seg = unit / (3 * D);
-            const int part = ch / D, cc = ch % D;
-            const int gch = part == 0 ? hk * D + cc : (part == 1 ? key_dim + hk * D + cc : 2 * key_dim + h * D + cc);
+            int part, seg, cc;
+            unit_of(unit, part, seg, cc);
+            const float *col = a.qkv + channel(a, part, h, hk);
             const int ts = t0 + seg * NSEG;
+            // rows past T are clamped (their outputs are zeroed); history rows
+            // before 0 are clamped too (chunk 0 takes its history from the ring)
 #pragma unroll
-            for (int t = 0; t < NSEG; t++) xin[u][t] = a.qkv[(size_t)min(ts + t, T - 1) * a.ld_qkv + gch];   // past T: unused
-            wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)gch * kConvRing);
-            // Branch-free: the first segment of chunk 0 takes its history from
-            // the ring at conv time instead (rows clamped to a valid range here).
-            const float *col = a.qkv + gch;
-            const int r0 = ts - (K - 1);
-            hv[u].x = col[(size_t)min(max(r0, 0), T - 1) * a.ld_qkv];
-            hv[u].y = col[(size_t)min(max(r0 + (K > 2 ? 1 : 0), 0), T - 1) * a.ld_qkv];
-            hv[u].z = col[(size_t)min(max(r0 + (K > 3 ? 2 : 0), 0), T - 1) * a.ld_qkv];
-            hv[u].w = 0.f;
+            for (int t = 0; t < NSEG; t++) x[u][t] = (col + (size_t)min(ts + t, T - 1) * a.ld_qkv)[cc];
+#pragma unroll
+            for (int j = 0; j < 3; j++) hv[u][j] = (col + (size_t)min(max(ts - 3 + j, 0), T - 1) * a.ld_qkv)[cc];
+            wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)(channel(a, part, h, hk) + cc) * kConvRing);
         }
-        if (gate_lane) {
+        if (gate_wave) {
             const int tt = min(t0 + lane, T - 1);
             ga = a.a[(size_t)tt * a.ld_ab + h];
             gb = a.b[(size_t)tt * a.ld_ab + h];
-            galog = a.L.A_log[h];
-            gdt = a.L.dt_bias[h];
+        }
+    }
+
+    // conv + SiLU in place (tokens at or past T are zero); on the gate wave
+    // the gates (qwen.c:337-338, zero past T) with an inclusive prefix sum of g
+    __device__ __forceinline__ void compute(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_wave, int lane) {
+        const int T = a.T, K = a.K, t0 = c * C;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const int unit = tid + u * WyShape<D>::NT;
+            if (unit >= NUNITS) continue;
+            int part, seg, cc;
+            unit_of(unit, part, seg, cc);
+            const int nvalid = T - t0 - seg * NSEG;
+            // the inputs before the segment, right-aligned, oldest first
+            float hist[kConvRing - 1];
+            if (t0 + seg * NSEG == 0) {
+                const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
+                const float4 rv = *reinterpret_cast<const float4 *>(
+                    a.L.conv_st + ring_at(a.seq, channel(a, part, h, hk) + cc, (2 * a.kh + a.vh) * D));
+#pragma unroll
+                for (int jj = 0; jj < kConvRing - 1; jj++) {
+                    const int src = jj - (kConvRing - K);
+                    hist[jj] = src >= 0 ? f4_get(rv, ring_slot(ph, K, src)) : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < kConvRing - 1; jj++) hist[jj] = hv[u][jj];
+            }
+            if (K == 4) conv_tokens_inplace<4, NSEG>(x[u], hist, wv[u], nvalid);
+            else if (K == 3) conv_tokens_inplace<3, NSEG>(x[u], hist, wv[u], nvalid);
+            else conv_tokens_inplace<2, NSEG>(x[u], hist, wv[u], nvalid);
+        }
+        if (gate_wave) {
+            float g = 0.f, be = 0.f;
+            if (t0 + lane < T) {
+                g = -expf(a.L.A_log[h]) * omh_softplus(ga + a.L.dt_bias[h]);
+                be = omh_sigmoid(gb);
+            }
+#pragma unroll
+            for (int off = 1; off < OMH_WAVE; off <<= 1) {
+                const float y = __shfl_up(g, off, OMH_WAVE);
+                if (lane >= off) g += y;
+            }
+            ga = g;
+            gb = be;
+        }
+    }
+
+    __device__ __forceinline__ void store(const PrefillArgs &a, size_t hc, int tid, bool gate_wave, int lane, float *Qs,
+                                          float *Ks, float *Vs, float *gcs, float *bs, float *ws) {
+        constexpr int PD = WyShape<D>::PD;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const int unit = tid + u * WyShape<D>::NT;
+            if (unit >= NUNITS) continue;
+            int part, seg, cc;
+            unit_of(unit, part, seg, cc);
+            float *dst = (part == 0 ? Qs : (part == 1 ? Ks : Vs)) + seg * NSEG * PD + cc;
+#pragma unroll
+            for (int t = 0; t < NSEG; t++) dst[t * PD] = x[u][t];
+        }
+        if (gate_wave) {
+            const float gl = __shfl(ga, C - 1, OMH_WAVE);
+            const float ex = expf(ga), ee = expf(gl - ga);
+            gcs[lane] = ga;
+            bs[lane] = gb;
+            ws[lane] = gb * ex;
+            a.pg[hc * C + lane] = ex;
+            a.pe[hc * C + lane] = ee;
+            if (lane == C - 1) a.glast[hc] = ex;
         }
     }
 };
+
+// c + A B for 16x16 tiles: A given as the D layout of A^T (lane holds
+// A[l%16][4g + s] in register s, the A operand of k-step s), B in D layout
+__device__ __forceinline__ v4f mm16(v4f at, v4f b, v4f c) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) c = mfma4(at[s], b[s], c);
+    return c;
+}
+
+// (I + N)^-1 for a strictly lower-triangular 16x16 N: with M = -N (M^16 = 0)
+// it is (I + M)(I + M^2)(I + M^4)(I + M^8), eight 16x16x16 products on the
+// matrix cores.  nd: N in D layout; nt: N^T in D layout.  Returns the
+// inverse's transpose in D layout.
+__device__ __forceinline__ v4f inv_unit_lower16(v4f nd, v4f nt, int lane) {
+    const int l16 = lane % 16, g4 = lane / 16;
+    v4f eye;
+#pragma unroll
+    for (int r = 0; r < 4; r++) eye[r] = 4 * g4 + r == l16 ? 1.f : 0.f;
+    const v4f md = -nd, mt = -nt;
+    const v4f z = v4zero();
+    const v4f m2d = mm16(mt, md, z), m2t = mm16(md, mt, z);
+    const v4f m3t = mm16(m2d, mt, z);                       // (M^3)^T = (M^2)^T M^T
+    const v4f m4d = mm16(m2t, m2d, z), m4t = mm16(m2d, m2t, z);
+    const v4f m8d = mm16(m4t, m4d, z);
+    const v4f p1t = eye + mt + m2t + m3t;                   // (I + M + M^2 + M^3)^T
+    const v4f p2t = mm16(m4d, p1t, p1t);                    // (P1 + P1 M^4)^T
+    return mm16(m8d, p2t, p2t);                             // (P2 + P2 M^8)^T
+}
 
 template <int D>
 __global__ __launch_bounds__(WyShape<D>::NT)
@@ -247,14 +358,14 @@ void prefill_wy_kernel(const PrefillArgs a) {
     constexpr int NW = WS::NW, NT = WS::NT, PD = WS::PD, PC = WS::PC, NCT = WS::NCT;
     constexpr int NST = ScanShape<D>::NST;
 
-    const int kh = a.kh, rep = a.vh / kh, K = a.K, T = a.T;
+    const int kh = a.kh, rep = a.vh / kh;
     const int nitems = a.vh * a.nc;
     const int tid = threadIdx.x, lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
     const int l16 = lane % 16, g4 = lane / 16;
     const bool gate_wave = wave == NW - 1;
 
     extern __shared__ float smem[];
-    float *Qs = smem;                            // [C][PD] q~ -> q^; later W
+    float *Qs = smem;                            // [C][PD] q~ -> q^; W staging in the substitution
     float *Ks = Qs + C * PD;                     // [C][PD]
     float *Vs = Ks + C * PD;                     // [C][PD]
     float *Ls = Vs + C * PD;                     // [C][PC] L
@@ -264,72 +375,32 @@ void prefill_wy_kernel(const PrefillArgs a) {
     float *bs = gcs + C;                         // [C] beta
     float *ws = bs + C;                          // [C] beta e^gc
 
+    // the tiles above the diagonal of L and Aqk stay zero for every item
+    for (int e = tid; e < C * C; e += NT) {
+        const int row = e / C, col = e % C;
+        if (col / 16 > row / 16) { Ls[row * PC + col] = 0.f; As[row * PC + col] = 0.f; }
+    }
+
     int m = blockIdx.x;
     WyIn<D> in;
     if (m < nitems) {
         int h, hk, c;
         wy_item(m, nitems, kh, rep, h, hk, c);
         in.load(a, h, hk, c, tid, gate_wave, lane);
+        in.compute(a, h, hk, c, tid, gate_wave, lane);
     }
     for (; m < nitems; m += gridDim.x) {
         int h, hk, c;
         wy_item(m, nitems, kh, rep, h, hk, c);
-        const int t0 = c * C;
         const size_t hc = (size_t)h * a.nc + c;
+        const int m2 = m + (int)gridDim.x;
+        int h2 = 0, hk2 = 0, c2 = 0;
+        if (m2 < nitems) wy_item(m2, nitems, kh, rep, h2, hk2, c2);
 
-        // 1. conv + SiLU of the q, k channels of key head hk and the v
-        // channels of head h; tokens past T are zero.  Gates on the gate wave
-        // (qwen.c:337-338, zero past T) with an inclusive prefix sum of g.
-#pragma unroll
-        for (int u = 0; u < WyIn<D>::NU; u++) {
-            const int unit = tid + u * NT;
-            if (unit >= WyIn<D>::NUNITS) continue;
-            const int ch = unit % (3 * D), seg = unit / (3 * D);
-            const int part = ch / D, cc = ch % D;
-            constexpr int NS = WyIn<D>::NSEG;
-            float *dst = (part == 0 ? Qs : (part == 1 ? Ks : Vs)) + seg * NS * PD + cc;
-            const int nvalid = T - t0 - seg * NS;
-            float hist[kConvRing - 1];
-            if (t0 + seg * NS == 0) {
-                const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
-                const int gch = part == 0 ? hk * D + cc : (part == 1 ? kh * D + hk * D + cc : 2 * kh * D + h * D + cc);
-                const float4 rv = *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, gch, (2 * kh + a.vh) * D));
-#pragma unroll
-                for (int jj = 0; jj < kConvRing - 1; jj++) hist[jj] = jj < K - 1 ? f4_get(rv, ring_slot(ph, K, jj)) : 0.f;
-            } else {
-                hist[0] = in.hv[u].x; hist[1] = in.hv[u].y; hist[2] = in.hv[u].z;
-            }
-            if (K == 4) conv_tokens_impl<4, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
-            else if (K == 3) conv_tokens_impl<3, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
-            else conv_tokens_impl<2, PD, NS>(in.xin[u], hist, in.wv[u], dst, nvalid);
-        }
-        if (gate_wave) {
-            float g = 0.f, be = 0.f;
-            if (t0 + lane < T) {
-                g = -expf(in.galog) * omh_softplus(in.ga + in.gdt);
-                be = omh_sigmoid(in.gb);
-            }
-            float x = g;
-#pragma unroll
-            for (int off = 1; off < OMH_WAVE; off <<= 1) {
-                const float y = __shfl_up(x, off, OMH_WAVE);
-                if (lane >= off) x += y;
-            }
-            const float gl = __shfl(x, C - 1, OMH_WAVE);
-            const float ex = expf(x), ee = expf(gl - x);
-            gcs[lane] = x;
-            bs[lane] = be;
-            ws[lane] = be * ex;
-            a.pg[hc * C + lane] = ex;
-            a.pe[hc * C + lane] = ee;
-            if (lane == C - 1) a.glast[hc] = ex;
-        }
-        // prefetch the next item's inputs; they land during this item's math
-        if (m + (int)gridDim.x < nitems) {
-            int h2, hk2, c2;
-            wy_item(m + gridDim.x, nitems, kh, rep, h2, hk2, c2);
-            in.load(a, h2, hk2, c2, tid, gate_wave, lane);
-        }
+        // 1. this item's conv outputs and gates (computed during the item
+        // before) into LDS; the next item's inputs start loading
+        in.store(a, hc, tid, gate_wave, lane, Qs, Ks, Vs, gcs, bs, ws);
+        if (m2 < nitems) in.load(a, h2, hk2, c2, tid, gate_wave, lane);
         omh_lds_barrier();
 
         // 2. L2 norm per token over the head's D channels (eps 1e-6), q also
@@ -363,56 +434,57 @@ void prefill_wy_kernel(const PrefillArgs a) {
 
         // 3. G = K K^T (products 0-9) and P = Q K^T (10-19) on the lower
         // tiles, dealt round-robin over the waves; lane group g4 sums the
-        // contiguous k range [g4 D/4, (g4+1) D/4), so operands load as float4.
+        // contiguous k range [g4 D/4, (g4+1) D/4), so operands load as
+        // float4, all of a product's before its first MFMA.  Then the next
+        // item's conv (VALU work beside the other waves' MFMAs).
         for (int p = wave; p < 20; p += NW) {
             int ti, tj;
             lower_tile(p % 10, ti, tj);
             const bool isP = p >= 10;
-            v4f acc = v4zero(), acc2 = v4zero();
             const float *aa = (isP ? Qs : Ks) + (16 * ti + l16) * PD + g4 * (D / 4);
             const float *kb = Ks + (16 * tj + l16) * PD + g4 * (D / 4);
-#pragma unroll 2
+            float4 A[D / 16], B[D / 16];
+#pragma unroll
             for (int s4 = 0; s4 < D / 16; s4++) {
-                const float4 A = *reinterpret_cast<const float4 *>(aa + 4 * s4);
-                const float4 B = *reinterpret_cast<const float4 *>(kb + 4 * s4);
-                acc = mfma4(A.x, B.x, acc);
-                acc2 = mfma4(A.y, B.y, acc2);
-                acc = mfma4(A.z, B.z, acc);
-                acc2 = mfma4(A.w, B.w, acc2);
+                A[s4] = *reinterpret_cast<const float4 *>(aa + 4 * s4);
+                B[s4] = *reinterpret_cast<const float4 *>(kb + 4 * s4);
+            }
+            const float4 gr = *reinterpret_cast<const float4 *>(gcs + 16 * ti + 4 * g4);
+            const float4 br = *reinterpret_cast<const float4 *>(bs + 16 * ti + 4 * g4);
+            const float gcol = gcs[16 * tj + l16];
+            v4f acc = v4zero(), acc2 = v4zero();
+#pragma unroll
+            for (int s4 = 0; s4 < D / 16; s4++) {
+                acc = mfma4(A[s4].x, B[s4].x, acc);
+                acc2 = mfma4(A[s4].y, B[s4].y, acc2);
+                acc = mfma4(A[s4].z, B[s4].z, acc);
+                acc2 = mfma4(A[s4].w, B[s4].w, acc2);
             }
             acc += acc2;
+            const float grr[4] = {gr.x, gr.y, gr.z, gr.w}, brr[4] = {br.x, br.y, br.z, br.w};
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = 16 * ti + 4 * g4 + r, col = 16 * tj + l16;
-                const float dec = col <= row ? expf(gcs[row] - gcs[col]) : 0.f;
-                if (isP) As[row * PC + col] = col <= row ? acc[r] * dec : 0.f;
-                else Ls[row * PC + col] = col < row ? bs[row] * acc[r] * dec : 0.f;
+                const float dec = col <= row ? expf(grr[r] - gcol) : 0.f;
+                if (isP) As[row * PC + col] = acc[r] * dec;
+                else Ls[row * PC + col] = col < row ? brr[r] * acc[r] * dec : 0.f;
             }
         }
-        for (int e = tid; e < C * C; e += NT) {  // upper tiles: zero (never multiplied)
-            const int row = e / C, col = e % C;
-            if (col / 16 > row / 16) { Ls[row * PC + col] = 0.f; As[row * PC + col] = 0.f; }
-        }
+        if (m2 < nitems) in.compute(a, h2, hk2, c2, tid, gate_wave, lane);
         omh_lds_barrier();
 
-        // 4. waves 0-3: diagonal blocks D_b = (I + L_bb)^-1 by forward
-        // substitution, lane jj < 16 keeping column jj (X[i][jj] = -sum_{m<i}
-        // L[i][m] X[m][jj] below the diagonal).  Meanwhile the other waves
-        // (all waves, after, when there are only four) write the panels that
-        // need no inverse: q^, k^T (once per key head) and Aqk, a float4 per lane.
+        // 4. waves 0-3: diagonal blocks D_b = (I + L_bb)^-1 on the matrix
+        // cores.  Meanwhile the other waves (all waves, after, when there are
+        // only four) write the panels that need no inverse: q^, k^T (once per
+        // key head) and Aqk, a float4 per lane.
         if (wave < 4) {
             const int b0 = 16 * wave;
-            float x[16];
+            v4f nd;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float acc = 0.f;
-#pragma unroll
-                for (int mm = 0; mm < i; mm++) acc += Ls[(b0 + i) * PC + b0 + mm] * x[mm];
-                x[i] = lane < i ? -acc : (lane == i ? 1.f : 0.f);
-            }
-            if (lane < 16)
-#pragma unroll
-                for (int i = 0; i < 16; i++) Xs[(b0 + i) * PC + b0 + lane] = x[i];
+            for (int r = 0; r < 4; r++) nd[r] = Ls[(b0 + 4 * g4 + r) * PC + b0 + l16];
+            const v4f nt = *reinterpret_cast<const v4f *>(Ls + (b0 + l16) * PC + b0 + 4 * g4);
+            const v4f xt = inv_unit_lower16(nd, nt, lane);
+            *reinterpret_cast<v4f *>(Xs + (b0 + l16) * PC + b0 + 4 * g4) = xt;   // row l16 of D_b
         }
         {
             constexpr int PW = NW > 4 ? NW - 4 : NW;         // panel-writing waves
@@ -445,64 +517,77 @@ void prefill_wy_kernel(const PrefillArgs a) {
         omh_lds_barrier();
 
         // 5. W and U by blocked forward substitution on (I + L) [W | U] =
-        // [K beta e^gc | V beta]: row tile i = D_i (RHS_i - sum_{k<i} L_ik R_k),
-        // column tile by column tile, the tiles kept in registers in MFMA D
-        // layout (a D-layout tile feeds the B operand directly: at k-step s
-        // lane group g supplies row 4g+s).  Each wave takes the W and the U
-        // tile of one column (two independent chains).  U goes straight to
-        // its panel (the scan's D layout); W is staged in Qs.
-        for (int q = wave; q < 2 * NCT; q += 2 * NW) {
-            const int tn = q % NCT;
-            const bool two = q + NW < 2 * NCT;           // this wave also has the U tile of column tn
-            const bool firstU = q >= NCT;
-            v4f R0[4], R1[4];
+        // [K beta e^gc | V beta], one 16-column tile per chain:
+        //   R_i = D_i (RHS_i - sum_{k<i} L_ik R_k),
+        // the tiles in registers in MFMA D layout (a D-layout tile feeds the
+        // B operand directly: at k-step s lane group g supplies row 4g+s),
+        // each R_k subtracted from every later row tile as soon as it is
+        // known.  With D/16 waves each takes the W and the U chain of one
+        // column tile; with fewer columns, one chain each.  U goes straight
+        // to its panel (the scan's D layout); W is transposed through the
+        // wave's own columns of Qs (no other wave reads them now) into the
+        // W panel's fragment order.
+        {
+            constexpr bool TWO = NCT == NW;
+            constexpr int NCH = TWO ? 2 : 1;
+            const int q = wave;
+            if (TWO || q < 2 * NCT) {
+                const int tn = TWO ? q : q % NCT;
+                const bool onlyU = !TWO && q >= NCT;
+                v4f R[NCH][4];
+                // right-hand sides (chain 0: W or U; chain 1: U)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v4f acc0, acc1;
+                for (int ch = 0; ch < NCH; ch++) {
+                    const bool isU = ch == 1 || onlyU;
+                    const float *src = (isU ? Vs : Ks) + 16 * tn + l16;
+                    const float *scl = (isU ? bs : ws) + 4 * g4;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = 16 * i + 4 * g4 + r;
-                    acc0[r] = firstU ? Vs[row * PD + 16 * tn + l16] * bs[row] : Ks[row * PD + 16 * tn + l16] * ws[row];
-                    acc1[r] = two ? Vs[row * PD + 16 * tn + l16] * bs[row] : 0.f;
-                }
-#pragma unroll
-                for (int k = 0; k < i; k++)
-#pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        const float nl = -Ls[(16 * i + l16) * PC + 16 * k + 4 * g4 + s];
-                        acc0 = mfma4(nl, R0[k][s], acc0);
-                        acc1 = mfma4(nl, R1[k][s], acc1);
+                    for (int i = 0; i < 4; i++) {
+                        const float4 sv = *reinterpret_cast<const float4 *>(scl + 16 * i);
+                        R[ch][i][0] = src[(16 * i + 4 * g4 + 0) * PD] * sv.x;
+                        R[ch][i][1] = src[(16 * i + 4 * g4 + 1) * PD] * sv.y;
+                        R[ch][i][2] = src[(16 * i + 4 * g4 + 2) * PD] * sv.z;
+                        R[ch][i][3] = src[(16 * i + 4 * g4 + 3) * PD] * sv.w;
                     }
-                R0[i] = v4zero();
-                R1[i] = v4zero();
-#pragma unroll
-                for (int s = 0; s < 4; s++) {
-                    const float dv = Xs[(16 * i + l16) * PC + 16 * i + 4 * g4 + s];
-                    R0[i] = mfma4(dv, acc0[s], R0[i]);
-                    R1[i] = mfma4(dv, acc1[s], R1[i]);
                 }
-            }
+                v4f Xd[4], Ln[6];        // D_i and -L_ik (k < i) as A operands
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < 4; i++) Xd[i] = *reinterpret_cast<const v4f *>(Xs + (16 * i + l16) * PC + 16 * i + 4 * g4);
+#pragma unroll
+                for (int i = 1, n = 0; i < 4; i++)
+#pragma unroll
+                    for (int k = 0; k < i; k++, n++)
+                        Ln[n] = -*reinterpret_cast<const v4f *>(Ls + (16 * i + l16) * PC + 16 * k + 4 * g4);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+#pragma unroll
+                    for (int ch = 0; ch < NCH; ch++) R[ch][i] = mm16(Xd[i], R[ch][i], v4zero());
+#pragma unroll
+                    for (int i2 = i + 1; i2 < 4; i2++)
+#pragma unroll
+                        for (int ch = 0; ch < NCH; ch++)
+                            R[ch][i2] = mm16(Ln[i2 * (i2 - 1) / 2 + i], R[ch][i], R[ch][i2]);
+                }
                 // U panel of column block tn, token tile i (the D layout of R)
-                float *up = a.pu + pan4(hc * NCT + tn, i, lane);
-                if (firstU) {
-                    *reinterpret_cast<v4f *>(up) = R0[i];
-                } else {
+                if (TWO || onlyU)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) Qs[(16 * i + 4 * g4 + r) * PD + 16 * tn + l16] = R0[i][r];
-                    if (two) *reinterpret_cast<v4f *>(up) = R1[i];
+                    for (int i = 0; i < 4; i++)
+                        *reinterpret_cast<v4f *>(a.pu + pan4(hc * NCT + tn, i, lane)) = R[NCH - 1][i];
+                if (TWO || !onlyU) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) Qs[(16 * i + 4 * g4 + r) * PD + 16 * tn + l16] = R[0][i][r];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    // W panel, k-group tn of token tile tt
+#pragma unroll
+                    for (int tt = 0; tt < 4; tt++)
+                        *reinterpret_cast<float4 *>(a.pw + panj<D>(hc, tt, tn, lane)) =
+                            *reinterpret_cast<const float4 *>(Qs + (16 * tt + l16) * PD + 16 * tn + 4 * g4);
                 }
             }
-        }
-        omh_lds_barrier();
-
-        // 6. W panel (the Q panel's order)
-        for (int e = tid; e < NST * 4 * OMH_WAVE; e += NT) {
-            const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
-            const int row = tt * 16 + l % 16, col = 16 * w + 4 * (l / 16);
-            *reinterpret_cast<float4 *>(a.pw + panj<D>(hc, tt, w, l)) =
-                *reinterpret_cast<const float4 *>(Qs + row * PD + col);
         }
         omh_lds_barrier();                       // LDS is reused by the next item
     }
