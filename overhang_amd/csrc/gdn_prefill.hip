@@ -30,6 +30,7 @@
 // S and v_new in registers this way for the whole scan.
 #include "omh_device.h"
 #include "omh_internal.h"
+#include <type_traits>
 
 namespace omh {
 namespace {
@@ -148,28 +149,36 @@ struct WyShape {
     static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 3 * C) * sizeof(float);
 };
 
-// conv1d (KK taps: the history oldest..newest, then the input; op order as
-// engines/qwen.c:311-319) + SiLU over NS consecutive tokens, the outputs
-// replacing the inputs in registers; tokens at or past nvalid are zero.  The
-// history is right-aligned (the last KK-1 entries of hist0).
+// conv1d over KK taps (the history oldest..newest, then the input; op
+// order as engines/qwen.c:311-319) + SiLU over NS consecutive tokens, the
+// outputs replacing the inputs in registers; tokens at or past nvalid are
+// zero.  The history h0 h1 h2 is the last three inputs (right-aligned: for
+// KK < 4 only the last KK-1 are used), w the taps 0..KK-1.
 template <int KK, int NS>
-__device__ __forceinline__ void conv_tokens_inplace(float (&x)[NS], const float (&hist0)[kConvRing - 1], float4 wv,
-                                                    int nvalid) {
-    const float w[4] = {wv.x, wv.y, wv.z, wv.w};
-    float h[KK - 1];
-#pragma unroll
-    for (int j = 0; j < KK - 1; j++) h[j] = hist0[j + (kConvRing - KK)];
+__device__ __forceinline__ void conv_inplace(float (&x)[NS], float h0, float h1, float h2, float4 w, int nvalid) {
+    const float wt[4] = {w.x, w.y, w.z, w.w};
+    float h[3] = {h0, h1, h2};
 #pragma unroll
     for (int t = 0; t < NS; t++) {
         const float xt = x[t];
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < KK - 1; j++) acc += w[j] * h[j];
-        acc += w[KK - 1] * xt;
-#pragma unroll
-        for (int j = 0; j + 1 < KK - 1; j++) h[j] = h[j + 1];
-        h[KK - 2] = xt;
-        x[t] = t < nvalid ? omh_silu_fast(acc) : 0.f;
+        for (int j = 0; j < KK - 1; j++) acc += wt[j] * h[3 - (KK - 1) + j];
+        acc += wt[KK - 1] * xt;
+        h[0] = h[1];
+        h[1] = h[2];
+        h[2] = xt;
+        const float y = omh_silu_fast(acc);
+        x[t] = t < nvalid ? y : 0.f;
+    }
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>)
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
     }
 }
 
@@ -193,13 +202,13 @@ __device__ __forceinline__ void wy_item(int m, int N, int kh, int rep, int &h, i
 
 // One work item's conv inputs, held in registers: loaded during the item
 // before (load), turned into conv + SiLU outputs in place while that item's
-// products run (compute), written to LDS when the item starts (store).  The
-// conv work of an item is 3D channels x C tokens, split into units of
-// (channel, NSEG-token segment) dealt round-robin over all threads (NU units
-// each), so every wave does an equal share; a unit's K-1 history is the
-// inputs before its segment (the ring for the first segment of chunk 0).
-// The gate wave also carries the gates of its token.
-template <int D>
+// products run (compute_unit, gates), written to LDS when the item starts
+// (store).  The conv work of an item is 3D channels x C tokens, split into
+// units of (channel, NSEG-token segment) dealt round-robin over all threads
+// (NU units each), so every wave does an equal share; a unit's history is
+// the three inputs before its segment (for the first segment of chunk 0 the
+// channel's ring entry).  The gate wave also carries the gates of its token.
+template <int D, int KK>
 struct WyIn {
     static constexpr int NSEG = 16;
     static constexpr int NUNITS = 3 * D * (C / NSEG);
@@ -208,7 +217,7 @@ struct WyIn {
     // segment are the same over a wave, so its row addresses are scalar
     static constexpr bool UNIFORM = (3 * D) % OMH_WAVE == 0;
     float x[NU][NSEG];    // inputs of the segment, then its conv + SiLU outputs
-    float hv[NU][3];      // the K-1 inputs before the segment
+    float4 hv[NU];        // the three inputs before the segment in .x .y .z
     float4 wv[NU];
     float ga, gb;         // gate inputs of the gate wave's token; then gc and beta
 
@@ -226,75 +235,82 @@ struct WyIn {
         return part == 0 ? hk * D : (part == 1 ? a.kh * D + hk * D : 2 * a.kh * D + h * D);
     }
 
-    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_wave, int lane) {
+    // ph: the sequence's ring phase
+    // units U0 .. U1-1 (and the gate inputs on the gate wave if gate)
+    template <int U0, int U1>
+    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate, int lane, int ph) {
         const int T = a.T, t0 = c * C;
+        const size_t ld = a.ld_qkv;
 #pragma unroll
-        for (int u = 0; u < NU; u++) {
+        for (int u = U0; u < (U1 < NU ? U1 : NU); u++) {
             const int unit = tid + u * WyShape<D>::NT;
             if (unit >= NUNITS) continue;
             int part, seg, cc;
             unit_of(unit, part, seg, cc);
-            const float *col = a.qkv + channel(a, part, h, hk);
+            const int ch0 = channel(a, part, h, hk);
             const int ts = t0 + seg * NSEG;
-            // rows past T are clamped (their outputs are zeroed); history rows
-            // before 0 are clamped too (chunk 0 takes its history from the ring)
+            float h0, h1, h2;
+            if (ts >= 3 && ts + NSEG <= T) {
+                // rows ts-3 .. ts+NSEG-1, one row pointer stepped down the column
+                const float *rp = a.qkv + (size_t)(ts - 3) * ld + ch0;
+                h0 = rp[cc]; rp += ld;
+                h1 = rp[cc]; rp += ld;
+                h2 = rp[cc]; rp += ld;
 #pragma unroll
-            for (int t = 0; t < NSEG; t++) x[u][t] = (col + (size_t)min(ts + t, T - 1) * a.ld_qkv)[cc];
+                for (int t = 0; t < NSEG; t++) { x[u][t] = rp[cc]; rp += ld; }
+            } else {
+                // the last segment (rows past T are clamped; their outputs
+                // are zeroed) or the first of the sequence (history: the ring)
+                const float *col = a.qkv + ch0 + cc;
 #pragma unroll
-            for (int j = 0; j < 3; j++) hv[u][j] = (col + (size_t)min(max(ts - 3 + j, 0), T - 1) * a.ld_qkv)[cc];
-            wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)(channel(a, part, h, hk) + cc) * kConvRing);
+                for (int t = 0; t < NSEG; t++) x[u][t] = col[(size_t)min(ts + t, T - 1) * ld];
+                if (ts == 0) {
+                    // the ring's K-1 history slots, oldest first, right-aligned
+                    // (this waits for the load: once per sequence)
+                    const float4 rv =
+                        *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, ch0 + cc, (2 * a.kh + a.vh) * D));
+                    h0 = KK >= 4 ? f4_get(rv, ring_slot(ph, KK, KK - 4)) : 0.f;
+                    h1 = KK >= 3 ? f4_get(rv, ring_slot(ph, KK, KK - 3)) : 0.f;
+                    h2 = f4_get(rv, ring_slot(ph, KK, KK - 2));
+                } else {
+                    h0 = col[(size_t)min(ts - 3, T - 1) * ld];
+                    h1 = col[(size_t)min(ts - 2, T - 1) * ld];
+                    h2 = col[(size_t)min(ts - 1, T - 1) * ld];
+                }
+            }
+            hv[u] = make_float4(h0, h1, h2, 0.f);
+            wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)(ch0 + cc) * kConvRing);
         }
-        if (gate_wave) {
+        if (gate) {
             const int tt = min(t0 + lane, T - 1);
             ga = a.a[(size_t)tt * a.ld_ab + h];
             gb = a.b[(size_t)tt * a.ld_ab + h];
         }
     }
 
-    // conv + SiLU in place (tokens at or past T are zero); on the gate wave
+    // conv + SiLU of unit u in place, branch-free
+    __device__ __forceinline__ void compute_unit(const PrefillArgs &a, int u, int c, int tid) {
+        const int unit = tid + u * WyShape<D>::NT;
+        if (NUNITS % WyShape<D>::NT != 0 && unit >= NUNITS) return;
+        int part, seg, cc;
+        unit_of(unit, part, seg, cc);
+        conv_inplace<KK, NSEG>(x[u], hv[u].x, hv[u].y, hv[u].z, wv[u], a.T - (c * C + seg * NSEG));
+    }
+
     // the gates (qwen.c:337-338, zero past T) with an inclusive prefix sum of g
-    __device__ __forceinline__ void compute(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate_wave, int lane) {
-        const int T = a.T, K = a.K, t0 = c * C;
-#pragma unroll
-        for (int u = 0; u < NU; u++) {
-            const int unit = tid + u * WyShape<D>::NT;
-            if (unit >= NUNITS) continue;
-            int part, seg, cc;
-            unit_of(unit, part, seg, cc);
-            const int nvalid = T - t0 - seg * NSEG;
-            // the inputs before the segment, right-aligned, oldest first
-            float hist[kConvRing - 1];
-            if (t0 + seg * NSEG == 0) {
-                const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
-                const float4 rv = *reinterpret_cast<const float4 *>(
-                    a.L.conv_st + ring_at(a.seq, channel(a, part, h, hk) + cc, (2 * a.kh + a.vh) * D));
-#pragma unroll
-                for (int jj = 0; jj < kConvRing - 1; jj++) {
-                    const int src = jj - (kConvRing - K);
-                    hist[jj] = src >= 0 ? f4_get(rv, ring_slot(ph, K, src)) : 0.f;
-                }
-            } else {
-#pragma unroll
-                for (int jj = 0; jj < kConvRing - 1; jj++) hist[jj] = hv[u][jj];
-            }
-            if (K == 4) conv_tokens_inplace<4, NSEG>(x[u], hist, wv[u], nvalid);
-            else if (K == 3) conv_tokens_inplace<3, NSEG>(x[u], hist, wv[u], nvalid);
-            else conv_tokens_inplace<2, NSEG>(x[u], hist, wv[u], nvalid);
+    __device__ __forceinline__ void gates(const PrefillArgs &a, int h, int c, int lane) {
+        float g = 0.f, be = 0.f;
+        if (c * C + lane < a.T) {
+            g = -expf(a.L.A_log[h]) * omh_softplus(ga + a.L.dt_bias[h]);
+            be = omh_sigmoid(gb);
         }
-        if (gate_wave) {
-            float g = 0.f, be = 0.f;
-            if (t0 + lane < T) {
-                g = -expf(a.L.A_log[h]) * omh_softplus(ga + a.L.dt_bias[h]);
-                be = omh_sigmoid(gb);
-            }
 #pragma unroll
-            for (int off = 1; off < OMH_WAVE; off <<= 1) {
-                const float y = __shfl_up(g, off, OMH_WAVE);
-                if (lane >= off) g += y;
-            }
-            ga = g;
-            gb = be;
+        for (int off = 1; off < OMH_WAVE; off <<= 1) {
+            const float y = __shfl_up(g, off, OMH_WAVE);
+            if (lane >= off) g += y;
         }
+        ga = g;
+        gb = be;
     }
 
     __device__ __forceinline__ void store(const PrefillArgs &a, size_t hc, int tid, bool gate_wave, int lane, float *Qs,
@@ -351,7 +367,7 @@ __device__ __forceinline__ v4f inv_unit_lower16(v4f nd, v4f nt, int lane) {
     return mm16(m8d, p2t, p2t);                             // (P2 + P2 M^8)^T
 }
 
-template <int D>
+template <int D, int KK>
 __global__ __launch_bounds__(WyShape<D>::NT)
 void prefill_wy_kernel(const PrefillArgs a) {
     using WS = WyShape<D>;
@@ -360,7 +376,8 @@ void prefill_wy_kernel(const PrefillArgs a) {
 
     const int kh = a.kh, rep = a.vh / kh;
     const int nitems = a.vh * a.nc;
-    const int tid = threadIdx.x, lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
     const int l16 = lane % 16, g4 = lane / 16;
     const bool gate_wave = wave == NW - 1;
 
@@ -381,13 +398,16 @@ void prefill_wy_kernel(const PrefillArgs a) {
         if (col / 16 > row / 16) { Ls[row * PC + col] = 0.f; As[row * PC + col] = 0.f; }
     }
 
+    const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];   // ring phase of the sequence
     int m = blockIdx.x;
-    WyIn<D> in;
+    WyIn<D, KK> in;
     if (m < nitems) {
         int h, hk, c;
         wy_item(m, nitems, kh, rep, h, hk, c);
-        in.load(a, h, hk, c, tid, gate_wave, lane);
-        in.compute(a, h, hk, c, tid, gate_wave, lane);
+        in.template load<0, WyIn<D, KK>::NU>(a, h, hk, c, tid, gate_wave, lane, ph);
+#pragma unroll
+        for (int u = 0; u < WyIn<D, KK>::NU; u++) in.compute_unit(a, u, c, tid);
+        if (gate_wave) in.gates(a, h, c, lane);
     }
     for (; m < nitems; m += gridDim.x) {
         int h, hk, c;
@@ -400,7 +420,9 @@ void prefill_wy_kernel(const PrefillArgs a) {
         // 1. this item's conv outputs and gates (computed during the item
         // before) into LDS; the next item's inputs start loading
         in.store(a, hc, tid, gate_wave, lane, Qs, Ks, Vs, gcs, bs, ws);
-        if (m2 < nitems) in.load(a, h2, hk2, c2, tid, gate_wave, lane);
+        // (spread over phases 1-3: one unit each, so the misses of one
+        // burst are in flight while the next phase computes)
+        if (m2 < nitems) in.template load<0, 1>(a, h2, hk2, c2, tid, gate_wave, lane, ph);
         omh_lds_barrier();
 
         // 2. L2 norm per token over the head's D channels (eps 1e-6), q also
@@ -430,47 +452,85 @@ void prefill_wy_kernel(const PrefillArgs a) {
                 }
             }
         }
+        if (m2 < nitems) in.template load<1, 2>(a, h2, hk2, c2, tid, false, lane, ph);
         omh_lds_barrier();
 
-        // 3. G = K K^T (products 0-9) and P = Q K^T (10-19) on the lower
-        // tiles, dealt round-robin over the waves; lane group g4 sums the
-        // contiguous k range [g4 D/4, (g4+1) D/4), so operands load as
-        // float4, all of a product's before its first MFMA.  Then the next
-        // item's conv (VALU work beside the other waves' MFMAs).
-        for (int p = wave; p < 20; p += NW) {
+        // 3. G = K K^T and P = Q K^T on the ten lower 16x16 tiles each:
+        // wave w takes G tiles w, w + NW, ... and P tiles (w + 2) mod NW, ...,
+        // five products per SIMD.  Lane group g4 sums the contiguous k range
+        // [g4 D/4, (g4+1) D/4), so operands load as float4, all of a
+        // product's before its first MFMA.  Each product shares a basic block
+        // with one unit of the next item's conv, so the conv's VALU work can
+        // issue between the MFMAs.
+        auto product = [&](auto isPc, int t) {
+            constexpr bool isP = decltype(isPc)::value;
             int ti, tj;
-            lower_tile(p % 10, ti, tj);
-            const bool isP = p >= 10;
+            lower_tile(t, ti, tj);
             const float *aa = (isP ? Qs : Ks) + (16 * ti + l16) * PD + g4 * (D / 4);
             const float *kb = Ks + (16 * tj + l16) * PD + g4 * (D / 4);
-            float4 A[D / 16], B[D / 16];
-#pragma unroll
-            for (int s4 = 0; s4 < D / 16; s4++) {
-                A[s4] = *reinterpret_cast<const float4 *>(aa + 4 * s4);
-                B[s4] = *reinterpret_cast<const float4 *>(kb + 4 * s4);
-            }
             const float4 gr = *reinterpret_cast<const float4 *>(gcs + 16 * ti + 4 * g4);
-            const float4 br = *reinterpret_cast<const float4 *>(bs + 16 * ti + 4 * g4);
             const float gcol = gcs[16 * tj + l16];
+            float4 br = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (!isP) br = *reinterpret_cast<const float4 *>(bs + 16 * ti + 4 * g4);
             v4f acc = v4zero(), acc2 = v4zero();
+            // operands in groups of up to four float4 pairs (bounded registers)
+            constexpr int NS4 = D / 16, GS = NS4 < 4 ? NS4 : 4;
 #pragma unroll
-            for (int s4 = 0; s4 < D / 16; s4++) {
-                acc = mfma4(A[s4].x, B[s4].x, acc);
-                acc2 = mfma4(A[s4].y, B[s4].y, acc2);
-                acc = mfma4(A[s4].z, B[s4].z, acc);
-                acc2 = mfma4(A[s4].w, B[s4].w, acc2);
+            for (int s0 = 0; s0 < NS4; s0 += GS) {
+                float4 A[GS], B[GS];
+#pragma unroll
+                for (int q = 0; q < GS; q++) {
+                    A[q] = *reinterpret_cast<const float4 *>(aa + 4 * (s0 + q));
+                    B[q] = *reinterpret_cast<const float4 *>(kb + 4 * (s0 + q));
+                }
+#pragma unroll
+                for (int q = 0; q < GS; q++) {
+                    acc = mfma4(A[q].x, B[q].x, acc);
+                    acc2 = mfma4(A[q].y, B[q].y, acc2);
+                    acc = mfma4(A[q].z, B[q].z, acc);
+                    acc2 = mfma4(A[q].w, B[q].w, acc2);
+                }
             }
             acc += acc2;
             const float grr[4] = {gr.x, gr.y, gr.z, gr.w}, brr[4] = {br.x, br.y, br.z, br.w};
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = 16 * ti + 4 * g4 + r, col = 16 * tj + l16;
-                const float dec = col <= row ? expf(grr[r] - gcol) : 0.f;
-                if (isP) As[row * PC + col] = acc[r] * dec;
-                else Ls[row * PC + col] = col < row ? brr[r] * acc[r] * dec : 0.f;
+                // gc falls along the chunk, so the exponent is <= 0 where used
+                const float e = expf(fminf(grr[r] - gcol, 0.f));
+                // Aqk keeps the diagonal; L is strictly lower and carries beta
+                if (isP) As[row * PC + col] = col <= row ? acc[r] * e : 0.f;
+                else Ls[row * PC + col] = col < row ? brr[r] * acc[r] * e : 0.f;
             }
+        };
+        if (m2 < nitems) in.template load<2, WyIn<D, KK>::NU>(a, h2, hk2, c2, tid, false, lane, ph);
+        {
+            constexpr int R = (10 + NW - 1) / NW;            // rounds of each product type
+            constexpr int NU = WyIn<D, KK>::NU;
+            const int tp0 = (wave + 2) % NW;
+            auto conv_unit = [&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                if (u < NU) in.compute_unit(a, u < NU ? u : 0, c2, tid);
+            };
+            static_for<R>([&](auto kc) {
+                constexpr int k = decltype(kc)::value;
+                const int tg = wave + NW * k, tq = tp0 + NW * k;
+                if (tg < 10) {
+                    product(std::false_type{}, tg);
+                    conv_unit(std::integral_constant<int, 2 * k>{});
+                } else {
+                    conv_unit(std::integral_constant<int, 2 * k>{});
+                }
+                if (tq < 10) {
+                    product(std::true_type{}, tq);
+                    conv_unit(std::integral_constant<int, 2 * k + 1>{});
+                } else {
+                    conv_unit(std::integral_constant<int, 2 * k + 1>{});
+                }
+            });
+            static_assert(2 * R >= NU, "every conv unit has a slot");
+            if (gate_wave) in.gates(a, h2, c2, lane);
         }
-        if (m2 < nitems) in.compute(a, h2, hk2, c2, tid, gate_wave, lane);
         omh_lds_barrier();
 
         // 4. waves 0-3: diagonal blocks D_b = (I + L_bb)^-1 on the matrix
@@ -899,7 +959,9 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     const int nitems = a.vh * a.nc;
     const int grid = nitems < wy_grid() ? nitems : wy_grid();
     // the WY kernel reads the ring for chunk 0 before the commit rewrites it
-    hipLaunchKernelGGL((prefill_wy_kernel<D>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
+    if (a.K == 4) hipLaunchKernelGGL((prefill_wy_kernel<D, 4>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
+    else if (a.K == 3) hipLaunchKernelGGL((prefill_wy_kernel<D, 3>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
+    else hipLaunchKernelGGL((prefill_wy_kernel<D, 2>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     hipLaunchKernelGGL(prefill_conv_commit_kernel, dim3((conv_dim + 255) / 256), dim3(256), 0, st, a, conv_dim);
     hipLaunchKernelGGL((prefill_scan_kernel<D>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
     constexpr int RPB = 256 / (D / 4);
@@ -910,8 +972,11 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
 
 template <int D>
 bool set_lds_limit() {
-    return hipFuncSetAttribute((const void *)prefill_wy_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)WyShape<D>::LDS) == hipSuccess;
+    bool ok = true;
+    for (const void *f : {(const void *)prefill_wy_kernel<D, 2>, (const void *)prefill_wy_kernel<D, 3>,
+                          (const void *)prefill_wy_kernel<D, 4>})
+        ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)WyShape<D>::LDS) == hipSuccess;
+    return ok;
 }
 
 }  // namespace
