@@ -130,13 +130,14 @@ void prefill_gated_norm_kernel(const PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- P1 WY
-// One workgroup per (value head h, chunk c): the chunk's conv + SiLU and
-// L2 norms straight from mixed_qkv, the gates, then on fp32 MFMA
-//   G = K K^T, P = Q K^T (lower 16x16 tiles), L = strict_lower(beta_i G e^{gc_i-gc_j}),
-//   Aqk = lower_incl(P e^{gc_i-gc_j}), X = (I + L)^-1 (blocked: four 16x16
-//   diagonal inverses by forward substitution in parallel, then the
-//   off-diagonal blocks level by level, X_ij = -D_i sum_k L_ik X_kj),
-//   W = X (K beta e^gc), U = X (V beta),
+// One workgroup per (key head, chunk, group of one or two of its value
+// heads): the chunk's conv + SiLU and L2 norms straight from mixed_qkv, the
+// gates, then on fp32 MFMA
+//   G = K K^T, P = Q K^T (lower 16x16 tiles; shared by the group's value heads),
+//   per value head: L = strict_lower(beta_i G e^{gc_i-gc_j}),
+//   Aqk = lower_incl(P e^{gc_i-gc_j}), X = (I + L)^-1 (four 16x16 diagonal
+//   inverses, then blocked forward substitution), W = X (K beta e^gc),
+//   U = X (V beta),
 // and the operand panels the scan reads.  Threads exchange data through
 // LDS only, so every barrier orders LDS alone: the next item's prefetched
 // inputs and this item's panel stores stay in flight across them.
@@ -146,7 +147,8 @@ struct WyShape {
     static constexpr int NT = NW * OMH_WAVE;
     static constexpr int PD = D + 4, PC = C + 4;         // padded LDS rows
     static constexpr int NCT = D / 16;                   // 16-column tiles of D
-    static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 3 * C) * sizeof(float);
+    // Qs Ks Vs, Ls Xs As, then gc, beta, beta e^gc for two value heads
+    static constexpr size_t LDS = (size_t)(3 * C * PD + 3 * C * PC + 6 * C) * sizeof(float);
 };
 
 // conv1d over KK taps (the history oldest..newest, then the input; op
@@ -188,74 +190,71 @@ __device__ __forceinline__ void lower_tile(int it, int &i, int &j) {
     j = it - i * (i + 1) / 2;
 }
 
-// Work item m -> (value head, chunk), XCD-aware: with N items and a grid
-// that is a multiple of 8, the items a given XCD processes together are
-// consecutive (the value heads of one key head, then the next key head, for
-// one chunk), so the q/k inputs they share are read once per XCD L2.
-__device__ __forceinline__ void wy_item(int m, int N, int kh, int rep, int &h, int &hk, int &c) {
+// Work item m -> (key head hk, first value head h0, chunk c) for items of
+// vpg value heads each (ngrp groups per key head), XCD-aware: with N items
+// and a grid that is a multiple of 8, the items a given XCD processes
+// together are consecutive (the groups of one key head, then the next key
+// head, for one chunk), so the q/k inputs they share are read once per XCD L2.
+__device__ __forceinline__ void wy_item(int m, int N, int kh, int rep, int vpg, int &hk, int &h0, int &c, int &grp) {
+    const int ngrp = rep / vpg;
     const int mm = N % 8 == 0 ? (m % 8) * (N / 8) + m / 8 : m;
-    const int j = mm % rep;
-    hk = (mm / rep) % kh;
-    c = mm / (rep * kh);
-    h = hk * rep + j;
+    grp = mm % ngrp;
+    hk = (mm / ngrp) % kh;
+    c = mm / (ngrp * kh);
+    h0 = hk * rep + grp * vpg;
 }
 
 // One work item's conv inputs, held in registers: loaded during the item
-// before (load), turned into conv + SiLU outputs in place while that item's
-// products run (compute_unit, gates), written to LDS when the item starts
-// (store).  The conv work of an item is 3D channels x C tokens, split into
-// units of (channel, NSEG-token segment) dealt round-robin over all threads
-// (NU units each), so every wave does an equal share; a unit's history is
-// the three inputs before its segment (for the first segment of chunk 0 the
-// channel's ring entry).  The gate wave also carries the gates of its token.
+// before (load), turned into conv + SiLU outputs in place during that item
+// (compute_unit, gates), written to LDS when they are needed (store; the
+// second value head's v when its turn comes, store_v1).  Unit u of a thread
+// is part u (q, k, v of value head 0, v of value head 1) of one (channel,
+// NSEG-token segment) pair, so the second value head's v has registers of
+// its own; a unit's history is the three inputs before its segment (for
+// the first segment of chunk 0 the channel's ring entry).  Gate wave j
+// (NW-1-j) carries the gates of value head j of the item for its token.
 template <int D, int KK>
 struct WyIn {
     static constexpr int NSEG = 16;
-    static constexpr int NUNITS = 3 * D * (C / NSEG);
-    static constexpr int NU = (NUNITS + WyShape<D>::NT - 1) / WyShape<D>::NT;
-    // with 3D a multiple of the wave size a unit's part (q, k or v) and
-    // segment are the same over a wave, so its row addresses are scalar
-    static constexpr bool UNIFORM = (3 * D) % OMH_WAVE == 0;
-    float x[NU][NSEG];    // inputs of the segment, then its conv + SiLU outputs
-    float4 hv[NU];        // the three inputs before the segment in .x .y .z
-    float4 wv[NU];
+    static constexpr int NT = WyShape<D>::NT;
+    static constexpr int NPAIR = D * (C / NSEG);            // (channel, segment) pairs per part
+    static_assert(NPAIR <= NT, "one pair per thread and part");
+    float x[4][NSEG];     // inputs of the segment, then its conv + SiLU outputs
+    float4 hv[4];         // the three inputs before the segment in .x .y .z
+    float4 wv[4];
     float ga, gb;         // gate inputs of the gate wave's token; then gc and beta
 
-    __device__ __forceinline__ static void unit_of(int unit, int &part, int &seg, int &cc) {
-        const int ch = unit % (3 * D);
-        seg = unit / (3 * D);
-        part = ch / D;
-        cc = ch % D;
-        if (UNIFORM) {
-            seg = __builtin_amdgcn_readfirstlane(seg);
-            part = __builtin_amdgcn_readfirstlane(part);
-        }
+    __device__ __forceinline__ static int channel(const PrefillArgs &a, int part, int h0, int hk) {
+        return part == 0 ? hk * D : (part == 1 ? a.kh * D + hk * D : 2 * a.kh * D + (h0 + part - 2) * D);
     }
-    __device__ __forceinline__ static int channel(const PrefillArgs &a, int part, int h, int hk) {
-        return part == 0 ? hk * D : (part == 1 ? a.kh * D + hk * D : 2 * a.kh * D + h * D);
+    // the thread's pair (uniform segment for D a multiple of the wave size)
+    __device__ __forceinline__ static bool pair_of(int tid, int &seg, int &cc) {
+        seg = tid / D;
+        if (D % OMH_WAVE == 0) seg = __builtin_amdgcn_readfirstlane(seg);
+        cc = tid % D;
+        return NPAIR == NT || tid < NPAIR;
     }
 
-    // ph: the sequence's ring phase
-    // units U0 .. U1-1 (and the gate inputs on the gate wave if gate)
+    // parts U0 .. U1-1 (and the gate inputs on the gate waves if gate)
     template <int U0, int U1>
-    __device__ __forceinline__ void load(const PrefillArgs &a, int h, int hk, int c, int tid, bool gate, int lane, int ph) {
+    __device__ __forceinline__ void load(const PrefillArgs &a, int vpg, int h0, int hk, int c, int tid, int gj, bool gate,
+                                         int lane, int ph) {
         const int T = a.T, t0 = c * C;
         const size_t ld = a.ld_qkv;
+        int seg, cc;
+        const bool has = pair_of(tid, seg, cc);
+        const int ts = t0 + seg * NSEG;
 #pragma unroll
-        for (int u = U0; u < (U1 < NU ? U1 : NU); u++) {
-            const int unit = tid + u * WyShape<D>::NT;
-            if (unit >= NUNITS) continue;
-            int part, seg, cc;
-            unit_of(unit, part, seg, cc);
-            const int ch0 = channel(a, part, h, hk);
-            const int ts = t0 + seg * NSEG;
-            float h0, h1, h2;
+        for (int u = U0; u < U1; u++) {
+            if (!has || u - 2 >= vpg) continue;
+            const int ch0 = channel(a, u, h0, hk);
+            float h0v, h1v, h2v;
             if (ts >= 3 && ts + NSEG <= T) {
                 // rows ts-3 .. ts+NSEG-1, one row pointer stepped down the column
                 const float *rp = a.qkv + (size_t)(ts - 3) * ld + ch0;
-                h0 = rp[cc]; rp += ld;
-                h1 = rp[cc]; rp += ld;
-                h2 = rp[cc]; rp += ld;
+                h0v = rp[cc]; rp += ld;
+                h1v = rp[cc]; rp += ld;
+                h2v = rp[cc]; rp += ld;
 #pragma unroll
                 for (int t = 0; t < NSEG; t++) { x[u][t] = rp[cc]; rp += ld; }
             } else {
@@ -269,35 +268,35 @@ struct WyIn {
                     // (this waits for the load: once per sequence)
                     const float4 rv =
                         *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, ch0 + cc, (2 * a.kh + a.vh) * D));
-                    h0 = KK >= 4 ? f4_get(rv, ring_slot(ph, KK, KK - 4)) : 0.f;
-                    h1 = KK >= 3 ? f4_get(rv, ring_slot(ph, KK, KK - 3)) : 0.f;
-                    h2 = f4_get(rv, ring_slot(ph, KK, KK - 2));
+                    h0v = KK >= 4 ? f4_get(rv, ring_slot(ph, KK, KK - 4)) : 0.f;
+                    h1v = KK >= 3 ? f4_get(rv, ring_slot(ph, KK, KK - 3)) : 0.f;
+                    h2v = f4_get(rv, ring_slot(ph, KK, KK - 2));
                 } else {
-                    h0 = col[(size_t)min(ts - 3, T - 1) * ld];
-                    h1 = col[(size_t)min(ts - 2, T - 1) * ld];
-                    h2 = col[(size_t)min(ts - 1, T - 1) * ld];
+                    h0v = col[(size_t)min(ts - 3, T - 1) * ld];
+                    h1v = col[(size_t)min(ts - 2, T - 1) * ld];
+                    h2v = col[(size_t)min(ts - 1, T - 1) * ld];
                 }
             }
-            hv[u] = make_float4(h0, h1, h2, 0.f);
+            hv[u] = make_float4(h0v, h1v, h2v, 0.f);
             wv[u] = *reinterpret_cast<const float4 *>(a.L.conv_w + (size_t)(ch0 + cc) * kConvRing);
         }
         if (gate) {
             const int tt = min(t0 + lane, T - 1);
-            ga = a.a[(size_t)tt * a.ld_ab + h];
-            gb = a.b[(size_t)tt * a.ld_ab + h];
+            ga = a.a[(size_t)tt * a.ld_ab + h0 + gj];
+            gb = a.b[(size_t)tt * a.ld_ab + h0 + gj];
         }
     }
 
-    // conv + SiLU of unit u in place, branch-free
-    __device__ __forceinline__ void compute_unit(const PrefillArgs &a, int u, int c, int tid) {
-        const int unit = tid + u * WyShape<D>::NT;
-        if (NUNITS % WyShape<D>::NT != 0 && unit >= NUNITS) return;
-        int part, seg, cc;
-        unit_of(unit, part, seg, cc);
-        conv_inplace<KK, NSEG>(x[u], hv[u].x, hv[u].y, hv[u].z, wv[u], a.T - (c * C + seg * NSEG));
+    // conv + SiLU of part u in place, branch-free
+    template <int U>
+    __device__ __forceinline__ void compute_unit(const PrefillArgs &a, int c, int tid) {
+        int seg, cc;
+        if (!pair_of(tid, seg, cc)) return;
+        conv_inplace<KK, NSEG>(x[U], hv[U].x, hv[U].y, hv[U].z, wv[U], a.T - (c * C + seg * NSEG));
     }
 
-    // the gates (qwen.c:337-338, zero past T) with an inclusive prefix sum of g
+    // the gates of value head h (qwen.c:337-338, zero past T) with an
+    // inclusive prefix sum of g
     __device__ __forceinline__ void gates(const PrefillArgs &a, int h, int c, int lane) {
         float g = 0.f, be = 0.f;
         if (c * C + lane < a.T) {
@@ -313,29 +312,30 @@ struct WyIn {
         gb = be;
     }
 
-    __device__ __forceinline__ void store(const PrefillArgs &a, size_t hc, int tid, bool gate_wave, int lane, float *Qs,
-                                          float *Ks, float *Vs, float *gcs, float *bs, float *ws) {
+    // parts U0 .. U1-1 to their LDS tile (Qs, Ks, Vs; part 3 also to Vs)
+    template <int U0, int U1>
+    __device__ __forceinline__ void store(int tid, float *Qs, float *Ks, float *Vs) {
         constexpr int PD = WyShape<D>::PD;
+        int seg, cc;
+        if (!pair_of(tid, seg, cc)) return;
 #pragma unroll
-        for (int u = 0; u < NU; u++) {
-            const int unit = tid + u * WyShape<D>::NT;
-            if (unit >= NUNITS) continue;
-            int part, seg, cc;
-            unit_of(unit, part, seg, cc);
-            float *dst = (part == 0 ? Qs : (part == 1 ? Ks : Vs)) + seg * NSEG * PD + cc;
+        for (int u = U0; u < U1; u++) {
+            float *dst = (u == 0 ? Qs : (u == 1 ? Ks : Vs)) + seg * NSEG * PD + cc;
 #pragma unroll
             for (int t = 0; t < NSEG; t++) dst[t * PD] = x[u][t];
         }
-        if (gate_wave) {
-            const float gl = __shfl(ga, C - 1, OMH_WAVE);
-            const float ex = expf(ga), ee = expf(gl - ga);
-            gcs[lane] = ga;
-            bs[lane] = gb;
-            ws[lane] = gb * ex;
-            a.pg[hc * C + lane] = ex;
-            a.pe[hc * C + lane] = ee;
-            if (lane == C - 1) a.glast[hc] = ex;
-        }
+    }
+    // the gates to gt (gc, beta, beta e^gc) and the scan's per-token scales
+    // of (value head, chunk) hc
+    __device__ __forceinline__ void store_gates(const PrefillArgs &a, size_t hc, int lane, float *gt) {
+        const float gl = __shfl(ga, C - 1, OMH_WAVE);
+        const float ex = expf(ga), ee = expf(gl - ga);
+        gt[lane] = ga;
+        gt[C + lane] = gb;
+        gt[2 * C + lane] = gb * ex;
+        a.pg[hc * C + lane] = ex;
+        a.pe[hc * C + lane] = ee;
+        if (lane == C - 1) a.glast[hc] = ex;
     }
 };
 
@@ -371,68 +371,236 @@ template <int D, int KK>
 __global__ __launch_bounds__(WyShape<D>::NT)
 void prefill_wy_kernel(const PrefillArgs a) {
     using WS = WyShape<D>;
-    constexpr int NW = WS::NW, NT = WS::NT, PD = WS::PD, PC = WS::PC, NCT = WS::NCT;
+    using In = WyIn<D, KK>;
+    constexpr int NW = WS::NW, PD = WS::PD, PC = WS::PC, NCT = WS::NCT;
     constexpr int NST = ScanShape<D>::NST;
 
-    const int kh = a.kh, rep = a.vh / kh;
-    const int nitems = a.vh * a.nc;
+    const int kh = a.kh, rep = a.vh / kh, nc = a.nc;
+    const int vpg = rep % 2 == 0 ? 2 : 1;                // value heads per item
+    const int nitems = kh * (rep / vpg) * nc;
     const int tid = threadIdx.x, lane = tid % OMH_WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
     const int l16 = lane % 16, g4 = lane / 16;
-    const bool gate_wave = wave == NW - 1;
+    const int gj = NW - 1 - wave;                        // value head whose gates this wave carries
+    const bool gate = gj < vpg;
 
     extern __shared__ float smem[];
     float *Qs = smem;                            // [C][PD] q~ -> q^; W staging in the substitution
     float *Ks = Qs + C * PD;                     // [C][PD]
-    float *Vs = Ks + C * PD;                     // [C][PD]
+    float *Vs = Ks + C * PD;                     // [C][PD] v of value head 0, then 1
     float *Ls = Vs + C * PD;                     // [C][PC] L
     float *Xs = Ls + C * PC;                     // [C][PC] diagonal blocks of (I + L)^-1
     float *As = Xs + C * PC;                     // [C][PC] Aqk
-    float *gcs = As + C * PC;                    // [C] cumulative log decay
-    float *bs = gcs + C;                         // [C] beta
-    float *ws = bs + C;                          // [C] beta e^gc
+    float *gts = As + C * PC;                    // [2][3][C] gc, beta, beta e^gc per value head
 
     // the tiles above the diagonal of L and Aqk stay zero for every item
-    for (int e = tid; e < C * C; e += NT) {
+    for (int e = tid; e < C * C; e += WS::NT) {
         const int row = e / C, col = e % C;
         if (col / 16 > row / 16) { Ls[row * PC + col] = 0.f; As[row * PC + col] = 0.f; }
     }
 
     const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];   // ring phase of the sequence
     int m = blockIdx.x;
-    WyIn<D, KK> in;
+    In in;
     if (m < nitems) {
-        int h, hk, c;
-        wy_item(m, nitems, kh, rep, h, hk, c);
-        in.template load<0, WyIn<D, KK>::NU>(a, h, hk, c, tid, gate_wave, lane, ph);
-#pragma unroll
-        for (int u = 0; u < WyIn<D, KK>::NU; u++) in.compute_unit(a, u, c, tid);
-        if (gate_wave) in.gates(a, h, c, lane);
+        int hk, h0, c, grp;
+        wy_item(m, nitems, kh, rep, vpg, hk, h0, c, grp);
+        in.template load<0, 4>(a, vpg, h0, hk, c, tid, gj, gate, lane, ph);
+        in.template compute_unit<0>(a, c, tid);
+        in.template compute_unit<1>(a, c, tid);
+        in.template compute_unit<2>(a, c, tid);
+        if (vpg == 2) in.template compute_unit<3>(a, c, tid);
+        if (gate) in.gates(a, h0 + gj, c, lane);
     }
-    for (; m < nitems; m += gridDim.x) {
-        int h, hk, c;
-        wy_item(m, nitems, kh, rep, h, hk, c);
-        const size_t hc = (size_t)h * a.nc + c;
-        const int m2 = m + (int)gridDim.x;
-        int h2 = 0, hk2 = 0, c2 = 0;
-        if (m2 < nitems) wy_item(m2, nitems, kh, rep, h2, hk2, c2);
 
-        // 1. this item's conv outputs and gates (computed during the item
-        // before) into LDS; the next item's inputs start loading
-        in.store(a, hc, tid, gate_wave, lane, Qs, Ks, Vs, gcs, bs, ws);
-        // (spread over phases 1-3: one unit each, so the misses of one
-        // burst are in flight while the next phase computes)
-        if (m2 < nitems) in.template load<0, 1>(a, h2, hk2, c2, tid, gate_wave, lane, ph);
+    // G and P tiles of this wave (raw, for every value head of the item):
+    // G tiles w, w + NW, ..., P tiles (w + 2) mod NW, ...; five products per SIMD
+    constexpr int R = (10 + NW - 1) / NW;
+    const int tp0 = (wave + 2) % NW;
+    v4f graw[R], praw[R];
+
+    // L (strict lower, beta) or Aqk (lower incl. diagonal) tile t of one value
+    // head from its raw product; gt: that head's gc, beta
+    auto scale_tile = [&](auto isPc, int t, const v4f &raw, const float *gt) {
+        constexpr bool isP = decltype(isPc)::value;
+        int ti, tj;
+        lower_tile(t, ti, tj);
+        const float4 gr = *reinterpret_cast<const float4 *>(gt + 16 * ti + 4 * g4);
+        const float gcol = gt[16 * tj + l16];
+        float4 br = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (!isP) br = *reinterpret_cast<const float4 *>(gt + C + 16 * ti + 4 * g4);
+        const float grr[4] = {gr.x, gr.y, gr.z, gr.w}, brr[4] = {br.x, br.y, br.z, br.w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = 16 * ti + 4 * g4 + r, col = 16 * tj + l16;
+            // gc falls along the chunk, so the exponent is <= 0 where used
+            const float e = expf(fminf(grr[r] - gcol, 0.f));
+            if (isP) As[row * PC + col] = col <= row ? raw[r] * e : 0.f;
+            else Ls[row * PC + col] = col < row ? brr[r] * raw[r] * e : 0.f;
+        }
+    };
+    auto scale_all = [&](auto isPc, const float *gt) {
+        constexpr bool isP = decltype(isPc)::value;
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+            const int t = (isP ? tp0 : wave) + NW * k;
+            if (t < 10) scale_tile(isPc, t, isP ? praw[k] : graw[k], gt);
+        }
+    };
+
+    // G = K K^T or P = Q K^T tile t: lane group g4 sums the contiguous k
+    // range [g4 D/4, (g4+1) D/4), so operands load as float4
+    auto product = [&](auto isPc, int t) {
+        constexpr bool isP = decltype(isPc)::value;
+        int ti, tj;
+        lower_tile(t, ti, tj);
+        const float *aa = (isP ? Qs : Ks) + (16 * ti + l16) * PD + g4 * (D / 4);
+        const float *kb = Ks + (16 * tj + l16) * PD + g4 * (D / 4);
+        v4f acc = v4zero(), acc2 = v4zero();
+        // operands in groups of up to four float4 pairs (bounded registers)
+        constexpr int NS4 = D / 16, GS = NS4 < 2 ? NS4 : 2;
+#pragma unroll
+        for (int s0 = 0; s0 < NS4; s0 += GS) {
+            float4 A[GS], B[GS];
+#pragma unroll
+            for (int q = 0; q < GS; q++) {
+                A[q] = *reinterpret_cast<const float4 *>(aa + 4 * (s0 + q));
+                B[q] = *reinterpret_cast<const float4 *>(kb + 4 * (s0 + q));
+            }
+#pragma unroll
+            for (int q = 0; q < GS; q++) {
+                acc = mfma4(A[q].x, B[q].x, acc);
+                acc2 = mfma4(A[q].y, B[q].y, acc2);
+                acc = mfma4(A[q].z, B[q].z, acc);
+                acc2 = mfma4(A[q].w, B[q].w, acc2);
+            }
+        }
+        return acc + acc2;
+    };
+
+    // the diagonal blocks D_b = (I + L_bb)^-1 on the matrix cores (waves 0-3)
+    auto inverses = [&]() {
+        if (wave < 4) {
+            const int b0 = 16 * wave;
+            v4f nd;
+#pragma unroll
+            for (int r = 0; r < 4; r++) nd[r] = Ls[(b0 + 4 * g4 + r) * PC + b0 + l16];
+            const v4f nt = *reinterpret_cast<const v4f *>(Ls + (b0 + l16) * PC + b0 + 4 * g4);
+            const v4f xt = inv_unit_lower16(nd, nt, lane);
+            *reinterpret_cast<v4f *>(Xs + (b0 + l16) * PC + b0 + 4 * g4) = xt;   // row l16 of D_b
+        }
+    };
+    // the Aqk panel of (value head, chunk) hc from As, on the panel-writing
+    // waves (4.. if there are more than four, else all)
+    constexpr int PW = NW > 4 ? NW - 4 : NW;
+    const int pw_t = NW > 4 ? tid - 4 * OMH_WAVE : tid;
+    auto aqk_panel = [&](size_t hc) {
+        if (pw_t >= 0)
+            for (int e = pw_t; e < 16 * OMH_WAVE; e += PW * OMH_WAVE) {
+                const int l = e % OMH_WAVE, kt = (e / OMH_WAVE) % 4, mt = e / (4 * OMH_WAVE);
+                const int row = 16 * mt + l % 16, col = 16 * kt + 4 * (l / 16);
+                *reinterpret_cast<float4 *>(a.pa + pan4(hc * 4 + mt, kt, l)) =
+                    *reinterpret_cast<const float4 *>(As + row * PC + col);
+            }
+    };
+
+    // W and U of (value head, chunk) hc by blocked forward substitution on
+    // (I + L) [W | U] = [K beta e^gc | V beta], one 16-column tile per chain:
+    //   R_i = D_i (RHS_i - sum_{k<i} L_ik R_k),
+    // the tiles in registers in MFMA D layout (a D-layout tile feeds the B
+    // operand directly: at k-step s lane group g supplies row 4g+s), each
+    // R_k subtracted from every later row tile as soon as it is known.  With
+    // D/16 waves each takes the W and the U chain of one column tile; with
+    // fewer columns, one chain each.  U goes straight to its panel (the
+    // scan's D layout); W is transposed through the wave's own columns of Qs
+    // (no other wave reads them now) into the W panel's fragment order.
+    auto substitution = [&](size_t hc, const float *gt) {
+        constexpr bool TWO = NCT == NW;
+        constexpr int NCH = TWO ? 2 : 1;
+        const int q = wave;
+        if (TWO || q < 2 * NCT) {
+            const int tn = TWO ? q : q % NCT;
+            const bool onlyU = !TWO && q >= NCT;
+            v4f R[NCH][4];
+            // right-hand sides (chain 0: W or U; chain 1: U)
+#pragma unroll
+            for (int ch = 0; ch < NCH; ch++) {
+                const bool isU = ch == 1 || onlyU;
+                const float *src = (isU ? Vs : Ks) + 16 * tn + l16;
+                const float *scl = gt + (isU ? C : 2 * C) + 4 * g4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 sv = *reinterpret_cast<const float4 *>(scl + 16 * i);
+                    R[ch][i][0] = src[(16 * i + 4 * g4 + 0) * PD] * sv.x;
+                    R[ch][i][1] = src[(16 * i + 4 * g4 + 1) * PD] * sv.y;
+                    R[ch][i][2] = src[(16 * i + 4 * g4 + 2) * PD] * sv.z;
+                    R[ch][i][3] = src[(16 * i + 4 * g4 + 3) * PD] * sv.w;
+                }
+            }
+            v4f Xd[4], Ln[6];        // D_i and -L_ik (k < i) as A operands
+#pragma unroll
+            for (int i = 0; i < 4; i++) Xd[i] = *reinterpret_cast<const v4f *>(Xs + (16 * i + l16) * PC + 16 * i + 4 * g4);
+#pragma unroll
+            for (int i = 1, n = 0; i < 4; i++)
+#pragma unroll
+                for (int k = 0; k < i; k++, n++)
+                    Ln[n] = -*reinterpret_cast<const v4f *>(Ls + (16 * i + l16) * PC + 16 * k + 4 * g4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int ch = 0; ch < NCH; ch++) R[ch][i] = mm16(Xd[i], R[ch][i], v4zero());
+#pragma unroll
+                for (int i2 = i + 1; i2 < 4; i2++)
+#pragma unroll
+                    for (int ch = 0; ch < NCH; ch++) R[ch][i2] = mm16(Ln[i2 * (i2 - 1) / 2 + i], R[ch][i], R[ch][i2]);
+            }
+            // U panel of column block tn, token tile i (the D layout of R)
+            if (TWO || onlyU)
+#pragma unroll
+                for (int i = 0; i < 4; i++) *reinterpret_cast<v4f *>(a.pu + pan4(hc * NCT + tn, i, lane)) = R[NCH - 1][i];
+            if (TWO || !onlyU) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) Qs[(16 * i + 4 * g4 + r) * PD + 16 * tn + l16] = R[0][i][r];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                // W panel, k-group tn of token tile tt
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+                    *reinterpret_cast<float4 *>(a.pw + panj<D>(hc, tt, tn, lane)) =
+                        *reinterpret_cast<const float4 *>(Qs + (16 * tt + l16) * PD + 16 * tn + 4 * g4);
+            }
+        }
+    };
+
+    for (; m < nitems; m += gridDim.x) {
+        int hk, h0, c, grp;
+        wy_item(m, nitems, kh, rep, vpg, hk, h0, c, grp);
+        const size_t hc0 = (size_t)h0 * nc + c, hc1 = hc0 + nc;   // value heads h0, h0 + 1
+        const int m2 = m + (int)gridDim.x;
+        const bool more = m2 < nitems;
+        int hk2 = 0, h02 = 0, c2 = 0, grp2 = 0;
+        if (more) wy_item(m2, nitems, kh, rep, vpg, hk2, h02, c2, grp2);
+
+        // 1. this item's q, k, v0 and gates (computed during the item
+        // before) into LDS; the next item's inputs start loading, spread
+        // over phases 1-3 (and 6 for the second value head's v) so the
+        // misses of one burst are in flight while the next phase computes
+        in.template store<0, 3>(tid, Qs, Ks, Vs);
+        if (gate) in.store_gates(a, gj == 0 ? hc0 : hc1, lane, gts + 3 * C * gj);
+        if (more) in.template load<0, 1>(a, vpg, h02, hk2, c2, tid, gj, gate, lane, ph);
         omh_lds_barrier();
 
         // 2. L2 norm per token over the head's D channels (eps 1e-6), q also
         // scaled by D^-1/2 (qwen.c:153-157, 326-329)
         {
             // TPR consecutive lanes per row, each over D/TPR columns
-            constexpr int TPR = NT / (2 * C) >= 4 ? 4 : 2;
+            constexpr int TPR = WS::NT / (2 * C) >= 4 ? 4 : 2;
             constexpr int EPT = D / TPR;
-            static_assert(EPT % 4 == 0 && NT / TPR >= 2 * C / 2, "norm layout");
-            for (int r = tid / TPR; r < 2 * C; r += NT / TPR) {
+            static_assert(EPT % 4 == 0 && WS::NT / TPR >= 2 * C / 2, "norm layout");
+            for (int r = tid / TPR; r < 2 * C; r += WS::NT / TPR) {
                 float *row = (r < C ? Qs + r * PD : Ks + (r - C) * PD) + (tid % TPR) * EPT;
                 float4 v[EPT / 4];
                 float ss = 0.f;
@@ -452,204 +620,78 @@ void prefill_wy_kernel(const PrefillArgs a) {
                 }
             }
         }
-        if (m2 < nitems) in.template load<1, 2>(a, h2, hk2, c2, tid, false, lane, ph);
+        if (more) in.template load<1, 2>(a, vpg, h02, hk2, c2, tid, gj, false, lane, ph);
         omh_lds_barrier();
 
-        // 3. G = K K^T and P = Q K^T on the ten lower 16x16 tiles each:
-        // wave w takes G tiles w, w + NW, ... and P tiles (w + 2) mod NW, ...,
-        // five products per SIMD.  Lane group g4 sums the contiguous k range
-        // [g4 D/4, (g4+1) D/4), so operands load as float4, all of a
-        // product's before its first MFMA.  Each product shares a basic block
-        // with one unit of the next item's conv, so the conv's VALU work can
-        // issue between the MFMAs.
-        auto product = [&](auto isPc, int t) {
-            constexpr bool isP = decltype(isPc)::value;
-            int ti, tj;
-            lower_tile(t, ti, tj);
-            const float *aa = (isP ? Qs : Ks) + (16 * ti + l16) * PD + g4 * (D / 4);
-            const float *kb = Ks + (16 * tj + l16) * PD + g4 * (D / 4);
-            const float4 gr = *reinterpret_cast<const float4 *>(gcs + 16 * ti + 4 * g4);
-            const float gcol = gcs[16 * tj + l16];
-            float4 br = make_float4(1.f, 1.f, 1.f, 1.f);
-            if (!isP) br = *reinterpret_cast<const float4 *>(bs + 16 * ti + 4 * g4);
-            v4f acc = v4zero(), acc2 = v4zero();
-            // operands in groups of up to four float4 pairs (bounded registers)
-            constexpr int NS4 = D / 16, GS = NS4 < 4 ? NS4 : 4;
-#pragma unroll
-            for (int s0 = 0; s0 < NS4; s0 += GS) {
-                float4 A[GS], B[GS];
-#pragma unroll
-                for (int q = 0; q < GS; q++) {
-                    A[q] = *reinterpret_cast<const float4 *>(aa + 4 * (s0 + q));
-                    B[q] = *reinterpret_cast<const float4 *>(kb + 4 * (s0 + q));
-                }
-#pragma unroll
-                for (int q = 0; q < GS; q++) {
-                    acc = mfma4(A[q].x, B[q].x, acc);
-                    acc2 = mfma4(A[q].y, B[q].y, acc2);
-                    acc = mfma4(A[q].z, B[q].z, acc);
-                    acc2 = mfma4(A[q].w, B[q].w, acc2);
-                }
+        // 3. the products, kept raw for every value head; L and Aqk of value
+        // head 0.  Each product shares a basic block with one conv unit of
+        // the next item, so the conv's VALU work can issue between the MFMAs.
+        if (more) in.template load<2, 3>(a, vpg, h02, hk2, c2, tid, gj, false, lane, ph);
+        static_for<R>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            const int tg = wave + NW * k, tq = tp0 + NW * k;
+            if (tg < 10) {
+                graw[k] = product(std::false_type{}, tg);
+                if (2 * k < 3) in.template compute_unit<(2 * k < 3 ? 2 * k : 0)>(a, c2, tid);
+                scale_tile(std::false_type{}, tg, graw[k], gts);
+            } else if (2 * k < 3) {
+                in.template compute_unit<(2 * k < 3 ? 2 * k : 0)>(a, c2, tid);
             }
-            acc += acc2;
-            const float grr[4] = {gr.x, gr.y, gr.z, gr.w}, brr[4] = {br.x, br.y, br.z, br.w};
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = 16 * ti + 4 * g4 + r, col = 16 * tj + l16;
-                // gc falls along the chunk, so the exponent is <= 0 where used
-                const float e = expf(fminf(grr[r] - gcol, 0.f));
-                // Aqk keeps the diagonal; L is strictly lower and carries beta
-                if (isP) As[row * PC + col] = col <= row ? acc[r] * e : 0.f;
-                else Ls[row * PC + col] = col < row ? brr[r] * acc[r] * e : 0.f;
+            if (tq < 10) {
+                praw[k] = product(std::true_type{}, tq);
+                if (2 * k + 1 < 3) in.template compute_unit<(2 * k + 1 < 3 ? 2 * k + 1 : 0)>(a, c2, tid);
+                scale_tile(std::true_type{}, tq, praw[k], gts);
+            } else if (2 * k + 1 < 3) {
+                in.template compute_unit<(2 * k + 1 < 3 ? 2 * k + 1 : 0)>(a, c2, tid);
             }
-        };
-        if (m2 < nitems) in.template load<2, WyIn<D, KK>::NU>(a, h2, hk2, c2, tid, false, lane, ph);
-        {
-            constexpr int R = (10 + NW - 1) / NW;            // rounds of each product type
-            constexpr int NU = WyIn<D, KK>::NU;
-            const int tp0 = (wave + 2) % NW;
-            auto conv_unit = [&](auto uc) {
-                constexpr int u = decltype(uc)::value;
-                if (u < NU) in.compute_unit(a, u < NU ? u : 0, c2, tid);
-            };
-            static_for<R>([&](auto kc) {
-                constexpr int k = decltype(kc)::value;
-                const int tg = wave + NW * k, tq = tp0 + NW * k;
-                if (tg < 10) {
-                    product(std::false_type{}, tg);
-                    conv_unit(std::integral_constant<int, 2 * k>{});
-                } else {
-                    conv_unit(std::integral_constant<int, 2 * k>{});
-                }
-                if (tq < 10) {
-                    product(std::true_type{}, tq);
-                    conv_unit(std::integral_constant<int, 2 * k + 1>{});
-                } else {
-                    conv_unit(std::integral_constant<int, 2 * k + 1>{});
-                }
-            });
-            static_assert(2 * R >= NU, "every conv unit has a slot");
-            if (gate_wave) in.gates(a, h2, c2, lane);
-        }
+        });
+        static_assert(2 * R >= 3, "every conv unit has a slot");
         omh_lds_barrier();
 
-        // 4. waves 0-3: diagonal blocks D_b = (I + L_bb)^-1 on the matrix
-        // cores.  Meanwhile the other waves (all waves, after, when there are
-        // only four) write the panels that need no inverse: q^, k^T (once per
-        // key head) and Aqk, a float4 per lane.
-        if (wave < 4) {
-            const int b0 = 16 * wave;
-            v4f nd;
-#pragma unroll
-            for (int r = 0; r < 4; r++) nd[r] = Ls[(b0 + 4 * g4 + r) * PC + b0 + l16];
-            const v4f nt = *reinterpret_cast<const v4f *>(Ls + (b0 + l16) * PC + b0 + 4 * g4);
-            const v4f xt = inv_unit_lower16(nd, nt, lane);
-            *reinterpret_cast<v4f *>(Xs + (b0 + l16) * PC + b0 + 4 * g4) = xt;   // row l16 of D_b
-        }
-        {
-            constexpr int PW = NW > 4 ? NW - 4 : NW;         // panel-writing waves
-            const int pw_t = NW > 4 ? tid - 4 * OMH_WAVE : tid;
-            if (pw_t >= 0) {
-                // q^ / k^T panels (NST kd tiles x 4 token tiles x 64 lanes),
-                // once per key head: by the item of its first value head
-                if (h % rep == 0) {
-                    const size_t hq = (size_t)hk * a.nc + c;
-                    for (int e = pw_t; e < NST * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
-                        const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
-                        const int ll16 = l % 16, lg = l / 16;
-                        const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
-                        const float4 vq = *reinterpret_cast<const float4 *>(Qs + rq * PD + cq);
-                        const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
-                        const float4 vk = make_float4(Ks[rk * PD + ck], Ks[(rk + 1) * PD + ck], Ks[(rk + 2) * PD + ck],
-                                                      Ks[(rk + 3) * PD + ck]);
-                        *reinterpret_cast<float4 *>(a.pq + panj<D>(hq, tt, w, l)) = vq;
-                        *reinterpret_cast<float4 *>(a.pk + pan4(hq * NST + w, tt, l)) = vk;
-                    }
-                }
-                for (int e = pw_t; e < 16 * OMH_WAVE; e += PW * OMH_WAVE) {
-                    const int l = e % OMH_WAVE, kt = (e / OMH_WAVE) % 4, mt = e / (4 * OMH_WAVE);
-                    const int row = 16 * mt + l % 16, col = 16 * kt + 4 * (l / 16);
-                    *reinterpret_cast<float4 *>(a.pa + pan4(hc * 4 + mt, kt, l)) =
-                        *reinterpret_cast<const float4 *>(As + row * PC + col);
-                }
+        // 4. value head 0: the diagonal inverses on waves 0-3 while the
+        // other waves write the q^ / k^T panels (once per key head: by the
+        // first group's item) and the Aqk panel
+        inverses();
+        if (pw_t >= 0 && grp == 0) {
+            // q^ / k^T panels (NST kd tiles x 4 token tiles x 64 lanes)
+            const size_t hq = (size_t)hk * nc + c;
+            for (int e = pw_t; e < NST * 4 * OMH_WAVE; e += PW * OMH_WAVE) {
+                const int l = e % OMH_WAVE, tt = (e / OMH_WAVE) % 4, w = e / (4 * OMH_WAVE);
+                const int ll16 = l % 16, lg = l / 16;
+                const int rq = tt * 16 + ll16, cq = 16 * w + 4 * lg;
+                const float4 vq = *reinterpret_cast<const float4 *>(Qs + rq * PD + cq);
+                const int rk = tt * 16 + 4 * lg, ck = 16 * w + ll16;
+                const float4 vk =
+                    make_float4(Ks[rk * PD + ck], Ks[(rk + 1) * PD + ck], Ks[(rk + 2) * PD + ck], Ks[(rk + 3) * PD + ck]);
+                *reinterpret_cast<float4 *>(a.pq + panj<D>(hq, tt, w, l)) = vq;
+                *reinterpret_cast<float4 *>(a.pk + pan4(hq * NST + w, tt, l)) = vk;
             }
         }
+        aqk_panel(hc0);
         omh_lds_barrier();
 
-        // 5. W and U by blocked forward substitution on (I + L) [W | U] =
-        // [K beta e^gc | V beta], one 16-column tile per chain:
-        //   R_i = D_i (RHS_i - sum_{k<i} L_ik R_k),
-        // the tiles in registers in MFMA D layout (a D-layout tile feeds the
-        // B operand directly: at k-step s lane group g supplies row 4g+s),
-        // each R_k subtracted from every later row tile as soon as it is
-        // known.  With D/16 waves each takes the W and the U chain of one
-        // column tile; with fewer columns, one chain each.  U goes straight
-        // to its panel (the scan's D layout); W is transposed through the
-        // wave's own columns of Qs (no other wave reads them now) into the
-        // W panel's fragment order.
-        {
-            constexpr bool TWO = NCT == NW;
-            constexpr int NCH = TWO ? 2 : 1;
-            const int q = wave;
-            if (TWO || q < 2 * NCT) {
-                const int tn = TWO ? q : q % NCT;
-                const bool onlyU = !TWO && q >= NCT;
-                v4f R[NCH][4];
-                // right-hand sides (chain 0: W or U; chain 1: U)
-#pragma unroll
-                for (int ch = 0; ch < NCH; ch++) {
-                    const bool isU = ch == 1 || onlyU;
-                    const float *src = (isU ? Vs : Ks) + 16 * tn + l16;
-                    const float *scl = (isU ? bs : ws) + 4 * g4;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float4 sv = *reinterpret_cast<const float4 *>(scl + 16 * i);
-                        R[ch][i][0] = src[(16 * i + 4 * g4 + 0) * PD] * sv.x;
-                        R[ch][i][1] = src[(16 * i + 4 * g4 + 1) * PD] * sv.y;
-                        R[ch][i][2] = src[(16 * i + 4 * g4 + 2) * PD] * sv.z;
-                        R[ch][i][3] = src[(16 * i + 4 * g4 + 3) * PD] * sv.w;
-                    }
-                }
-                v4f Xd[4], Ln[6];        // D_i and -L_ik (k < i) as A operands
-#pragma unroll
-                for (int i = 0; i < 4; i++) Xd[i] = *reinterpret_cast<const v4f *>(Xs + (16 * i + l16) * PC + 16 * i + 4 * g4);
-#pragma unroll
-                for (int i = 1, n = 0; i < 4; i++)
-#pragma unroll
-                    for (int k = 0; k < i; k++, n++)
-                        Ln[n] = -*reinterpret_cast<const v4f *>(Ls + (16 * i + l16) * PC + 16 * k + 4 * g4);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-#pragma unroll
-                    for (int ch = 0; ch < NCH; ch++) R[ch][i] = mm16(Xd[i], R[ch][i], v4zero());
-#pragma unroll
-                    for (int i2 = i + 1; i2 < 4; i2++)
-#pragma unroll
-                        for (int ch = 0; ch < NCH; ch++)
-                            R[ch][i2] = mm16(Ln[i2 * (i2 - 1) / 2 + i], R[ch][i], R[ch][i2]);
-                }
-                // U panel of column block tn, token tile i (the D layout of R)
-                if (TWO || onlyU)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        *reinterpret_cast<v4f *>(a.pu + pan4(hc * NCT + tn, i, lane)) = R[NCH - 1][i];
-                if (TWO || !onlyU) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) Qs[(16 * i + 4 * g4 + r) * PD + 16 * tn + l16] = R[0][i][r];
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                    __builtin_amdgcn_wave_barrier();
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                    // W panel, k-group tn of token tile tt
-#pragma unroll
-                    for (int tt = 0; tt < 4; tt++)
-                        *reinterpret_cast<float4 *>(a.pw + panj<D>(hc, tt, tn, lane)) =
-                            *reinterpret_cast<const float4 *>(Qs + (16 * tt + l16) * PD + 16 * tn + 4 * g4);
-                }
-            }
+        // 5. value head 0: W and U; the gates of the next item
+        substitution(hc0, gts);
+        if (gate) in.gates(a, h02 + gj, c2, lane);
+        omh_lds_barrier();
+
+        if (vpg == 2) {
+            // 6. value head 1: L, Aqk (nothing reads Ls, As now) and v into LDS
+            scale_all(std::false_type{}, gts + 3 * C);
+            scale_all(std::true_type{}, gts + 3 * C);
+            in.template store<3, 4>(tid, Qs, Ks, Vs);
+            omh_lds_barrier();
+            // 7. value head 1: inverses and the Aqk panel; the next item's v
+            // of its second value head starts loading
+            if (more) in.template load<3, 4>(a, vpg, h02, hk2, c2, tid, gj, false, lane, ph);
+            inverses();
+            aqk_panel(hc1);
+            omh_lds_barrier();
+            // 8. value head 1: W and U; the next item's second v conv
+            substitution(hc1, gts + 3 * C);
+            in.template compute_unit<3>(a, c2, tid);
+            omh_lds_barrier();
         }
-        omh_lds_barrier();                       // LDS is reused by the next item
     }
 }
 
@@ -956,7 +998,8 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     const int conv_dim = 2 * a.kh * D + a.vh * D;
     // persistent: one workgroup per CU (the LDS footprint allows one), a
     // multiple of 8 so the XCD-aware item order holds
-    const int nitems = a.vh * a.nc;
+    const int rep = a.vh / a.kh;
+    const int nitems = a.kh * (rep % 2 == 0 ? rep / 2 : rep) * a.nc;   // as in the kernel
     const int grid = nitems < wy_grid() ? nitems : wy_grid();
     // the WY kernel reads the ring for chunk 0 before the commit rewrites it
     if (a.K == 4) hipLaunchKernelGGL((prefill_wy_kernel<D, 4>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);

@@ -49,6 +49,27 @@ def test_prefill_matches_recurrent_oracle(D, T):
     L.free()
 
 
+@pytest.mark.parametrize("kh,vh,D,K", [(2, 2, 64, 4), (1, 3, 32, 4), (1, 4, 64, 4), (2, 8, 128, 4), (1, 6, 16, 4),
+                                        (2, 4, 32, 3), (2, 4, 32, 2), (1, 2, 128, 3)])
+@pytest.mark.parametrize("T", [65, 200])
+def test_prefill_head_groupings_and_conv_widths(kh, vh, D, K, T):
+    """The WY kernel takes a key head's value heads two at a time when their
+    number is even, one at a time otherwise (rep 1, 3), in several groups
+    when there are more (rep 4, 6); conv widths 2-4 are separate kernels."""
+    d = GdnDims(kh, vh, D, D, K, 0)
+    seed = 3000 + 7 * kh + vh + D + K + T
+    L, w, conv0, S0 = _layer(d, seed)
+    inp = synth.core_inputs(d, T, seed)
+    core = L.prefill_core(0, inp["qkv"], inp["z"], inp["a"], inp["b"])
+    ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"], inp["z"], inp["a"], inp["b"], conv0, S0)
+    conv, S = L.get_state(0)
+    what = f"kh={kh} vh={vh} D={D} K={K} T={T}"
+    assert_close(core, ref, what=what + " core")
+    assert_close(S, Sref, what=what + " S")
+    assert np.array_equal(conv, cref), "conv history is a copy of the inputs"
+    L.free()
+
+
 @pytest.mark.parametrize("name", ["core_rep3_d16", "core_d128", "core_d32_decay"])
 def test_prefill_matches_reference_golden(name):
     d, w, inp, (conv, S), exp = fixtures.load(name)
