@@ -23,11 +23,21 @@
 //     k-slices are summed through LDS.
 #include "omh_device.h"
 #include "omh_internal.h"
+#include <type_traits>
 
 namespace omh {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>)
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 // Weight fragment: 16 consecutive weights of one row, as loaded (int8 or
 // fp32) and as fp32.
@@ -246,7 +256,7 @@ void proj_mfma_kernel(const ProjArgs p) {
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
     const int rt = wv % RT, ks = wv / RT;
     const int r0 = (blockIdx.x * RT + rt) * 16;
-    const int t0 = blockIdx.y * kMfmaTok;
+    const int t0 = blockIdx.y * (TT * 16);
     const int klen = p.I / KS, kbeg = ks * klen;
     v4f acc[4];
 #pragma unroll
@@ -281,10 +291,10 @@ void proj_mfma_kernel(const ProjArgs p) {
 }
 
 template <int RT, int PF>
-void launch_mfma_tt(const ProjArgs &p, dim3 grid, hipStream_t st) {
+void launch_mfma_tt(const ProjArgs &p, dim3 grid, int tpw, hipStream_t st) {
     // token tiles per workgroup: all tiles when every workgroup sees one
-    // token block, else 4 (the last block's missing tokens are clamped)
-    const int tt = grid.y > 1 ? 4 : (p.T + 15) / 16;
+    // token block, else tpw / 16 (the last block's missing tokens are clamped)
+    const int tt = grid.y > 1 ? tpw / 16 : (p.T + 15) / 16;
     const dim3 blk(4 * OMH_WAVE);
     switch (tt) {
     case 1: hipLaunchKernelGGL((proj_mfma_kernel<RT, 1, PF>), grid, blk, 0, st, p); break;
@@ -295,11 +305,272 @@ void launch_mfma_tt(const ProjArgs &p, dim3 grid, hipStream_t st) {
 }
 
 template <int RT>
-void launch_mfma_rt(const ProjArgs &p, dim3 grid, hipStream_t st) {
+void launch_mfma_rt(const ProjArgs &p, dim3 grid, int tpw, hipStream_t st) {
     const int nb = p.I / (4 / RT) / 64;       // 64-wide blocks per k-slice
-    if (nb % 8 == 0) launch_mfma_tt<RT, 8>(p, grid, st);
-    else if (nb % 2 == 0) launch_mfma_tt<RT, 2>(p, grid, st);
-    else launch_mfma_tt<RT, 1>(p, grid, st);
+    if (nb % 8 == 0) launch_mfma_tt<RT, 8>(p, grid, tpw, st);
+    else if (nb % 2 == 0) launch_mfma_tt<RT, 2>(p, grid, tpw, st);
+    else launch_mfma_tt<RT, 1>(p, grid, tpw, st);
+}
+
+// ---------------------------------------------------------------- int8 rows, T > 4: bf16 x 3
+// int8 weights are exact in bf16, and x splits exactly into three bf16
+// terms, x = hi + mid + lo (hi = bf16(x), mid = bf16(x - hi), lo = the
+// rest, which has at most 8 significant bits left), so
+// sum_i x_i w_i = sum_i (hi_i w_i + mid_i w_i + lo_i w_i) with every product
+// exact, accumulated in fp32 on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16).  x is split once per launch into three bf16
+// planes [3][T][I] (proj_split_x_kernel); a workgroup of RG row groups x KS
+// k-slices of waves (RG * KS = 4) stages, per 64-wide k block, the planes'
+// rows of its 16 * TT tokens in LDS (double-buffered, shared by the RG waves
+// of a k-slice), while each wave streams its weights (16 B of int8 per lane
+// per row tile and block) PF blocks ahead.  A wave owns RW = 2 tiles of 16
+// rows.  Operand layout of a 32-wide k step s: lane (l%16, g) holds rows /
+// tokens l%16 at k = 16g + 8s + j, j < 8 (the same permutation of k on both
+// operands).
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+constexpr int kQ8Rows = 32;                 // rows per wave
+constexpr int kQ8Tok = 32;                  // tokens per workgroup
+
+// planes[p][t][k] = term p of x[t][k]; 8 values per thread
+__global__ __launch_bounds__(256)
+void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ xb, int T, int I) {
+    const size_t n8 = (size_t)T * (I / 8);
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n8) return;
+    const int t = (int)(e / (I / 8)), k = (int)(e % (I / 8)) * 8;
+    const float4 a = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + k);
+    const float4 b = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + k + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    v8bf hi, mid, lo;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        hi[j] = (__bf16)v[j];
+        const float r1 = v[j] - (float)hi[j];
+        mid[j] = (__bf16)r1;
+        lo[j] = (__bf16)(r1 - (float)mid[j]);
+    }
+    const size_t plane = (size_t)T * I, o = (size_t)t * I + k;
+    *reinterpret_cast<v8bf *>(xb + o) = hi;
+    *reinterpret_cast<v8bf *>(xb + plane + o) = mid;
+    *reinterpret_cast<v8bf *>(xb + 2 * plane + o) = lo;
+}
+
+// 8 int8 weights w as bf16 of u = w + 128 (0..255, exact in bf16): one
+// unsigned-byte conversion per value and one pack per pair; the products
+// then carry + 128 x, which the caller takes off as 128 * (sum of x)
+__device__ __forceinline__ v8bf q8_to_bf16_u(unsigned lo, unsigned hi) {
+    const unsigned u[2] = {lo ^ 0x80808080u, hi ^ 0x80808080u};
+    v8bf r;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) r[4 * i + b] = (__bf16)(float)((u[i] >> (8 * b)) & 0xFFu);
+    return r;
+}
+
+// NBC: the k blocks per slice when known at compile time (the loop is then
+// straight-line: across a loop back edge the compiler's load-counter waits
+// fall back to draining the prefetched blocks), else 0
+template <int RG, int KS, int TT, int PF, int NBC>
+__global__ __launch_bounds__(4 * OMH_WAVE)
+void proj_q8_bf16x3_kernel(const ProjArgs p) {
+    constexpr int RW = kQ8Rows / 16, KB = 64, XR = KB + 8;     // padded staging row (bf16)
+    constexpr int NU4 = KS * 3 * TT * 16 * (KB / 8) / (4 * OMH_WAVE);   // 16-byte pieces per thread per block
+    static_assert(NU4 >= 1 && KS * 3 * TT * 16 * (KB / 8) % (4 * OMH_WAVE) == 0, "x staging split");
+    __shared__ __align__(16) __bf16 xs[2][KS][3][TT * 16][XR];
+    __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RG][RW][TT][OMH_WAVE];
+
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int rg = wv % RG, ks = wv / RG;
+    const int l16 = lane % 16, g = lane / 16;
+    const int r0 = (blockIdx.x * RG + rg) * kQ8Rows;
+    const int t0 = blockIdx.y * (TT * 16);
+    const int klen = p.I / KS, nb = NBC > 0 ? NBC : klen / KB;
+    const size_t plane = (size_t)p.T * p.I;
+
+    // x staging: piece f of block b -> (k-slice, term, token, 16-byte column),
+    // XD blocks ahead in a ring of registers
+    constexpr int XD0 = NU4 <= 3 ? 4 : (NU4 <= 6 ? 2 : 1);
+    constexpr int XD = XD0 < PF ? XD0 : PF;
+    static_assert(PF % XD == 0, "ring slots known at compile time");
+    v4u xr[XD][NU4];       // (a clang vector: the HIP uint4 struct is copied through memory)
+    auto piece = [&](int f, int &kq, int &sp, int &t, int &c) __attribute__((always_inline)) {
+        const int idx = tid + f * 4 * OMH_WAVE;
+        c = idx % (KB / 8);
+        t = (idx / (KB / 8)) % (TT * 16);
+        sp = (idx / (KB / 8 * TT * 16)) % 3;
+        kq = idx / (KB / 8 * TT * 16 * 3);
+    };
+    // (slot is a compile-time constant at every call, so the ring stays in
+    // registers)
+    auto x_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value;
+        b = min(b, nb - 1);
+#pragma unroll
+        for (int f = 0; f < NU4; f++) {
+            int kq, sp, t, c;
+            piece(f, kq, sp, t, c);
+            xr[slot][f] = *reinterpret_cast<const v4u *>(p.xb + sp * plane + (size_t)min(t0 + t, p.T - 1) * p.I + kq * klen +
+                                                           b * KB + 8 * c);
+        }
+    };
+    auto x_stage = [&](int buf, auto slot_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+        for (int f = 0; f < NU4; f++) {
+            int kq, sp, t, c;
+            piece(f, kq, sp, t, c);
+            *reinterpret_cast<v4u *>(&xs[buf][kq][sp][t][8 * c]) = xr[slot][f];
+        }
+    };
+
+    // weights: 16 int8 per lane per row tile and block, PF blocks ahead
+    const int8_t *wrow[RW];
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+        wrow[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + ks * klen + 16 * g;
+    int4 wq[PF][RW];
+    auto w_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int slot = decltype(slot_c)::value;
+#pragma unroll
+        for (int rw = 0; rw < RW; rw++) wq[slot][rw] = *reinterpret_cast<const int4 *>(wrow[rw] + (size_t)min(b, nb - 1) * KB);
+    };
+
+    v4f acc[RW][TT], xsum[TT];            // xsum: sum of x over k per token (every row alike)
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) acc[rw][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) xsum[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v8bf ones;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ones[j] = (__bf16)1.f;
+
+    // the prologue issues x then w per block, as the loop does, so the wait
+    // counts are the same on entry and on the back edge
+    static_for<PF>([&](auto sc) __attribute__((always_inline)) {
+        constexpr int s = decltype(sc)::value;
+        if constexpr (s < XD) x_load(s, std::integral_constant<int, s>{});
+        w_load(s, sc);
+    });
+    x_stage(0, std::integral_constant<int, 0>{});
+    x_load(XD, std::integral_constant<int, 0>{});
+    // PF divides nb
+    auto step = [&](int b0) __attribute__((always_inline)) {
+        static_for<PF>([&](auto sc) __attribute__((always_inline)) {
+            constexpr int s = decltype(sc)::value;
+            const int b = b0 + s;
+            const int buf = b & 1;
+            // no code motion across blocks: the weights of a block are
+            // unpacked only after its loads (PF blocks old) are in
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();                     // block b staged; every wave is past block b-1
+            // every x operand of the block read at once (one LDS latency);
+            // block b+1 staged into the other buffer while this block's
+            // products run (its writes are done by the next barrier); the
+            // weights unpacked meanwhile, then the 24 products
+            v4u B[2][TT][3];
+            v8bf A[2][RW];
+#pragma unroll
+            for (int st = 0; st < 2; st++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                    for (int sp = 0; sp < 3; sp++)
+                        B[st][tt][sp] = *reinterpret_cast<const v4u *>(&xs[buf][ks][sp][16 * tt + l16][16 * g + 8 * st]);
+            x_stage(buf ^ 1, std::integral_constant<int, (s + 1) % XD>{});
+            x_load(b + 1 + XD, std::integral_constant<int, (s + 1) % XD>{});
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++) {
+                const int4 w = wq[s][rw];
+                A[0][rw] = q8_to_bf16_u((unsigned)w.x, (unsigned)w.y);
+                A[1][rw] = q8_to_bf16_u((unsigned)w.z, (unsigned)w.w);
+            }
+#pragma unroll
+            for (int st = 0; st < 2; st++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                    for (int sp = 0; sp < 3; sp++) {
+                        const v8bf xb8 = __builtin_bit_cast(v8bf, B[st][tt][sp]);
+#pragma unroll
+                        for (int rw = 0; rw < RW; rw++)
+                            acc[rw][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[st][rw], xb8, acc[rw][tt], 0, 0, 0);
+                        xsum[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, xb8, xsum[tt], 0, 0, 0);
+                    }
+            w_load(b + PF, sc);
+        });
+    };
+    if constexpr (NBC > 0) {
+#pragma unroll
+        for (int b0 = 0; b0 < NBC; b0 += PF) step(b0);
+    } else {
+        for (int b0 = 0; b0 < nb; b0 += PF) step(b0);
+    }
+
+    // sum x (w + 128) - 128 sum x = sum x w
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) acc[rw][tt] -= 128.f * xsum[tt];
+    if (KS > 1) {
+        if (ks > 0)
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++) s_red[ks - 1][rg][rw][tt][lane] = acc[rw][tt];
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int j = 0; j < KS - 1; j++)
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+                for (int tt = 0; tt < TT; tt++) acc[rw][tt] += s_red[j][rg][rw][tt][lane];
+    }
+    // lane holds rows 4g .. 4g+3 of row tile rw for token l16 of token tile tt
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++) {
+        const int o = r0 + 16 * rw + 4 * g;
+        if (o >= p.O) continue;
+        const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            const int t = t0 + 16 * tt + l16;
+            if (t >= p.T) continue;
+            float4 y;
+            y.x = acc[rw][tt][0] * sc.x;
+            y.y = acc[rw][tt][1] * sc.y;
+            y.z = acc[rw][tt][2] * sc.z;
+            y.w = acc[rw][tt][3] * sc.w;
+            *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = y;
+        }
+    }
+}
+
+inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+template <int RG, int KS>
+void launch_q8(const ProjArgs &p, hipStream_t st) {
+    constexpr int TT = kQ8Tok / 16;
+    const dim3 grid((p.O + RG * kQ8Rows - 1) / (RG * kQ8Rows), (p.T + kQ8Tok - 1) / kQ8Tok);
+    const int nb = p.I / KS / 64;
+    const dim3 blk(4 * OMH_WAVE);
+    switch (nb) {
+    case 1: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 1, 1>), grid, blk, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 2, 2>), grid, blk, 0, st, p); break;
+    case 4: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 4, 4>), grid, blk, 0, st, p); break;
+    case 8: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 4, 8>), grid, blk, 0, st, p); break;
+    case 16: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 4, 16>), grid, blk, 0, st, p); break;
+    case 32: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 4, 32>), grid, blk, 0, st, p); break;
+    default:
+        if (nb % 4 == 0) hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 4, 0>), grid, blk, 0, st, p);
+        else if (nb % 2 == 0) hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 2, 0>), grid, blk, 0, st, p);
+        else hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 1, 0>), grid, blk, 0, st, p);
+    }
 }
 
 }  // namespace
@@ -327,18 +598,41 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
 #undef OMH_GEMV
         return hipGetLastError();
     }
+    // int8 rows on the bf16 matrix cores (bf16 x 3), the fp32 rows after
+    if (p.n_q > 0 && p.xb && al16(p.x) && al16(p.y) && p.ldx % 4 == 0 && p.ldy % 4 == 0) {
+        const size_t n8 = (size_t)p.T * (p.I / 8);
+        hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb, p.T, p.I);
+        ProjArgs q = p;
+        q.O = p.n_q;
+        // enough workgroups for the device (a k split where rows are few)
+        const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;
+        const int rb = (q.O + kQ8Rows - 1) / kQ8Rows;           // row blocks of one wave
+        if (rb / 4 * tb >= 128 || p.I % 128 != 0) launch_q8<4, 1>(q, st);
+        else launch_q8<2, 2>(q, st);
+        if (p.O == p.n_q) return hipGetLastError();
+        ProjArgs f = p;
+        f.y = p.y + p.n_q;
+        f.O = p.O - p.n_q;
+        f.n_q = 0;
+        f.Q = nullptr;
+        f.scale = nullptr;
+        return launch_proj(f, st);
+    }
     // one row tile per workgroup (k split over its 4 waves) unless that
     // leaves k-slices narrower than a 64-wide block or far more workgroups
     // than the device holds at once
-    const int tb = (p.T + kMfmaTok - 1) / kMfmaTok;
+    // (a few rows, e.g. the fp32 b / a rows beside int8 ones: one token
+    // tile per workgroup, so there are more of them)
     const int tiles = (p.O + 15) / 16;
+    const int tpw = tiles * ((p.T + kMfmaTok - 1) / kMfmaTok) < 64 ? 16 : kMfmaTok;
+    const int tb = (p.T + tpw - 1) / tpw;
     int rt = 1;
     if (p.I % 256 != 0 || tiles * tb > 4096) rt = 2;
     if (p.I % 128 != 0 || tiles * tb > 8192) rt = 4;
     const dim3 grid((tiles + rt - 1) / rt, tb);
-    if (rt == 4) launch_mfma_rt<4>(p, grid, st);
-    else if (rt == 2) launch_mfma_rt<2>(p, grid, st);
-    else launch_mfma_rt<1>(p, grid, st);
+    if (rt == 4) launch_mfma_rt<4>(p, grid, tpw, st);
+    else if (rt == 2) launch_mfma_rt<2>(p, grid, tpw, st);
+    else launch_mfma_rt<1>(p, grid, tpw, st);
     return hipGetLastError();
 }
 

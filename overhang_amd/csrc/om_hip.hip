@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -71,7 +72,7 @@ struct Scratch {
     void *p = nullptr;
     size_t n = 0;
 };
-Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre;
+Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre, g_xb;
 
 int ensure(Scratch &s, size_t bytes) {
     if (bytes <= s.n) return OMH_OK;
@@ -184,16 +185,22 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     const int D = L.d.hidden;
     if (int rc = ensure(g_in, (size_t)B * L.in_rows * sizeof(float))) return rc;
     if (int rc = ensure(g_core, (size_t)B * L.vdim * sizeof(float))) return rc;
+    uint16_t *xb = nullptr;
+    if (B > 4 && (L.in_nq > 0 || L.out_nq > 0)) {
+        const size_t xbn = std::max(proj_xb_bytes(B, D), proj_xb_bytes(B, L.vdim));
+        if (int rc = ensure(g_xb, xbn)) return rc;
+        xb = static_cast<uint16_t *>(g_xb.p);
+    }
     float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
     ProjArgs p{};
-    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows;
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
@@ -236,16 +243,22 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     const int D = L.d.hidden;
     if (int rc = ensure(g_in, (size_t)T * L.in_rows * sizeof(float))) return rc;
     if (int rc = ensure(g_core, (size_t)T * L.vdim * sizeof(float))) return rc;
+    uint16_t *xb = nullptr;
+    if (T > 4 && (L.in_nq > 0 || L.out_nq > 0)) {
+        const size_t xbn = std::max(proj_xb_bytes(T, D), proj_xb_bytes(T, L.vdim));
+        if (int rc = ensure(g_xb, xbn)) return rc;
+        xb = static_cast<uint16_t *>(g_xb.p);
+    }
     float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
     ProjArgs p{};
-    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows;
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     if (int rc = prefill_core(li, seq, T, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;

@@ -76,7 +76,10 @@ struct ProjArgs {
     const float *W;        // [O - n_q][I]
     int64_t ldx, ldy;
     int T, I, O, n_q;
+    uint16_t *xb;          // scratch for x as three bf16 planes [3][T][I] (int8 rows, T > 4), or null
 };
+// bytes of the bf16 x planes a projection of T tokens over I inputs uses
+inline size_t proj_xb_bytes(int T, int I) { return (size_t)3 * T * I * sizeof(uint16_t); }
 // hidden size I and int8 row count n_q the projection kernels take
 bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
