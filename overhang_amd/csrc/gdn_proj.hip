@@ -330,35 +330,46 @@ void launch_mfma_rt(const ProjArgs &p, dim3 grid, int tpw, hipStream_t st) {
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 constexpr int kQ8Rows = 32;                 // rows per wave
+constexpr int kQ8K = 64;                    // k per staged block
 constexpr int kQ8Tok = 32;                  // tokens per workgroup
 
-// planes[p][t][k] = term p of x[t][k]; 8 values per thread
+// planes[p][t][k] = term p of x[t][k], and the sum of x[t][k] over each
+// 64-wide k block (sums[t][k / 64], after the planes); 8 values per thread
 __global__ __launch_bounds__(256)
 void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ xb, int T, int I) {
     const size_t n8 = (size_t)T * (I / 8);
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= n8) return;
-    const int t = (int)(e / (I / 8)), k = (int)(e % (I / 8)) * 8;
+    const bool live = e < n8;
+    const size_t ec = live ? e : n8 - 1;
+    const int t = (int)(ec / (I / 8)), k = (int)(ec % (I / 8)) * 8;
     const float4 a = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + k);
     const float4 b = *reinterpret_cast<const float4 *>(x + (size_t)t * ldx + k + 4);
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     v8bf hi, mid, lo;
+    float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         hi[j] = (__bf16)v[j];
         const float r1 = v[j] - (float)hi[j];
         mid[j] = (__bf16)r1;
         lo[j] = (__bf16)(r1 - (float)mid[j]);
+        sum += v[j];
     }
+    // the 8 threads of a 64-wide block are 8 consecutive lanes (I % 64 == 0)
+    sum += __shfl_xor(sum, 1, OMH_WAVE);
+    sum += __shfl_xor(sum, 2, OMH_WAVE);
+    sum += __shfl_xor(sum, 4, OMH_WAVE);
+    if (!live) return;
     const size_t plane = (size_t)T * I, o = (size_t)t * I + k;
     *reinterpret_cast<v8bf *>(xb + o) = hi;
     *reinterpret_cast<v8bf *>(xb + plane + o) = mid;
     *reinterpret_cast<v8bf *>(xb + 2 * plane + o) = lo;
+    if (k % 64 == 0) reinterpret_cast<float *>(xb + 3 * plane)[(size_t)t * (I / 64) + k / 64] = sum;
 }
 
 // 8 int8 weights w as bf16 of u = w + 128 (0..255, exact in bf16): one
 // unsigned-byte conversion per value and one pack per pair; the products
-// then carry + 128 x, which the caller takes off as 128 * (sum of x)
+// then carry + 128 x, which the epilogue takes off as 128 * (sum of x)
 __device__ __forceinline__ v8bf q8_to_bf16_u(unsigned lo, unsigned hi) {
     const unsigned u[2] = {lo ^ 0x80808080u, hi ^ 0x80808080u};
     v8bf r;
@@ -375,8 +386,10 @@ __device__ __forceinline__ v8bf q8_to_bf16_u(unsigned lo, unsigned hi) {
 template <int RG, int KS, int TT, int PF, int NBC>
 __global__ __launch_bounds__(4 * OMH_WAVE)
 void proj_q8_bf16x3_kernel(const ProjArgs p) {
-    constexpr int RW = kQ8Rows / 16, KB = 64, XR = KB + 8;     // padded staging row (bf16)
-    constexpr int NU4 = KS * 3 * TT * 16 * (KB / 8) / (4 * OMH_WAVE);   // 16-byte pieces per thread per block
+    constexpr int RW = kQ8Rows / 16, KB = kQ8K, XR = KB + 8;     // padded staging row (bf16)
+    constexpr int NST = KB / 32;                                 // 32-wide MFMA steps per block
+    constexpr int NW4 = KB / 64;                                 // 16-byte weight loads per row tile and block
+    constexpr int NU4 = KS * 3 * TT * 16 * (KB / 8) / (4 * OMH_WAVE);   // 16-byte x pieces per thread per block
     static_assert(NU4 >= 1 && KS * 3 * TT * 16 * (KB / 8) % (4 * OMH_WAVE) == 0, "x staging split");
     __shared__ __align__(16) __bf16 xs[2][KS][3][TT * 16][XR];
     __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RG][RW][TT][OMH_WAVE];
@@ -413,7 +426,7 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
             int kq, sp, t, c;
             piece(f, kq, sp, t, c);
             xr[slot][f] = *reinterpret_cast<const v4u *>(p.xb + sp * plane + (size_t)min(t0 + t, p.T - 1) * p.I + kq * klen +
-                                                           b * KB + 8 * c);
+                                                          b * KB + 8 * c);
         }
     };
     auto x_stage = [&](int buf, auto slot_c) __attribute__((always_inline)) {
@@ -426,28 +439,27 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
         }
     };
 
-    // weights: 16 int8 per lane per row tile and block, PF blocks ahead
+    // weights: KB / 4 int8 per lane per row tile and block, PF blocks ahead;
+    // lane group g holds k = (KB / 4) g + 8 s + j of step s
     const int8_t *wrow[RW];
 #pragma unroll
     for (int rw = 0; rw < RW; rw++)
-        wrow[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + ks * klen + 16 * g;
-    int4 wq[PF][RW];
+        wrow[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + ks * klen + (KB / 4) * g;
+    int4 wq[PF][RW][NW4];
     auto w_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
         constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
-        for (int rw = 0; rw < RW; rw++) wq[slot][rw] = *reinterpret_cast<const int4 *>(wrow[rw] + (size_t)min(b, nb - 1) * KB);
+        for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+            for (int h = 0; h < NW4; h++)
+                wq[slot][rw][h] = *reinterpret_cast<const int4 *>(wrow[rw] + (size_t)min(b, nb - 1) * KB + 16 * h);
     };
 
-    v4f acc[RW][TT], xsum[TT];            // xsum: sum of x over k per token (every row alike)
+    v4f acc[RW][TT];
 #pragma unroll
     for (int rw = 0; rw < RW; rw++)
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) acc[rw][tt] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) xsum[tt] = v4f{0.f, 0.f, 0.f, 0.f};
-    v8bf ones;
-#pragma unroll
-    for (int j = 0; j < 8; j++) ones[j] = (__bf16)1.f;
 
     // the prologue issues x then w per block, as the loop does, so the wait
     // counts are the same on entry and on the back edge
@@ -471,36 +483,35 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
             // every x operand of the block read at once (one LDS latency);
             // block b+1 staged into the other buffer while this block's
             // products run (its writes are done by the next barrier); the
-            // weights unpacked meanwhile, then the 24 products
-            v4u B[2][TT][3];
-            v8bf A[2][RW];
+            // weights unpacked meanwhile, then the products
+            v4u B[NST][TT][3];
+            v8bf A[NST][RW];
 #pragma unroll
-            for (int st = 0; st < 2; st++)
+            for (int st = 0; st < NST; st++)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
 #pragma unroll
                     for (int sp = 0; sp < 3; sp++)
-                        B[st][tt][sp] = *reinterpret_cast<const v4u *>(&xs[buf][ks][sp][16 * tt + l16][16 * g + 8 * st]);
+                        B[st][tt][sp] = *reinterpret_cast<const v4u *>(&xs[buf][ks][sp][16 * tt + l16][(KB / 4) * g + 8 * st]);
             x_stage(buf ^ 1, std::integral_constant<int, (s + 1) % XD>{});
             x_load(b + 1 + XD, std::integral_constant<int, (s + 1) % XD>{});
 #pragma unroll
-            for (int rw = 0; rw < RW; rw++) {
-                const int4 w = wq[s][rw];
-                A[0][rw] = q8_to_bf16_u((unsigned)w.x, (unsigned)w.y);
-                A[1][rw] = q8_to_bf16_u((unsigned)w.z, (unsigned)w.w);
-            }
+            for (int rw = 0; rw < RW; rw++)
 #pragma unroll
-            for (int st = 0; st < 2; st++)
+                for (int st = 0; st < NST; st++) {
+                    const int4 w = wq[s][rw][st / 2];
+                    A[st][rw] = st % 2 == 0 ? q8_to_bf16_u((unsigned)w.x, (unsigned)w.y) : q8_to_bf16_u((unsigned)w.z, (unsigned)w.w);
+                }
+#pragma unroll
+            for (int st = 0; st < NST; st++)
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
 #pragma unroll
-                    for (int sp = 0; sp < 3; sp++) {
-                        const v8bf xb8 = __builtin_bit_cast(v8bf, B[st][tt][sp]);
+                    for (int sp = 0; sp < 3; sp++)
 #pragma unroll
                         for (int rw = 0; rw < RW; rw++)
-                            acc[rw][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[st][rw], xb8, acc[rw][tt], 0, 0, 0);
-                        xsum[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, xb8, xsum[tt], 0, 0, 0);
-                    }
+                            acc[rw][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[st][rw], __builtin_bit_cast(v8bf, B[st][tt][sp]),
+                                                                                  acc[rw][tt], 0, 0, 0);
             w_load(b + PF, sc);
         });
     };
@@ -511,11 +522,26 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
         for (int b0 = 0; b0 < nb; b0 += PF) step(b0);
     }
 
-    // sum x (w + 128) - 128 sum x = sum x w
+    // sum x (w + 128) - 128 sum x = sum x w, the sums of the k-slice's
+    // 64-wide blocks from the split kernel
+    {
+        const float *sums = reinterpret_cast<const float *>(p.xb + 3 * plane);
 #pragma unroll
-    for (int rw = 0; rw < RW; rw++)
+        for (int tt = 0; tt < TT; tt++) {
+            const float *sr = sums + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * (p.I / 64) + ks * (klen / 64);
+            // (independent loads in flight, not one L2 round trip per block)
+            float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            const int nq = klen / 64;
+            int q = 0;
+            for (; q + 8 <= nq; q += 8)
 #pragma unroll
-        for (int tt = 0; tt < TT; tt++) acc[rw][tt] -= 128.f * xsum[tt];
+                for (int u = 0; u < 8; u++) part[u] += sr[q + u];
+            for (; q < nq; q++) part[0] += sr[q];
+            const float sx = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++) acc[rw][tt] -= 128.f * sx;
+        }
+    }
     if (KS > 1) {
         if (ks > 0)
 #pragma unroll
@@ -557,7 +583,7 @@ template <int RG, int KS>
 void launch_q8(const ProjArgs &p, hipStream_t st) {
     constexpr int TT = kQ8Tok / 16;
     const dim3 grid((p.O + RG * kQ8Rows - 1) / (RG * kQ8Rows), (p.T + kQ8Tok - 1) / kQ8Tok);
-    const int nb = p.I / KS / 64;
+    const int nb = p.I / KS / kQ8K;
     const dim3 blk(4 * OMH_WAVE);
     switch (nb) {
     case 1: hipLaunchKernelGGL((proj_q8_bf16x3_kernel<RG, KS, TT, 1, 1>), grid, blk, 0, st, p); break;
@@ -599,7 +625,7 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         return hipGetLastError();
     }
     // int8 rows on the bf16 matrix cores (bf16 x 3), the fp32 rows after
-    if (p.n_q > 0 && p.xb && al16(p.x) && al16(p.y) && p.ldx % 4 == 0 && p.ldy % 4 == 0) {
+    if (p.n_q > 0 && p.xb && p.I % kQ8K == 0 && al16(p.x) && al16(p.y) && p.ldx % 4 == 0 && p.ldy % 4 == 0) {
         const size_t n8 = (size_t)p.T * (p.I / 8);
         hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb, p.T, p.I);
         ProjArgs q = p;
@@ -607,7 +633,7 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         // enough workgroups for the device (a k split where rows are few)
         const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;
         const int rb = (q.O + kQ8Rows - 1) / kQ8Rows;           // row blocks of one wave
-        if (rb / 4 * tb >= 128 || p.I % 128 != 0) launch_q8<4, 1>(q, st);
+        if (rb / 4 * tb >= 128 || p.I % (2 * kQ8K) != 0) launch_q8<4, 1>(q, st);
         else launch_q8<2, 2>(q, st);
         if (p.O == p.n_q) return hipGetLastError();
         ProjArgs f = p;

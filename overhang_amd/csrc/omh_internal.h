@@ -76,10 +76,10 @@ struct ProjArgs {
     const float *W;        // [O - n_q][I]
     int64_t ldx, ldy;
     int T, I, O, n_q;
-    uint16_t *xb;          // scratch for x as three bf16 planes [3][T][I] (int8 rows, T > 4), or null
+    uint16_t *xb;          // scratch: x as three bf16 planes [3][T][I], then fp32 sums over 64-wide k blocks [T][I/64] (int8 rows, T > 4), or null
 };
-// bytes of the bf16 x planes a projection of T tokens over I inputs uses
-inline size_t proj_xb_bytes(int T, int I) { return (size_t)3 * T * I * sizeof(uint16_t); }
+// bytes of the x planes and block sums a projection of T tokens over I inputs uses
+inline size_t proj_xb_bytes(int T, int I) { return (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float); }
 // hidden size I and int8 row count n_q the projection kernels take
 bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
