@@ -36,8 +36,8 @@
 //    slice order, so the result does not depend on arrival order.
 //
 // Conv history lives in a per-channel ring (omh_internal.h): readers use
-// the K-1 history slots, the single owner of a channel rewrites its entry
-// with the new input in the free slot.
+// the K-1 history slots, the single owner of a channel writes the new input
+// into the free slot.
 //
 // Thread layout: TPB threads hold RPT rows x 4 adjacent columns (a float4)
 // of a head (or slice); a wavefront's loads cover whole consecutive row
@@ -114,19 +114,26 @@ __device__ __forceinline__ float4 gated(float4 o, float rn, float4 gn, float4 zz
 // Conv inputs of the NIT channels a thread handles, loaded into registers
 // in one batch (vector memory operations complete in issue order for the
 // wait counter, so the first use waits for exactly these and what came
-// before them).
+// before them).  History is right-aligned: h[it][m] is the input
+// kConvRing-1-m tokens back, in ring slot (ph + 1 + m) mod kConvRing; the
+// taps are stored right-aligned the same way, so tap m multiplies h[m] and
+// the last tap the new input.
 template <int NIT>
 struct ConvIn {
-    float x[NIT];
-    float4 w[NIT], r[NIT];
+    static constexpr int NH = kConvRing - 1;
+    float x[NIT], h[NIT][NH];
+    float4 w[NIT];
     int gch[NIT];
 
     // gch_of(c) maps the workgroup's channel c < nch to a global channel.
     // The loads are branch-free (out-of-range slots load channel 0 and are
-    // marked gch = -1), so the compiler's wait counts stay exact.
+    // marked gch = -1; history slots a K < kConvRing kernel does not use
+    // repeat the first used slot's address), so the compiler's wait counts
+    // stay exact and no unused bytes are fetched.
     template <typename F>
     __device__ __forceinline__ void load(F gch_of, int nch, int tid, int tpb, const float *qkv, const float *conv_w,
-                                         const float *ring, int conv_dim, int seq) {
+                                         const float *ring, int conv_dim, int seq, int ph, int K) {
+        const int m0 = kConvRing - K;
 #pragma unroll
         for (int it = 0; it < NIT; it++) {
             const int c = tid + it * tpb;
@@ -134,21 +141,25 @@ struct ConvIn {
             gch[it] = c < nch ? g : -1;
             x[it] = qkv[g];
             w[it] = *reinterpret_cast<const float4 *>(conv_w + (size_t)g * kConvRing);
-            r[it] = *reinterpret_cast<const float4 *>(ring + ring_at(seq, g, conv_dim));
+            const float *rs = ring + ring_at(seq, 0, g, conv_dim);
+#pragma unroll
+            for (int m = 0; m < NH; m++)
+                h[it][m] = rs[(size_t)((ph + 1 + (m < m0 ? m0 : m)) & (kConvRing - 1)) * conv_dim];
         }
     }
     // conv1d + SiLU (op order as engines/qwen.c:311-319) of the it-th channel.
-    __device__ __forceinline__ float conv(int it, int K, int ph) const {
+    __device__ __forceinline__ float conv(int it, int K) const {
+        const float wt[kConvRing] = {w[it].x, w[it].y, w[it].z, w[it].w};
         float acc = 0.f;
-        for (int j = 0; j < K - 1; j++) acc += f4_get(w[it], j) * f4_get(r[it], ring_slot(ph, K, j));
-        acc += f4_get(w[it], K - 1) * x[it];
+#pragma unroll
+        for (int m = 0; m < NH; m++)
+            if (m >= kConvRing - K) acc += wt[m] * h[it][m];
+        acc += wt[kConvRing - 1] * x[it];
         return omh_silu(acc);
     }
-    // Ring entry with the new input in the free slot of phase ph.
-    __device__ __forceinline__ float4 appended(int it, int ph) const {
-        float4 e = r[it];
-        f4_set(e, ph & (kConvRing - 1), x[it]);
-        return e;
+    // Append the new input: it goes to the free slot of phase ph.
+    __device__ __forceinline__ void append(int it, float *ring, int conv_dim, int seq, int ph) const {
+        ring[ring_at(seq, ph & (kConvRing - 1), gch[it], conv_dim)] = x[it];
     }
 };
 
@@ -293,7 +304,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
                  return c < KD ? hk * KD + c
                                : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h0 * VD + (c - 2 * KD));
              },
-             nch, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b);
+             nch, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b, ph, K);
     const float *zrow = args.z + tok * args.ld_z + (size_t)h0 * VD;
     float zin[NZ];
 #pragma unroll
@@ -310,11 +321,11 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     for (int it = 0; it < NIT; it++) {
         if (cin.gch[it] < 0) continue;
         const int c = tid + it * TPB;
-        const float y = cin.conv(it, K, ph);
+        const float y = cin.conv(it, K);
         if (c < KD) s_q[c] = y;
         else if (c < 2 * KD) s_k[c - KD] = y;
         else s_v[c - 2 * KD] = y;
-        *reinterpret_cast<float4 *>(L.conv_st + ring_at(b, cin.gch[it], conv_dim)) = cin.appended(it, ph);
+        cin.append(it, L.conv_st, conv_dim, b, ph);
     }
 #pragma unroll
     for (int it = 0; it < NZ; it++) {
@@ -394,7 +405,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
                  return c < KD ? hk * KD + c
                                : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h * VD + col0 + (c - 2 * KD));
              },
-             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b);
+             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b, ph, K);
     const int t4 = tid < VD / 4 ? tid : 0;
     const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + t4 * 4);
     const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + t4 * 4);
@@ -411,12 +422,12 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     for (int it = 0; it < NIT; it++) {
         if (cin.gch[it] < 0) continue;
         const int c = tid + it * TPB;
-        const float y = cin.conv(it, K, ph);
+        const float y = cin.conv(it, K);
         bool own = true;
         if (c < KD) { s_q[c] = y; own = own_qk; }
         else if (c < 2 * KD) { s_k[c - KD] = y; own = own_qk; }
         else s_v[c - 2 * KD] = y;
-        if (own) *reinterpret_cast<float4 *>(L.conv_st + ring_at(b, cin.gch[it], conv_dim)) = cin.appended(it, ph);
+        if (own) cin.append(it, L.conv_st, conv_dim, b, ph);
     }
     if (tid == 0) {
         // gates (qwen.c:337-338)

@@ -72,9 +72,11 @@ __device__ __forceinline__ size_t panj(size_t hc, int j, int kt, int l) {
 }
 
 // ---------------------------------------------------------------- P2 commit
-// New conv history = last K-1 entries of [old history, x_0 .. x_{T-1}],
-// written in ring order for phase (p + T) mod ring size.  Every block reads
-// the phase from phase[epoch]; the new one goes to phase[1 - epoch] (block 0
+// New conv history = last K-1 entries of [old history, x_0 .. x_{T-1}] for
+// phase (p + T) mod ring size.  A token's ring slot is its index mod the
+// ring size, so old history values that stay are already in place: only
+// the new inputs among the last K-1 are written.  Every block reads the
+// phase from phase[epoch]; the new one goes to phase[1 - epoch] (block 0
 // also carries the other sequences' phases over) and the host flips the
 // layer's epoch after the launch, as for decode launches.
 __global__ __launch_bounds__(256)
@@ -84,16 +86,12 @@ void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
     const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
     const int nph = (ph + T) & (kConvRing - 1);
     if (c < conv_dim) {
-        float4 *ring = reinterpret_cast<float4 *>(a.L.conv_st + ring_at(a.seq, c, conv_dim));
-        const float4 old = *ring;
-        float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
+        float *rs = a.L.conv_st + ring_at(a.seq, 0, c, conv_dim);
         for (int j = 0; j < K - 1; j++) {
             const int idx = T + j;               // index into [old history (K-1), x_0 ..]
-            const float v = idx < K - 1 ? f4_get(old, ring_slot(ph, K, idx))
-                                        : a.qkv[(size_t)(idx - (K - 1)) * a.ld_qkv + c];
-            f4_set(e, ring_slot(nph, K, j), v);
+            if (idx >= K - 1)
+                rs[(size_t)ring_slot(nph, K, j) * conv_dim] = a.qkv[(size_t)(idx - (K - 1)) * a.ld_qkv + c];
         }
-        *ring = e;
     }
     if (blockIdx.x == 0) {
         int *nxt = a.L.phase + (1 - a.L.epoch) * a.L.max_seqs;
@@ -155,7 +153,8 @@ struct WyShape {
 // order as engines/qwen.c:311-319) + SiLU over NS consecutive tokens, the
 // outputs replacing the inputs in registers; tokens at or past nvalid are
 // zero.  The history h0 h1 h2 is the last three inputs (right-aligned: for
-// KK < 4 only the last KK-1 are used), w the taps 0..KK-1.
+// KK < 4 only the last KK-1 are used), w the taps right-aligned (tap j in
+// component 4-KK+j).
 template <int KK, int NS>
 __device__ __forceinline__ void conv_inplace(float (&x)[NS], float h0, float h1, float h2, float4 w, int nvalid) {
     const float wt[4] = {w.x, w.y, w.z, w.w};
@@ -165,8 +164,8 @@ __device__ __forceinline__ void conv_inplace(float (&x)[NS], float h0, float h1,
         const float xt = x[t];
         float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < KK - 1; j++) acc += wt[j] * h[3 - (KK - 1) + j];
-        acc += wt[KK - 1] * xt;
+        for (int j = 0; j < KK - 1; j++) acc += wt[4 - KK + j] * h[4 - KK + j];
+        acc += wt[3] * xt;
         h[0] = h[1];
         h[1] = h[2];
         h[2] = xt;
@@ -266,11 +265,11 @@ struct WyIn {
                 if (ts == 0) {
                     // the ring's K-1 history slots, oldest first, right-aligned
                     // (this waits for the load: once per sequence)
-                    const float4 rv =
-                        *reinterpret_cast<const float4 *>(a.L.conv_st + ring_at(a.seq, ch0 + cc, (2 * a.kh + a.vh) * D));
-                    h0v = KK >= 4 ? f4_get(rv, ring_slot(ph, KK, KK - 4)) : 0.f;
-                    h1v = KK >= 3 ? f4_get(rv, ring_slot(ph, KK, KK - 3)) : 0.f;
-                    h2v = f4_get(rv, ring_slot(ph, KK, KK - 2));
+                    const int conv_dim = (2 * a.kh + a.vh) * D;
+                    const float *rs = a.L.conv_st + ring_at(a.seq, 0, ch0 + cc, conv_dim);
+                    h0v = KK >= 4 ? rs[(size_t)((ph + 1) & (kConvRing - 1)) * conv_dim] : 0.f;
+                    h1v = KK >= 3 ? rs[(size_t)((ph + 2) & (kConvRing - 1)) * conv_dim] : 0.f;
+                    h2v = rs[(size_t)((ph + 3) & (kConvRing - 1)) * conv_dim];
                 } else {
                     h0v = col[(size_t)min(ts - 3, T - 1) * ld];
                     h1v = col[(size_t)min(ts - 2, T - 1) * ld];

@@ -313,10 +313,10 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
     int rc = OMH_OK;
 #define UP(dst, n, src) do { if ((rc = upload(&(dst), (size_t)(n), (src))) != OMH_OK) { free_layer(L); return rc; } } while (0)
     {
-        // device layout [conv_dim][kConvRing]: taps 0..K-1, zero padded
+        // device layout [conv_dim][kConvRing]: zeros, then taps 0..K-1
         std::vector<float> cw((size_t)L.conv_dim * kConvRing, 0.f);
         for (int c = 0; c < L.conv_dim; c++)
-            for (int j = 0; j < K; j++) cw[(size_t)c * kConvRing + j] = w->conv_w[(size_t)c * K + j];
+            for (int j = 0; j < K; j++) cw[(size_t)c * kConvRing + (kConvRing - K) + j] = w->conv_w[(size_t)c * K + j];
         UP(L.conv_w, cw.size(), cw.data());
     }
     UP(L.A_log, vh, w->A_log);
@@ -424,7 +424,7 @@ int omh_gdn_state_get(int li, int seq, float *conv, float *S) {
         HIP_OK(hipMemcpy(&ph, L.phase + (size_t)L.epoch * L.max_seqs + seq, sizeof(int), hipMemcpyDeviceToHost));
         for (int c = 0; c < L.conv_dim; c++)
             for (int j = 0; j < K - 1; j++)
-                conv[(size_t)c * (K - 1) + j] = ring[ring_at(0, c, L.conv_dim) + ring_slot(ph, K, j)];
+                conv[(size_t)c * (K - 1) + j] = ring[ring_at(0, ring_slot(ph, K, j), c, L.conv_dim)];
     }
     if (S) HIP_OK(hipMemcpy(S, L.S + seq * sn, sn * sizeof(float), hipMemcpyDeviceToHost));
     return OMH_OK;
@@ -442,7 +442,7 @@ int omh_gdn_state_set(int li, int seq, const float *conv, const float *S) {
         std::vector<float> ring(cn, 0.f);       // written at phase 0
         for (int c = 0; c < L.conv_dim; c++)
             for (int j = 0; j < K - 1; j++)
-                ring[ring_at(0, c, L.conv_dim) + ring_slot(0, K, j)] = conv[(size_t)c * (K - 1) + j];
+                ring[ring_at(0, ring_slot(0, K, j), c, L.conv_dim)] = conv[(size_t)c * (K - 1) + j];
         const int zero = 0;
         HIP_OK(hipMemcpy(L.conv_st + seq * cn, ring.data(), cn * sizeof(float), hipMemcpyHostToDevice));
         HIP_OK(hipMemcpy(L.phase + (size_t)L.epoch * L.max_seqs + seq, &zero, sizeof(int), hipMemcpyHostToDevice));

@@ -6,21 +6,24 @@
 
 namespace omh {
 
-// Conv history ring: every channel keeps kConvRing slots; at phase p the
-// K-1 history values, oldest first, sit in slots (p + kConvRing+1 - K + j)
-// mod kConvRing and slot p mod kConvRing is free.  Consuming a token writes
-// it into the free slot and advances p.  A channel's slots are one 16-byte
-// entry ([seq][conv_dim][kConvRing]); its owner rewrites the whole entry
-// with only the free slot changed, so a concurrent reader of the entry sees
-// the history slots it uses unchanged, and every write covers whole lines.
+// Conv history ring: every channel keeps kConvRing slots, and token n of a
+// sequence (counted from the last reset or state_set) sits in slot
+// n mod kConvRing.  At phase p (= tokens consumed, mod kConvRing) the K-1
+// history values, oldest first, are in slots (p + kConvRing+1 - K + j) mod
+// kConvRing and slot p is free.  Consuming a token writes it into the free
+// slot and advances p; no other slot changes, so readers of the history
+// slots never race with the writer.  Slot-major layout
+// [seq][kConvRing][conv_dim]: one slot of consecutive channels is one
+// contiguous run, so a token reads K-1 values and writes one per channel,
+// all in whole lines.
 constexpr int kConvRing = 4;          // supports conv kernels K = 2..4
 
 __host__ __device__ inline int ring_slot(int p, int K, int j) {
     return (p + kConvRing + 1 - K + j) & (kConvRing - 1);
 }
-// Offset of channel ch's ring entry for sequence seq.
-__host__ __device__ inline size_t ring_at(int seq, int ch, int conv_dim) {
-    return ((size_t)seq * conv_dim + ch) * kConvRing;
+// Offset of slot `slot` of channel ch for sequence seq.
+__host__ __device__ inline size_t ring_at(int seq, int slot, int ch, int conv_dim) {
+    return ((size_t)seq * kConvRing + slot) * conv_dim + ch;
 }
 // Element j (0..3) of a float4.
 __host__ __device__ inline float f4_get(const float4 &v, int j) {
@@ -35,11 +38,11 @@ __host__ __device__ inline void f4_set(float4 &v, int j, float x) {
 // reads phase[epoch][b] and writes phase[1-epoch][b], and the host flips
 // the layer's epoch after enqueueing it.
 struct LayerPtrs {
-    const float *conv_w;   // [conv_dim][kConvRing], taps 0..K-1 then zeros
+    const float *conv_w;   // [conv_dim][kConvRing], taps right-aligned: zeros, then taps 0..K-1
     const float *A_log;    // [vh]
     const float *dt_bias;  // [vh]
     const float *gnorm;    // [vd]
-    float *conv_st;        // [max_seqs][conv_dim][kConvRing] ring
+    float *conv_st;        // [max_seqs][kConvRing][conv_dim] ring
     float *S;              // [max_seqs][vh][kd][vd]
     int *phase;            // [2][max_seqs]
     float *o_raw;          // [max_seqs][vh][vd]   cross-slice gated-norm scratch
