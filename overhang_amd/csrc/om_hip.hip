@@ -168,7 +168,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
         A.b = b + t0 * ld_ab;
         A.core = core + t0 * vdim;
         A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
-        A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
+        A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.rep = d.vh / d.kh; A.K = d.conv_k; A.eps = d.eps;
         for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
         HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_variant(), st));
         for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;

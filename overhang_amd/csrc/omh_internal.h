@@ -65,6 +65,7 @@ struct DecodeArgs {
     int64_t ld_qkv, ld_z, ld_ab;
     int B, nl, kh, vh, K;
     float eps;
+    int rep;            // vh / kh
     LayerPtrs L[kMaxDecodeLayers];
 };
 
