@@ -247,16 +247,16 @@ __device__ __forceinline__ void mfma_tiles(const ProjArgs &p, int r0, int t0, in
     }
 }
 
+// One workgroup (bx, by) of the fp32-MFMA projection.
 template <int RT, int TT, int PF>
-__global__ __launch_bounds__(4 * OMH_WAVE)
-void proj_mfma_kernel(const ProjArgs p) {
+__device__ __forceinline__ void proj_mfma_wg(const ProjArgs &p, int bx, int by) {
     constexpr int KS = 4 / RT;
     __shared__ v4f s_red[KS > 1 ? KS - 1 : 1][RT][TT][OMH_WAVE];
     const int lane = threadIdx.x % OMH_WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
     const int rt = wv % RT, ks = wv / RT;
-    const int r0 = (blockIdx.x * RT + rt) * 16;
-    const int t0 = blockIdx.y * (TT * 16);
+    const int r0 = (bx * RT + rt) * 16;
+    const int t0 = by * (TT * 16);
     const int klen = p.I / KS, kbeg = ks * klen;
     v4f acc[4];
 #pragma unroll
@@ -288,6 +288,12 @@ void proj_mfma_kernel(const ProjArgs p) {
             const int t = t0 + 16 * tt + 4 * g + r;
             if (t < p.T) p.y[(size_t)t * p.ldy + o] = acc[tt][r] * sc;
         }
+}
+
+template <int RT, int TT, int PF>
+__global__ __launch_bounds__(4 * OMH_WAVE)
+void proj_mfma_kernel(const ProjArgs p) {
+    proj_mfma_wg<RT, TT, PF>(p, blockIdx.x, blockIdx.y);
 }
 
 template <int RT, int PF>
@@ -333,10 +339,26 @@ constexpr int kQ8Rows = 32;                 // rows per wave
 constexpr int kQ8K = 64;                    // k per staged block
 constexpr int kQ8Tok = 32;                  // tokens per workgroup
 
-// planes[p][t][k] = term p of x[t][k], and the sum of x[t][k] over each
-// 64-wide k block (sums[t][k / 64], after the planes); 8 values per thread
+// Layout of the x planes: per plane, 32-value chunks [2 * (I / 64)][T][32]
+// (bf16).  Chunk 2c + s of token t holds, at position 8g + j, the value at
+// k = 64c + 16g + 8s + j (g < 4, j < 8): exactly what lane group g of a
+// 16-token MFMA operand reads in step s of 64-wide k block c (the k order
+// both operands share).  So 16 tokens' operand for one step is one
+// contiguous 1 KiB run, and every 16-byte piece of 8 consecutive k is
+// contiguous.  Offset of the piece holding k = 8m .. 8m+7 of token t:
+__device__ __forceinline__ size_t xpiece(int m, int t, int T) {
+    return ((size_t)(2 * (m / 8) + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
+}
+
+// planes[p] = term p of x in the chunk layout above, and the sum of x[t][k]
+// over each 64-wide k block (sums[t][k / 64], after the planes); 8 values
+// per thread
+// (block 0 also clears the k-split arrival counters of the launch after it)
 __global__ __launch_bounds__(256)
-void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ xb, int T, int I) {
+void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__restrict__ xb, int T, int I, int *cnt,
+                         int ncnt) {
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < ncnt; i += 256) cnt[i] = 0;
     const size_t n8 = (size_t)T * (I / 8);
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     const bool live = e < n8;
@@ -360,7 +382,7 @@ void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__r
     sum += __shfl_xor(sum, 2, OMH_WAVE);
     sum += __shfl_xor(sum, 4, OMH_WAVE);
     if (!live) return;
-    const size_t plane = (size_t)T * I, o = (size_t)t * I + k;
+    const size_t plane = (size_t)T * I, o = xpiece(k / 8, t, T);
     *reinterpret_cast<v8bf *>(xb + o) = hi;
     *reinterpret_cast<v8bf *>(xb + plane + o) = mid;
     *reinterpret_cast<v8bf *>(xb + 2 * plane + o) = lo;
@@ -425,8 +447,8 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
         for (int f = 0; f < NU4; f++) {
             int kq, sp, t, c;
             piece(f, kq, sp, t, c);
-            xr[slot][f] = *reinterpret_cast<const v4u *>(p.xb + sp * plane + (size_t)min(t0 + t, p.T - 1) * p.I + kq * klen +
-                                                          b * KB + 8 * c);
+            xr[slot][f] = *reinterpret_cast<const v4u *>(
+                p.xb + sp * plane + xpiece((kq * klen + b * KB) / 8 + c, min(t0 + t, p.T - 1), p.T));
         }
     };
     auto x_stage = [&](int buf, auto slot_c) __attribute__((always_inline)) {
@@ -577,7 +599,315 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
     }
 }
 
+// ------------------------------------------------ int8 rows, wave tiles
+// The int8 rows on the bf16 matrix cores with a 64-row x 64-token output
+// tile per wave: each x fragment (16 tokens x one 32-wide k step of one
+// bf16 plane) feeds 4 row tiles and each weight fragment 4 token tiles x 3
+// planes.  A wave then needs 256 B of x and 43 B of weights per 16x16x32
+// product, loaded straight into registers (the x planes stay in L2, the
+// weights stream from HBM three blocks ahead), so no operand goes through
+// LDS and the main loop has no barriers.  The 4 waves of a workgroup take
+// consecutive k-subslices of the same tile and are summed through LDS in
+// wave order.  With few rows, G workgroups split k further: each stores
+// its partial tile, and the last of the G to arrive (arrival counter) sums
+// the G tiles in order, so the result does not depend on arrival order
+// (device-coherent atomic stores and loads, as the sliced decode norm).
+// Operand k order within a 64-wide block: lane (l%16, g) holds
+// k = 16g + 8s + j of step s, j < 8, on both operands.
+constexpr int kWvRows = 64, kWvTok = 64, kWvK = 64;
+constexpr int kWvTileFloats = kWvRows * kWvTok;          // one partial tile
+
+// Rows beside the int8 ones in the same launch: the fp32 rows of the
+// projection (the b / a rows of in_proj), run by kF32Wgs extra workgroups
+// of the fp32-MFMA path (one 16-row tile x 16 tokens each, k split over
+// its 4 waves), appended along x after the int8 row groups, so they run
+// alongside the int8 tiles instead of in a launch of their own.
+struct F32Part {
+    ProjArgs p;    // the fp32 rows as a projection of their own (n_q = 0)
+    int nrg;       // int8 row groups (gridDim.x without the extra workgroups)
+    int gx, nwg;   // fp32 workgroup grid width and count
+};
+
+template <int G, int WD, bool F32>
+__global__ __launch_bounds__(4 * OMH_WAVE, 1)
+void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
+    constexpr int RW = kWvRows / 16, TT = kWvTok / 16;
+    if constexpr (F32) {
+        if ((int)blockIdx.x >= f.nrg) {
+            const int i = (blockIdx.x - f.nrg) + (gridDim.x - f.nrg) * blockIdx.y;
+            if (i < f.nwg) proj_mfma_wg<1, 1, 8>(f.p, i % f.gx, i / f.gx);
+            return;
+        }
+    }
+    __shared__ v4f s_red[4][RW][TT][OMH_WAVE];
+    __shared__ float s_sx[kWvTok];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, gq = lane / 16;
+    const int r0 = blockIdx.x * kWvRows, t0 = blockIdx.y * kWvTok;
+    const int g = blockIdx.z;
+    const int k0 = (g * 4 + w) * (nb * kWvK);
+    const size_t plane = (size_t)p.T * p.I;
+
+    // sum of x per token for the epilogue, from the split kernel's sums of
+    // 64-wide blocks: thread tid takes a quarter of token tid / 4's blocks.
+    // Requested first, summed after the main loop (one load latency for
+    // the whole launch, hidden under it).
+    constexpr int kSxRegs = 16;
+    const int nq = p.I / 64, nq4 = nq / 4;
+    const float *sq = reinterpret_cast<const float *>(p.xb + 3 * plane) + (size_t)min(t0 + tid / 4, p.T - 1) * nq +
+                      (tid % 4) * nq4;
+    float sxr[kSxRegs];
+#pragma unroll
+    for (int j = 0; j < kSxRegs; j++) sxr[j] = sq[min(j, nq4 - 1)];
+
+    const int8_t *wp[RW];
+    const uint16_t *xp[TT];
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++) wp[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + k0 + 16 * gq;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) xp[tt] = p.xb + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * 32 + 8 * gq;
+    const size_t chunk = (size_t)p.T * 32;        // one 32-value chunk of every token
+
+    // x one 32-wide step ahead (two steps per block) in two register slots,
+    // the weights WD blocks ahead in WD.  The loop body is WD blocks, one
+    // period of both rings, so every slot index is a compile-time constant;
+    // the loop stays a loop (a fully unrolled body outruns the instruction
+    // cache: every wave would run thousands of instructions exactly once).
+    // The prologue leaves the same loads outstanding, in the same order, as
+    // the end of an iteration (the weights of the next WD - 1 blocks, the
+    // next step's x, the weights of the block after), so the wait counts
+    // agree on both edges into the loop.
+    int4 wq[WD][RW];
+    v4u xq[2][TT][3];
+    auto w_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        b = min(b, nb - 1);
+#pragma unroll
+        for (int rw = 0; rw < RW; rw++) wq[sl][rw] = *reinterpret_cast<const int4 *>(wp[rw] + b * kWvK);
+    };
+    auto x_load = [&](int q, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        q = min(q, 2 * nb - 1);
+        const size_t off = (size_t)(2 * (k0 / kWvK) + q) * chunk;   // step q of the wave's k range
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int sp = 0; sp < 3; sp++) xq[sl][tt][sp] = *reinterpret_cast<const v4u *>(xp[tt] + sp * plane + off);
+    };
+
+    v4f acc[RW][TT];
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) acc[rw][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // step st of a block from x slot xs and weight slot ws
+    auto step = [&](auto xs_c, auto ws_c, auto st_c) __attribute__((always_inline)) {
+        constexpr int xs = decltype(xs_c)::value, ws = decltype(ws_c)::value, st = decltype(st_c)::value;
+        v8bf A[RW];
+#pragma unroll
+        for (int rw = 0; rw < RW; rw++) {
+            const int4 w4 = wq[ws][rw];
+            A[rw] = st == 0 ? q8_to_bf16_u((unsigned)w4.x, (unsigned)w4.y) : q8_to_bf16_u((unsigned)w4.z, (unsigned)w4.w);
+        }
+#pragma unroll
+        for (int sp = 0; sp < 3; sp++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int rw = 0; rw < RW; rw++)
+                    acc[rw][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        A[rw], __builtin_bit_cast(v8bf, xq[xs][tt][sp]), acc[rw][tt], 0, 0, 0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    static_for<WD - 1>([&](auto jc) __attribute__((always_inline)) { w_load(decltype(jc)::value, jc); });
+    x_load(0, I0{});
+    w_load(WD - 1, std::integral_constant<int, WD - 1>{});
+#pragma unroll 1
+    for (int b0 = 0; b0 < nb; b0 += WD) {
+        // (the scheduler would otherwise sink each prefetch next to its
+        // use, where its wait drains everything in flight)
+        static_for<WD>([&](auto jc) __attribute__((always_inline)) {
+            constexpr int j = decltype(jc)::value;
+            const int q = 2 * (b0 + j);
+            __builtin_amdgcn_sched_barrier(0);
+            x_load(q + 1, I1{});
+            __builtin_amdgcn_sched_barrier(0);
+            step(I0{}, jc, I0{});
+            __builtin_amdgcn_sched_barrier(0);
+            x_load(q + 2, I0{});
+            __builtin_amdgcn_sched_barrier(0);
+            step(I1{}, jc, I1{});
+            __builtin_amdgcn_sched_barrier(0);
+            w_load(b0 + j + WD, jc);
+        });
+    }
+
+    // the workgroup's 4 k-subslices, in wave order; wave w then finishes
+    // row tile w
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) s_red[w][rw][tt][lane] = acc[rw][tt];
+    {
+        float sx = 0.f;
+#pragma unroll
+        for (int j = 0; j < kSxRegs; j++) sx += j < nq4 ? sxr[j] : 0.f;
+        for (int j = kSxRegs; j < nq4; j++) sx += sq[j];
+        sx += __shfl_xor(sx, 1, OMH_WAVE);
+        sx += __shfl_xor(sx, 2, OMH_WAVE);
+        if (tid % 4 == 0) s_sx[tid / 4] = sx;
+    }
+    __syncthreads();
+    v4f y[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+        y[tt] = ((s_red[0][w][tt][lane] + s_red[1][w][tt][lane]) + s_red[2][w][tt][lane]) + s_red[3][w][tt][lane];
+
+    if constexpr (G > 1) {
+        const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+        float *mine = p.part + (tile * G + g) * kWvTileFloats;
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            float *d = mine + ((w * TT + tt) * OMH_WAVE + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) __hip_atomic_store(d + r, y[tt][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);           // this thread's stores are complete
+        __syncthreads();
+        if (tid == 0) s_last = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+        __syncthreads();
+        if (!s_last) return;
+        // all G partial tiles requested at once, then summed in order
+        v4f pt[G][TT];
+#pragma unroll
+        for (int gg = 0; gg < G; gg++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+                const float *q = p.part + (tile * G + gg) * kWvTileFloats + ((w * TT + tt) * OMH_WAVE + lane) * 4;
+#pragma unroll
+                for (int r = 0; r < 4; r++) pt[gg][tt][r] = __hip_atomic_load(q + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            y[tt] = pt[0][tt];
+#pragma unroll
+            for (int gg = 1; gg < G; gg++) y[tt] += pt[gg][tt];
+        }
+        if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // sum x (w + 128) - 128 sum x = sum x w, times the row scales
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) y[tt] -= 128.f * s_sx[16 * tt + l16];
+    // lane holds rows 4g .. 4g+3 of row tile w for token l16 of token tile tt
+    const int o = r0 + 16 * w + 4 * gq;
+    if (o >= p.O) return;
+    const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int t = t0 + 16 * tt + l16;
+        if (t >= p.T) continue;
+        float4 v;
+        v.x = y[tt][0] * sc.x;
+        v.y = y[tt][1] * sc.y;
+        v.z = y[tt][2] * sc.z;
+        v.w = y[tt][3] * sc.w;
+        *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = v;
+    }
+}
+
+// Launch shape of the fp32-MFMA projection: one row tile per workgroup (k
+// split over its 4 waves) unless that leaves k-slices narrower than a
+// 64-wide block or far more workgroups than the device holds at once; a
+// few rows (e.g. the fp32 b / a rows beside int8 ones) take one token tile
+// per workgroup, so there are more of them.
+struct F32Plan {
+    int rt, tpw;
+    dim3 grid;
+};
+F32Plan f32_plan(const ProjArgs &p) {
+    F32Plan f;
+    const int tiles = (p.O + 15) / 16;
+    f.tpw = tiles * ((p.T + kMfmaTok - 1) / kMfmaTok) < 64 ? 16 : kMfmaTok;
+    const int tb = (p.T + f.tpw - 1) / f.tpw;
+    f.rt = 1;
+    if (p.I % 256 != 0 || tiles * tb > 4096) f.rt = 2;
+    if (p.I % 128 != 0 || tiles * tb > 8192) f.rt = 4;
+    f.grid = dim3((tiles + f.rt - 1) / f.rt, tb);
+    return f;
+}
+
+// The int8 rows of q; with f32 (the fp32 rows, n_q = 0) also those, in the
+// same launch, when their plan is the one-token-tile shape the wave kernel
+// carries (proj_mfma_wg<1, 1, 8>).  Returns false (nothing launched) for a
+// shape the kernel does not take; *f32_done says whether f32 was launched.
+bool launch_q8_wave(const ProjArgs &p, int G, const ProjArgs *f32, bool *f32_done, hipStream_t st) {
+    constexpr int WD = 2;
+    const int nb = p.I / (4 * kWvK * G);
+    if (nb < WD || nb % WD != 0) return false;
+    F32Part f{};
+    f.nrg = (p.O + kWvRows - 1) / kWvRows;
+    const int ty = (p.T + kWvTok - 1) / kWvTok;
+    bool with = false;
+    if (f32 && G == 1) {
+        const F32Plan fp = f32_plan(*f32);
+        with = fp.rt == 1 && fp.tpw == 16 && fp.grid.y > 1 && f32->I / 4 / 64 % 8 == 0;
+        if (with) {
+            f.p = *f32;
+            f.gx = fp.grid.x;
+            f.nwg = fp.grid.x * fp.grid.y;
+        }
+    }
+    *f32_done = with;
+    const int extra = with ? (f.nwg + ty - 1) / ty : 0;
+    const dim3 grid(f.nrg + extra, ty, G), blk(4 * OMH_WAVE);
+    switch (G) {
+    case 1:
+        if (with) hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, true>), grid, blk, 0, st, p, nb, f);
+        else hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, false>), grid, blk, 0, st, p, nb, f);
+        return true;
+    case 2: hipLaunchKernelGGL((proj_q8_wave_kernel<2, WD, false>), grid, blk, 0, st, p, nb, f); return true;
+    case 4: hipLaunchKernelGGL((proj_q8_wave_kernel<4, WD, false>), grid, blk, 0, st, p, nb, f); return true;
+    case 8: hipLaunchKernelGGL((proj_q8_wave_kernel<8, WD, false>), grid, blk, 0, st, p, nb, f); return true;
+    default: return false;
+    }
+}
+
 inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+// k split of the wave-tile kernel: 1, or doubled while the launch has fewer
+// than 768 waves (three quarters of the SIMDs) and each wave keeps at least
+// 4 blocks of k; 0 if the kernel does not take the shape
+int q8_wave_split(int O, int T, int I) {
+    if (I % (4 * kWvK) != 0) return 0;
+    const long tiles = (long)((O + kWvRows - 1) / kWvRows) * ((T + kWvTok - 1) / kWvTok);
+    int G = 1;
+    while (G < 8 && tiles * 4 * G < 768 && I % (4 * kWvK * 2 * G) == 0 && I / (4 * kWvK * 2 * G) >= 4) G *= 2;
+    const int nb = I / (4 * kWvK * G);
+    return nb >= 2 && nb % 2 == 0 ? G : 0;
+}
+
+struct XbLayout {
+    size_t part, cnt, total;   // byte offsets of the partial tiles and counters, total bytes
+    int G, ncnt;
+};
+XbLayout xb_layout(int T, int I, int n_q) {
+    XbLayout l{};
+    const size_t planes = (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float);
+    l.G = n_q > 0 ? q8_wave_split(n_q, T, I) : 0;
+    const size_t tiles = (size_t)((n_q + kWvRows - 1) / kWvRows) * ((T + kWvTok - 1) / kWvTok);
+    l.part = (planes + 255) / 256 * 256;
+    const size_t npart = l.G > 1 ? tiles * l.G * kWvTileFloats * sizeof(float) : 0;
+    l.cnt = l.part + npart;
+    l.ncnt = l.G > 1 ? (int)tiles : 0;
+    l.total = l.cnt + (size_t)l.ncnt * sizeof(int);
+    return l;
+}
 
 template <int RG, int KS>
 void launch_q8(const ProjArgs &p, hipStream_t st) {
@@ -603,6 +933,8 @@ void launch_q8(const ProjArgs &p, hipStream_t st) {
 
 bool proj_supported(int I, int n_q) { return I >= 64 && I % 64 == 0 && n_q % 16 == 0; }
 
+size_t proj_xb_bytes(int T, int I, int n_q) { return xb_layout(T, I, n_q).total; }
+
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
     if (p.O <= 0 || p.T <= 0) return hipSuccess;
     if (!proj_supported(p.I, p.n_q)) return hipErrorInvalidValue;
@@ -626,39 +958,37 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
     }
     // int8 rows on the bf16 matrix cores (bf16 x 3), the fp32 rows after
     if (p.n_q > 0 && p.xb && p.I % kQ8K == 0 && al16(p.x) && al16(p.y) && p.ldx % 4 == 0 && p.ldy % 4 == 0) {
-        const size_t n8 = (size_t)p.T * (p.I / 8);
-        hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb, p.T, p.I);
+        const XbLayout lay = xb_layout(p.T, p.I, p.n_q);
+        if (lay.total > p.xb_n) return hipErrorInvalidValue;
         ProjArgs q = p;
         q.O = p.n_q;
-        // enough workgroups for the device (a k split where rows are few)
-        const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;
-        const int rb = (q.O + kQ8Rows - 1) / kQ8Rows;           // row blocks of one wave
-        if (rb / 4 * tb >= 128 || p.I % (2 * kQ8K) != 0) launch_q8<4, 1>(q, st);
-        else launch_q8<2, 2>(q, st);
-        if (p.O == p.n_q) return hipGetLastError();
+        q.part = reinterpret_cast<float *>(reinterpret_cast<char *>(p.xb) + lay.part);
+        q.cnt = reinterpret_cast<int *>(reinterpret_cast<char *>(p.xb) + lay.cnt);
+        const size_t n8 = (size_t)p.T * (p.I / 8);
+        hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb, p.T,
+                           p.I, q.cnt, lay.ncnt);
         ProjArgs f = p;
         f.y = p.y + p.n_q;
         f.O = p.O - p.n_q;
         f.n_q = 0;
         f.Q = nullptr;
         f.scale = nullptr;
+        bool f32_done = false;
+        const bool done = lay.G > 0 && launch_q8_wave(q, lay.G, p.O > p.n_q ? &f : nullptr, &f32_done, st);
+        if (!done) {
+            // enough workgroups for the device (a k split where rows are few)
+            const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;
+            const int rb = (q.O + kQ8Rows - 1) / kQ8Rows;       // row blocks of one wave
+            if (rb / 4 * tb >= 128 || p.I % (2 * kQ8K) != 0) launch_q8<4, 1>(q, st);
+            else launch_q8<2, 2>(q, st);
+        }
+        if (p.O == p.n_q || f32_done) return hipGetLastError();
         return launch_proj(f, st);
     }
-    // one row tile per workgroup (k split over its 4 waves) unless that
-    // leaves k-slices narrower than a 64-wide block or far more workgroups
-    // than the device holds at once
-    // (a few rows, e.g. the fp32 b / a rows beside int8 ones: one token
-    // tile per workgroup, so there are more of them)
-    const int tiles = (p.O + 15) / 16;
-    const int tpw = tiles * ((p.T + kMfmaTok - 1) / kMfmaTok) < 64 ? 16 : kMfmaTok;
-    const int tb = (p.T + tpw - 1) / tpw;
-    int rt = 1;
-    if (p.I % 256 != 0 || tiles * tb > 4096) rt = 2;
-    if (p.I % 128 != 0 || tiles * tb > 8192) rt = 4;
-    const dim3 grid((tiles + rt - 1) / rt, tb);
-    if (rt == 4) launch_mfma_rt<4>(p, grid, tpw, st);
-    else if (rt == 2) launch_mfma_rt<2>(p, grid, tpw, st);
-    else launch_mfma_rt<1>(p, grid, tpw, st);
+    const F32Plan fp = f32_plan(p);
+    if (fp.rt == 4) launch_mfma_rt<4>(p, fp.grid, fp.tpw, st);
+    else if (fp.rt == 2) launch_mfma_rt<2>(p, fp.grid, fp.tpw, st);
+    else launch_mfma_rt<1>(p, fp.grid, fp.tpw, st);
     return hipGetLastError();
 }
 

@@ -187,20 +187,20 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     if (int rc = ensure(g_core, (size_t)B * L.vdim * sizeof(float))) return rc;
     uint16_t *xb = nullptr;
     if (B > 4 && (L.in_nq > 0 || L.out_nq > 0)) {
-        const size_t xbn = std::max(proj_xb_bytes(B, D), proj_xb_bytes(B, L.vdim));
+        const size_t xbn = std::max(proj_xb_bytes(B, D, L.in_nq), proj_xb_bytes(B, L.vdim, L.out_nq));
         if (int rc = ensure(g_xb, xbn)) return rc;
         xb = static_cast<uint16_t *>(g_xb.p);
     }
     float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
     ProjArgs p{};
-    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb;
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
@@ -245,20 +245,20 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     if (int rc = ensure(g_core, (size_t)T * L.vdim * sizeof(float))) return rc;
     uint16_t *xb = nullptr;
     if (T > 4 && (L.in_nq > 0 || L.out_nq > 0)) {
-        const size_t xbn = std::max(proj_xb_bytes(T, D), proj_xb_bytes(T, L.vdim));
+        const size_t xbn = std::max(proj_xb_bytes(T, D, L.in_nq), proj_xb_bytes(T, L.vdim, L.out_nq));
         if (int rc = ensure(g_xb, xbn)) return rc;
         xb = static_cast<uint16_t *>(g_xb.p);
     }
     float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
     ProjArgs p{};
-    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb;
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     if (int rc = prefill_core(li, seq, T, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;

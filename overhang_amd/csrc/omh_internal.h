@@ -80,10 +80,13 @@ struct ProjArgs {
     const float *W;        // [O - n_q][I]
     int64_t ldx, ldy;
     int T, I, O, n_q;
-    uint16_t *xb;          // scratch: x as three bf16 planes [3][T][I], then fp32 sums over 64-wide k blocks [T][I/64] (int8 rows, T > 4), or null
+    uint16_t *xb;          // scratch for int8 rows with T > 4 (proj_xb_bytes), or null: x as three bf16 planes [3][T][I], fp32 sums over 64-wide k blocks [T][I/64], k-split partial tiles and arrival counters
+    size_t xb_n;           // bytes at xb (launch_proj refuses a shape whose scratch does not fit)
+    float *part;           // (set by launch_proj from xb)
+    int *cnt;
 };
-// bytes of the x planes and block sums a projection of T tokens over I inputs uses
-inline size_t proj_xb_bytes(int T, int I) { return (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float); }
+// bytes of the scratch a projection of T tokens over I inputs into n_q int8 rows uses
+size_t proj_xb_bytes(int T, int I, int n_q);
 // hidden size I and int8 row count n_q the projection kernels take
 bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
