@@ -614,8 +614,7 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
 // (device-coherent atomic stores and loads, as the sliced decode norm).
 // Operand k order within a 64-wide block: lane (l%16, g) holds
 // k = 16g + 8s + j of step s, j < 8, on both operands.
-constexpr int kWvRows = 64, kWvTok = 64, kWvK = 64;
-constexpr int kWvTileFloats = kWvRows * kWvTok;          // one partial tile
+constexpr int kWvRows = 64, kWvK = 64;
 
 // Rows beside the int8 ones in the same launch: the fp32 rows of the
 // projection (the b / a rows of in_proj), run by kF32Wgs extra workgroups
@@ -628,10 +627,11 @@ struct F32Part {
     int gx, nwg;   // fp32 workgroup grid width and count
 };
 
-template <int G, int WD, bool F32>
+template <int G, int WD, bool F32, int TT>
 __global__ __launch_bounds__(4 * OMH_WAVE, 1)
 void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
-    constexpr int RW = kWvRows / 16, TT = kWvTok / 16;
+    constexpr int RW = kWvRows / 16, NTOK = 16 * TT;          // rows and tokens of a wave's tile
+    constexpr int kTileFloats = kWvRows * NTOK;               // one partial tile
     if constexpr (F32) {
         if ((int)blockIdx.x >= f.nrg) {
             const int i = (blockIdx.x - f.nrg) + (gridDim.x - f.nrg) * blockIdx.y;
@@ -640,27 +640,27 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
         }
     }
     __shared__ v4f s_red[4][RW][TT][OMH_WAVE];
-    __shared__ float s_sx[kWvTok];
+    __shared__ float s_sx[NTOK];
     __shared__ int s_last;
     const int tid = threadIdx.x, lane = tid % OMH_WAVE;
     const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
     const int l16 = lane % 16, gq = lane / 16;
-    const int r0 = blockIdx.x * kWvRows, t0 = blockIdx.y * kWvTok;
+    const int r0 = blockIdx.x * kWvRows, t0 = blockIdx.y * NTOK;
     const int g = blockIdx.z;
     const int k0 = (g * 4 + w) * (nb * kWvK);
     const size_t plane = (size_t)p.T * p.I;
 
     // sum of x per token for the epilogue, from the split kernel's sums of
-    // 64-wide blocks: thread tid takes a quarter of token tid / 4's blocks.
-    // Requested first, summed after the main loop (one load latency for
-    // the whole launch, hidden under it).
-    constexpr int kSxRegs = 16;
-    const int nq = p.I / 64, nq4 = nq / 4;
-    const float *sq = reinterpret_cast<const float *>(p.xb + 3 * plane) + (size_t)min(t0 + tid / 4, p.T - 1) * nq +
-                      (tid % 4) * nq4;
+    // 64-wide blocks: TPT consecutive threads share a token, each taking
+    // 1 / TPT of its blocks.  Requested first, summed after the main loop
+    // (one load latency for the whole launch, hidden under it).
+    constexpr int kSxRegs = 16, TPT = 4 * OMH_WAVE / NTOK;
+    const int nq = p.I / 64, nqt = nq / TPT;
+    const float *sq = reinterpret_cast<const float *>(p.xb + 3 * plane) + (size_t)min(t0 + tid / TPT, p.T - 1) * nq +
+                      (tid % TPT) * nqt;
     float sxr[kSxRegs];
 #pragma unroll
-    for (int j = 0; j < kSxRegs; j++) sxr[j] = sq[min(j, nq4 - 1)];
+    for (int j = 0; j < kSxRegs; j++) sxr[j] = sq[min(j, nqt - 1)];
 
     const int8_t *wp[RW];
     const uint16_t *xp[TT];
@@ -670,17 +670,21 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
     for (int tt = 0; tt < TT; tt++) xp[tt] = p.xb + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * 32 + 8 * gq;
     const size_t chunk = (size_t)p.T * 32;        // one 32-value chunk of every token
 
-    // x one 32-wide step ahead (two steps per block) in two register slots,
-    // the weights WD blocks ahead in WD.  The loop body is WD blocks, one
-    // period of both rings, so every slot index is a compile-time constant;
-    // the loop stays a loop (a fully unrolled body outruns the instruction
-    // cache: every wave would run thousands of instructions exactly once).
-    // The prologue leaves the same loads outstanding, in the same order, as
-    // the end of an iteration (the weights of the next WD - 1 blocks, the
-    // next step's x, the weights of the block after), so the wait counts
-    // agree on both edges into the loop.
+    // x XD - 1 steps ahead (two 32-wide steps per block) in a ring of XD
+    // register slots, the weights WD blocks ahead in a ring of WD.  The loop
+    // body is WD blocks, one period of both rings (XD divides 2 WD), so
+    // every slot index is a compile-time constant; the loop stays a loop (a
+    // fully unrolled body outruns the instruction cache: every wave would
+    // run thousands of instructions exactly once).  Order within the loop:
+    // at the start of step q the x of step q + XD - 1, after block b the
+    // weights of block b + WD.  The prologue issues the loads of the
+    // iteration before the first, in that order (those of negative steps
+    // and blocks left out), so the wait counts agree on both edges into
+    // the loop.
+    constexpr int XD = 2;
+    static_assert((2 * WD) % XD == 0, "ring periods");
     int4 wq[WD][RW];
-    v4u xq[2][TT][3];
+    v4u xq[XD][TT][3];
     auto w_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
         constexpr int sl = decltype(slot_c)::value;
         b = min(b, nb - 1);
@@ -721,29 +725,27 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
                     acc[rw][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         A[rw], __builtin_bit_cast(v8bf, xq[xs][tt][sp]), acc[rw][tt], 0, 0, 0);
     };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    static_for<WD - 1>([&](auto jc) __attribute__((always_inline)) { w_load(decltype(jc)::value, jc); });
-    x_load(0, I0{});
-    w_load(WD - 1, std::integral_constant<int, WD - 1>{});
+    // the loads of one loop iteration's step u (0 <= u < 2 WD) relative to
+    // its first block b0, with step u's products in between when run
+    auto loads_at = [&](int b0, auto uc, auto run) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        const int q = 2 * b0 + u;
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + XD - 1 >= 0) x_load(q + XD - 1, std::integral_constant<int, (u + XD - 1) % XD>{});
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(run)::value)
+            step(std::integral_constant<int, u % XD>{}, std::integral_constant<int, u / 2>{}, std::integral_constant<int, u % 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (u % 2 == 1)
+            if (b0 + u / 2 + WD >= 0) w_load(b0 + u / 2 + WD, std::integral_constant<int, u / 2>{});
+    };
+    // prologue: the previous iteration's loads (b0 = -WD), without products
+    static_for<2 * WD>([&](auto uc) __attribute__((always_inline)) { loads_at(-WD, uc, std::false_type{}); });
 #pragma unroll 1
     for (int b0 = 0; b0 < nb; b0 += WD) {
         // (the scheduler would otherwise sink each prefetch next to its
         // use, where its wait drains everything in flight)
-        static_for<WD>([&](auto jc) __attribute__((always_inline)) {
-            constexpr int j = decltype(jc)::value;
-            const int q = 2 * (b0 + j);
-            __builtin_amdgcn_sched_barrier(0);
-            x_load(q + 1, I1{});
-            __builtin_amdgcn_sched_barrier(0);
-            step(I0{}, jc, I0{});
-            __builtin_amdgcn_sched_barrier(0);
-            x_load(q + 2, I0{});
-            __builtin_amdgcn_sched_barrier(0);
-            step(I1{}, jc, I1{});
-            __builtin_amdgcn_sched_barrier(0);
-            w_load(b0 + j + WD, jc);
-        });
+        static_for<2 * WD>([&](auto uc) __attribute__((always_inline)) { loads_at(b0, uc, std::true_type{}); });
     }
 
     // the workgroup's 4 k-subslices, in wave order; wave w then finishes
@@ -755,11 +757,11 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
     {
         float sx = 0.f;
 #pragma unroll
-        for (int j = 0; j < kSxRegs; j++) sx += j < nq4 ? sxr[j] : 0.f;
-        for (int j = kSxRegs; j < nq4; j++) sx += sq[j];
-        sx += __shfl_xor(sx, 1, OMH_WAVE);
-        sx += __shfl_xor(sx, 2, OMH_WAVE);
-        if (tid % 4 == 0) s_sx[tid / 4] = sx;
+        for (int j = 0; j < kSxRegs; j++) sx += j < nqt ? sxr[j] : 0.f;
+        for (int j = kSxRegs; j < nqt; j++) sx += sq[j];
+#pragma unroll
+        for (int off = 1; off < TPT; off <<= 1) sx += __shfl_xor(sx, off, OMH_WAVE);
+        if (tid % TPT == 0) s_sx[tid / TPT] = sx;
     }
     __syncthreads();
     v4f y[TT];
@@ -769,7 +771,7 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
 
     if constexpr (G > 1) {
         const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
-        float *mine = p.part + (tile * G + g) * kWvTileFloats;
+        float *mine = p.part + (tile * G + g) * kTileFloats;
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             float *d = mine + ((w * TT + tt) * OMH_WAVE + lane) * 4;
@@ -788,7 +790,7 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
         for (int gg = 0; gg < G; gg++)
 #pragma unroll
             for (int tt = 0; tt < TT; tt++) {
-                const float *q = p.part + (tile * G + gg) * kWvTileFloats + ((w * TT + tt) * OMH_WAVE + lane) * 4;
+                const float *q = p.part + (tile * G + gg) * kTileFloats + ((w * TT + tt) * OMH_WAVE + lane) * 4;
 #pragma unroll
                 for (int r = 0; r < 4; r++) pt[gg][tt][r] = __hip_atomic_load(q + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -842,19 +844,58 @@ F32Plan f32_plan(const ProjArgs &p) {
     return f;
 }
 
-// The int8 rows of q; with f32 (the fp32 rows, n_q = 0) also those, in the
-// same launch, when their plan is the one-token-tile shape the wave kernel
-// carries (proj_mfma_wg<1, 1, 8>).  Returns false (nothing launched) for a
-// shape the kernel does not take; *f32_done says whether f32 was launched.
-bool launch_q8_wave(const ProjArgs &p, int G, const ProjArgs *f32, bool *f32_done, hipStream_t st) {
-    constexpr int WD = 2;
-    const int nb = p.I / (4 * kWvK * G);
-    if (nb < WD || nb % WD != 0) return false;
+// Launch plan of the wave-tile kernel for O int8 rows, T tokens, I inputs:
+// tokens per wave 16 * TT, with the largest TT (up to what T needs) that
+// still gives 768 waves
+// (three quarters of the SIMDs); with few rows, TT = 1, and a k split
+// over G workgroups only while that leaves fewer than 256 waves (the split
+// costs a round trip of partial tiles through memory).  TT = 0: the kernel
+// does not take the shape.
+struct WvPlan {
+    int TT, G;
+};
+// weight ring depth (blocks ahead) of the wave kernel (deeper rings for the
+// narrow token tiles measured no faster: their loop is bound by issue, not
+// by load latency)
+constexpr int wv_wd(int) { return 2; }
+WvPlan q8_wave_plan(int O, int T, int I) {
+    WvPlan w{0, 1};
+    if (I % (4 * kWvK * 2) != 0) return w;
+    const long rg = (O + kWvRows - 1) / kWvRows;
+    auto waves = [&](int tt) { return rg * ((T + 16 * tt - 1) / (16 * tt)) * 4; };
+    int tt = T <= 16 ? 1 : (T <= 32 ? 2 : 4);     // no wider than the tokens there are
+    while (tt > 1 && waves(tt) < 768) tt /= 2;
+    // TPT = 16 / tt threads per token share its block sums
+    if ((I / 64) % (16 / tt) != 0) return w;
+    const int wd = wv_wd(tt);                      // blocks per wave: a multiple of wd
+    while (w.G < 8 && waves(tt) * w.G < 256 && I % (4 * kWvK * wd * 2 * w.G) == 0) w.G *= 2;
+    if (I % (4 * kWvK * wd * w.G) != 0) return w;
+    w.TT = tt;
+    return w;
+}
+
+template <int TT>
+void launch_q8_wave_tt(const ProjArgs &p, int G, int nb, const F32Part &f, bool with, dim3 grid, hipStream_t st) {
+    constexpr int WD = wv_wd(TT);
+    const dim3 blk(4 * OMH_WAVE);
+    if (G == 1 && with) hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, true, TT>), grid, blk, 0, st, p, nb, f);
+    else if (G == 1) hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, false, TT>), grid, blk, 0, st, p, nb, f);
+    else if (G == 2) hipLaunchKernelGGL((proj_q8_wave_kernel<2, WD, false, TT>), grid, blk, 0, st, p, nb, f);
+    else if (G == 4) hipLaunchKernelGGL((proj_q8_wave_kernel<4, WD, false, TT>), grid, blk, 0, st, p, nb, f);
+    else hipLaunchKernelGGL((proj_q8_wave_kernel<8, WD, false, TT>), grid, blk, 0, st, p, nb, f);
+}
+
+// The int8 rows of q by plan w; with f32 (the fp32 rows, n_q = 0) also
+// those, in the same launch, when their plan is the one-token-tile shape
+// the wave kernel carries (proj_mfma_wg<1, 1, 8>).  *f32_done says whether
+// f32 was launched.
+void launch_q8_wave(const ProjArgs &p, WvPlan w, const ProjArgs *f32, bool *f32_done, hipStream_t st) {
+    const int nb = p.I / (4 * kWvK * w.G);
     F32Part f{};
     f.nrg = (p.O + kWvRows - 1) / kWvRows;
-    const int ty = (p.T + kWvTok - 1) / kWvTok;
+    const int ty = (p.T + 16 * w.TT - 1) / (16 * w.TT);
     bool with = false;
-    if (f32 && G == 1) {
+    if (f32 && w.G == 1) {
         const F32Plan fp = f32_plan(*f32);
         with = fp.rt == 1 && fp.tpw == 16 && fp.grid.y > 1 && f32->I / 4 / 64 % 8 == 0;
         if (with) {
@@ -865,46 +906,30 @@ bool launch_q8_wave(const ProjArgs &p, int G, const ProjArgs *f32, bool *f32_don
     }
     *f32_done = with;
     const int extra = with ? (f.nwg + ty - 1) / ty : 0;
-    const dim3 grid(f.nrg + extra, ty, G), blk(4 * OMH_WAVE);
-    switch (G) {
-    case 1:
-        if (with) hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, true>), grid, blk, 0, st, p, nb, f);
-        else hipLaunchKernelGGL((proj_q8_wave_kernel<1, WD, false>), grid, blk, 0, st, p, nb, f);
-        return true;
-    case 2: hipLaunchKernelGGL((proj_q8_wave_kernel<2, WD, false>), grid, blk, 0, st, p, nb, f); return true;
-    case 4: hipLaunchKernelGGL((proj_q8_wave_kernel<4, WD, false>), grid, blk, 0, st, p, nb, f); return true;
-    case 8: hipLaunchKernelGGL((proj_q8_wave_kernel<8, WD, false>), grid, blk, 0, st, p, nb, f); return true;
-    default: return false;
-    }
+    const dim3 grid(f.nrg + extra, ty, w.G);
+    if (w.TT == 4) launch_q8_wave_tt<4>(p, w.G, nb, f, with, grid, st);
+    else if (w.TT == 2) launch_q8_wave_tt<2>(p, w.G, nb, f, with, grid, st);
+    else launch_q8_wave_tt<1>(p, w.G, nb, f, with, grid, st);
 }
 
 inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
-// k split of the wave-tile kernel: 1, or doubled while the launch has fewer
-// than 768 waves (three quarters of the SIMDs) and each wave keeps at least
-// 4 blocks of k; 0 if the kernel does not take the shape
-int q8_wave_split(int O, int T, int I) {
-    if (I % (4 * kWvK) != 0) return 0;
-    const long tiles = (long)((O + kWvRows - 1) / kWvRows) * ((T + kWvTok - 1) / kWvTok);
-    int G = 1;
-    while (G < 8 && tiles * 4 * G < 768 && I % (4 * kWvK * 2 * G) == 0 && I / (4 * kWvK * 2 * G) >= 4) G *= 2;
-    const int nb = I / (4 * kWvK * G);
-    return nb >= 2 && nb % 2 == 0 ? G : 0;
-}
-
 struct XbLayout {
     size_t part, cnt, total;   // byte offsets of the partial tiles and counters, total bytes
-    int G, ncnt;
+    WvPlan w;
+    int ncnt;
 };
 XbLayout xb_layout(int T, int I, int n_q) {
     XbLayout l{};
     const size_t planes = (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float);
-    l.G = n_q > 0 ? q8_wave_split(n_q, T, I) : 0;
-    const size_t tiles = (size_t)((n_q + kWvRows - 1) / kWvRows) * ((T + kWvTok - 1) / kWvTok);
+    l.w = n_q > 0 ? q8_wave_plan(n_q, T, I) : WvPlan{0, 1};
+    const int ntok = 16 * (l.w.TT > 0 ? l.w.TT : 1);
+    const size_t tiles = (size_t)((n_q + kWvRows - 1) / kWvRows) * ((T + ntok - 1) / ntok);
     l.part = (planes + 255) / 256 * 256;
-    const size_t npart = l.G > 1 ? tiles * l.G * kWvTileFloats * sizeof(float) : 0;
+    const bool split = l.w.TT > 0 && l.w.G > 1;
+    const size_t npart = split ? tiles * l.w.G * kWvRows * ntok * sizeof(float) : 0;
     l.cnt = l.part + npart;
-    l.ncnt = l.G > 1 ? (int)tiles : 0;
+    l.ncnt = split ? (int)tiles : 0;
     l.total = l.cnt + (size_t)l.ncnt * sizeof(int);
     return l;
 }
@@ -974,7 +999,8 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         f.Q = nullptr;
         f.scale = nullptr;
         bool f32_done = false;
-        const bool done = lay.G > 0 && launch_q8_wave(q, lay.G, p.O > p.n_q ? &f : nullptr, &f32_done, st);
+        const bool done = lay.w.TT > 0;
+        if (done) launch_q8_wave(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
         if (!done) {
             // enough workgroups for the device (a k split where rows are few)
             const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;
