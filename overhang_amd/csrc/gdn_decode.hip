@@ -240,12 +240,48 @@ __device__ __forceinline__ void load_head(float4 (&s)[RPT], const float *Sp, int
     for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream(Sp + (size_t)(rg + Sh::RG * m) * VD + c4 * 4);
 }
 
+// Where the core output also goes, when the decode step feeds an int8
+// out_proj: the projection scratch's bf16 planes and block sums (xpiece
+// layout, T tokens of I = vh * vd inputs).  null xb: not written.
+struct PlaneOut {
+    uint16_t *xb;
+    int T, I;
+};
+
+// Columns col .. col+3 (= 4 * c4 of a head starting at a multiple of 64) of
+// token tok's output y, split exactly into three bf16 terms (hi = bf16(y),
+// mid = bf16(y - hi), lo = the rest), and the sums of its 64-wide column
+// blocks: a block is 16 lanes with consecutive c4, all active here.
+__device__ __forceinline__ void write_planes(const PlaneOut &po, int tok, int col, int c4, float4 y) {
+    typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+    const float v[4] = {y.x, y.y, y.z, y.w};
+    v4bf hi, mid, lo;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        hi[j] = (__bf16)v[j];
+        const float r1 = v[j] - (float)hi[j];
+        mid[j] = (__bf16)r1;
+        lo[j] = (__bf16)(r1 - (float)mid[j]);
+    }
+    const size_t plane = (size_t)po.T * po.I, o = xpiece(col / 8, tok, po.T) + col % 8;
+    *reinterpret_cast<v4bf *>(po.xb + o) = hi;
+    *reinterpret_cast<v4bf *>(po.xb + plane + o) = mid;
+    *reinterpret_cast<v4bf *>(po.xb + 2 * plane + o) = lo;
+    float sm = (y.x + y.y) + (y.z + y.w);
+    sm += __shfl_xor(sm, 1, OMH_WAVE);
+    sm += __shfl_xor(sm, 2, OMH_WAVE);
+    sm += __shfl_xor(sm, 4, OMH_WAVE);
+    sm += __shfl_xor(sm, 8, OMH_WAVE);
+    if (c4 % 16 == 0) reinterpret_cast<float *>(po.xb + 3 * plane)[(size_t)tok * (po.I / 64) + col / 64] = sm;
+}
+
 // Delta rule + gated norm of one value head of the workgroup.
 template <int KD, int VD, int RPT, int C4>
 __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *core, const float *s_q,
                                             const float *s_k, const float *s_v, const float *s_z,
                                             const HeadCoef &hc, float4 gn, float eps, float4 (*red)[2][C4],
-                                            int wave, int lane, int c4, int rg) {
+                                            int wave, int lane, int c4, int rg, const PlaneOut &po, int tok,
+                                            int col0) {
     using Sh = PairShape<KD, VD>;
     static_assert(RPT == Sh::RPT && C4 == Sh::C4, "tile shape");
     const float4 vv = *reinterpret_cast<const float4 *>(&s_v[c4 * 4]);
@@ -255,7 +291,10 @@ __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *
     if (rg == 0) {
         const float rn = 1.f / sqrtf(ss / (float)VD + eps);     // qwen.c:353-357
         const float4 zz = *reinterpret_cast<const float4 *>(&s_z[c4 * 4]);
-        *reinterpret_cast<float4 *>(core + c4 * 4) = gated(o, rn, gn, zz);
+        const float4 y = gated(o, rn, gn, zz);
+        *reinterpret_cast<float4 *>(core + c4 * 4) = y;
+        if constexpr (VD % 64 == 0)
+            if (po.xb) write_planes(po, tok, col0 + c4 * 4, c4, y);
     }
 }
 
@@ -357,18 +396,19 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     // the two reduction buffers, so a wave that runs ahead into the next
     // head never overwrites sums another wave is still reading.
     float *core = args.core + tok * vdim + (size_t)h0 * VD;
+    const PlaneOut po{args.xb, args.B, vdim};
     for (int j = 0; j < rep; j += 2) {
         hc.gam = s_gam[j];
         hc.beta = s_beta[j];
         paired_head<KD, VD>(sa, S0 + (size_t)j * KD * VD, core + j * VD, s_q, s_k, s_v + j * VD, s_z + j * VD, hc,
-                            gn, args.eps, s_red[0], wave, lane, c4, rg);
+                            gn, args.eps, s_red[0], wave, lane, c4, rg, po, (int)tok, (h0 + j) * VD);
         if (j + 2 < rep) load_head<KD, VD>(sa, S0 + (size_t)(j + 2) * KD * VD, rg, c4);
         if (REPMAX > 1 && j + 1 < rep) {
             hc.gam = s_gam[j + 1];
             hc.beta = s_beta[j + 1];
             paired_head<KD, VD>(sb, S0 + (size_t)(j + 1) * KD * VD, core + (j + 1) * VD, s_q, s_k,
                                 s_v + (j + 1) * VD, s_z + (j + 1) * VD, hc, gn, args.eps, s_red[1], wave, lane,
-                                c4, rg);
+                                c4, rg, po, (int)tok, (h0 + j + 1) * VD);
             if (j + 3 < rep) load_head<KD, VD>(sb, S0 + (size_t)(j + 3) * KD * VD, rg, c4);
         }
     }
@@ -465,7 +505,10 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     if constexpr (NCS == 1) {
         if (rg == 0) {
             const float rn = 1.f / sqrtf(ss / (float)VD + args.eps);
-            *reinterpret_cast<float4 *>(core + c4 * 4) = gated(o, rn, gn, zz);
+            const float4 y = gated(o, rn, gn, zz);
+            *reinterpret_cast<float4 *>(core + c4 * 4) = y;
+            if constexpr (VD % 64 == 0)
+                if (args.xb) write_planes(PlaneOut{args.xb, args.B, vdim}, (int)tok, h * VD + c4 * 4, c4, y);
         }
     } else {
         // Cross-slice exchange with device-coherent (agent-scope) relaxed
@@ -558,8 +601,14 @@ bool decode_core_supported(int kd, int vd, int rep, int K) {
     return (kd == vd && (kd == 16 || kd == 32 || kd == 64 || kd == 128)) || (kd == 32 && vd == 16);
 }
 
+bool decode_planes_supported(int vd, int variant) {
+    return vd % 64 == 0 && (variant == 0 || variant == kDecodePaired || variant == 1);
+}
+
 hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, hipStream_t st) {
     if (!decode_core_supported(kd, vd, a.vh / a.kh, a.K)) return hipErrorInvalidValue;
+    if (a.rep != a.vh / a.kh) return hipErrorInvalidValue;
+    if (a.xb && (a.nl != 1 || !decode_planes_supported(vd, variant))) return hipErrorInvalidValue;
     if (variant == 0) variant = choose_variant(a, kd, vd);
     if (variant == kDecodePaired && a.vh / a.kh > kMaxRep) return hipErrorInvalidValue;
     if (kd == 16 && vd == 16) return launch_kd_vd<16, 16>(a, variant, st);

@@ -339,18 +339,7 @@ constexpr int kQ8Rows = 32;                 // rows per wave
 constexpr int kQ8K = 64;                    // k per staged block
 constexpr int kQ8Tok = 32;                  // tokens per workgroup
 
-// Layout of the x planes: per plane, 32-value chunks [2 * (I / 64)][T][32]
-// (bf16).  Chunk 2c + s of token t holds, at position 8g + j, the value at
-// k = 64c + 16g + 8s + j (g < 4, j < 8): exactly what lane group g of a
-// 16-token MFMA operand reads in step s of 64-wide k block c (the k order
-// both operands share).  So 16 tokens' operand for one step is one
-// contiguous 1 KiB run, and every 16-byte piece of 8 consecutive k is
-// contiguous.  Offset of the piece holding k = 8m .. 8m+7 of token t:
-__device__ __forceinline__ size_t xpiece(int m, int t, int T) {
-    return ((size_t)(2 * (m / 8) + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
-}
-
-// planes[p] = term p of x in the chunk layout above, and the sum of x[t][k]
+// planes[p] = term p of x in the chunk layout (xpiece), and the sum of x[t][k]
 // over each 64-wide k block (sums[t][k / 64], after the planes); 8 values
 // per thread
 // (block 0 also clears the k-split arrival counters of the launch after it)
@@ -989,9 +978,12 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         q.O = p.n_q;
         q.part = reinterpret_cast<float *>(reinterpret_cast<char *>(p.xb) + lay.part);
         q.cnt = reinterpret_cast<int *>(reinterpret_cast<char *>(p.xb) + lay.cnt);
-        const size_t n8 = (size_t)p.T * (p.I / 8);
-        hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb, p.T,
-                           p.I, q.cnt, lay.ncnt);
+        // (planes written by the decode core: no split, unless counters need clearing)
+        if (!p.x_split || lay.ncnt > 0) {
+            const size_t n8 = (size_t)p.T * (p.I / 8);
+            hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb,
+                               p.T, p.I, q.cnt, lay.ncnt);
+        }
         ProjArgs f = p;
         f.y = p.y + p.n_q;
         f.O = p.O - p.n_q;

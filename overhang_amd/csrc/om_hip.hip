@@ -131,9 +131,11 @@ int decode_variant() {
 }
 
 // Core decode on device pointers for layers lis[0..nl), B sequences each.
+// planes: or null; with one layer, where the core output also goes as the
+// out_proj scratch's bf16 planes and block sums (DecodeArgs::xb)
 int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv, const float *z,
                 int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
-                hipStream_t st) {
+                hipStream_t st, uint16_t *planes = nullptr) {
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
     for (int i = 0; i < nl; i++) {
         if (int rc = check_layer(lis[i])) return rc;
@@ -169,6 +171,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
         A.core = core + t0 * vdim;
         A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
         A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.rep = d.vh / d.kh; A.K = d.conv_k; A.eps = d.eps;
+        A.xb = nl == 1 ? planes : nullptr;
         for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
         HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_variant(), st));
         for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
@@ -198,9 +201,11 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
-    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
+    // the core writes out_proj's bf16 planes itself, saving the split launch
+    uint16_t *planes = xb && L.out_nq > 0 && decode_planes_supported(L.d.vd, decode_variant()) ? xb : nullptr;
+    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0; q.x_split = planes != nullptr;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;

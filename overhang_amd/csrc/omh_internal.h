@@ -66,8 +66,22 @@ struct DecodeArgs {
     int B, nl, kh, vh, K;
     float eps;
     int rep;            // vh / kh
+    uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's bf16 planes and block sums (T = B, I = vh*vd; xpiece)
     LayerPtrs L[kMaxDecodeLayers];
 };
+
+// Layout of the bf16 planes of x (the int8 projections' scratch, x as
+// hi + mid + lo): per plane, 32-value chunks [2 * (I / 64)][T][32].  Chunk
+// 2c + s of token t holds, at position 8g + j, the value at
+// k = 64c + 16g + 8s + j (g < 4, j < 8): exactly what lane group g of a
+// 16-token MFMA operand reads in step s of 64-wide k block c (the k order
+// both operands share).  So 16 tokens' operand for one step is one
+// contiguous 1 KiB run, and every 16-byte piece of 8 consecutive k is
+// contiguous.  Element offset of the piece holding k = 8m .. 8m+7 of
+// token t (planes of T * I elements each, then fp32 sums [T][I / 64]):
+__host__ __device__ inline size_t xpiece(int m, int t, int T) {
+    return ((size_t)(2 * (m / 8) + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
+}
 
 // y[t][o] = sum_i x[t][i] * W[o][i] for t < T, o < O.  Rows o < n_q come
 // from the int8 matrix Q (times scale[o]); rows o >= n_q from the fp32
@@ -82,6 +96,7 @@ struct ProjArgs {
     int T, I, O, n_q;
     uint16_t *xb;          // scratch for int8 rows with T > 4 (proj_xb_bytes), or null: x as three bf16 planes [3][T][I], fp32 sums over 64-wide k blocks [T][I/64], k-split partial tiles and arrival counters
     size_t xb_n;           // bytes at xb (launch_proj refuses a shape whose scratch does not fit)
+    bool x_split;          // the planes and block sums of x are already in xb (written by the decode core)
     float *part;           // (set by launch_proj from xb)
     int *cnt;
 };
@@ -123,5 +138,7 @@ hipError_t launch_prefill_core(const PrefillArgs &a, int D, hipStream_t st);
 constexpr int kDecodePaired = -1;
 hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int variant, hipStream_t st);
 bool decode_core_supported(int kd, int vd, int rep, int K);
+// whether a launch with this variant request can also write the out_proj planes (DecodeArgs::xb)
+bool decode_planes_supported(int vd, int variant);
 
 }  // namespace omh

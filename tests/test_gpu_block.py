@@ -89,6 +89,36 @@ def test_35b_int8_block_batch64():
     L.free()
 
 
+@pytest.mark.parametrize("shape,B", [
+    ((2, 4, 64, 64, 512), 5),        # sliced core kernel; out_proj on the staged bf16 x 3 kernel
+    ((2, 4, 64, 64, 512), 40),
+    ((4, 8, 128, 128, 1024), 64),    # paired core kernel; out_proj wave tiles of 16 tokens
+    ((16, 32, 128, 128, 2048), 8),   # the 35B shape, sliced core; out_proj with a k split
+], ids=["d64-B5", "d64-B40", "d128-B64", "35b-B8"])
+def test_int8_block_core_writes_out_proj_planes(shape, B):
+    """int8 blocks whose decode core also writes out_proj's bf16 planes and
+    block sums (so the projection skips its split launch): two steps, three
+    sequences against the per-token oracle."""
+    from overhang_amd.dims import GdnDims
+    kh, vh, kd, vd, hidden = shape
+    d = GdnDims(kh=kh, vh=vh, kd=kd, vd=vd, K=4, hidden=hidden)
+    seed = 9700 + B + kd
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    T = 2
+    x = _x(d, seed, (T, B))
+    got = np.stack([L.decode(x[t]) for t in range(T)], axis=1)       # [B][T][D]
+    for s in sorted({0, B // 2, B - 1}):
+        ref, cref, Sref = oracle.layer_seq(d, w, x[:, s], conv0[s], S0[s], int8=True)
+        conv, S = L.get_state(s)
+        assert_close(got[s], ref, what=f"{shape} B={B} seq {s} out")
+        assert_close(S, Sref, what=f"{shape} B={B} seq {s} S")
+    L.free()
+
+
 def test_projection_shape_limits_are_reported():
     from overhang_amd.dims import GdnDims
     d = GdnDims(kh=2, vh=4, kd=16, vd=16, K=4, hidden=96)       # hidden not a multiple of 64
