@@ -185,13 +185,14 @@ __device__ __forceinline__ void qk_factors(const float *s_q, const float *s_k, i
 }
 
 // Phase bookkeeping of the ring, per sequence: launch reads phase[epoch],
-// writes phase[1 - epoch]; sequences outside the launch carry theirs over.
-__device__ __forceinline__ void advance_phase(const LayerPtrs &L, int B, int b, bool writer, bool copier,
+// writes phase[1 - epoch]; sequences outside the launch (outside
+// [b0, b0 + B)) carry theirs over.
+__device__ __forceinline__ void advance_phase(const LayerPtrs &L, int b0, int B, int seq, bool writer, bool copier,
                                               int ph, int tid, int tpb) {
-    if (writer && tid == 0) L.phase[(1 - L.epoch) * L.max_seqs + b] = (ph + 1) & (kConvRing - 1);
+    if (writer && tid == 0) L.phase[(1 - L.epoch) * L.max_seqs + seq] = (ph + 1) & (kConvRing - 1);
     if (copier)
-        for (int bb = B + tid; bb < L.max_seqs; bb += tpb)
-            L.phase[(1 - L.epoch) * L.max_seqs + bb] = L.phase[L.epoch * L.max_seqs + bb];
+        for (int bb = tid; bb < L.max_seqs; bb += tpb)
+            if (bb < b0 || bb >= b0 + B) L.phase[(1 - L.epoch) * L.max_seqs + bb] = L.phase[L.epoch * L.max_seqs + bb];
 }
 
 // Per-head scalars of the delta rule.
@@ -307,7 +308,8 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     constexpr int NZ = (REPMAX * VD + TPB - 1) / TPB;             // z values per thread
 
     const int hk = blockIdx.x;                   // key head
-    const int b = blockIdx.y;                    // sequence
+    const int b = blockIdx.y;                    // token row of the launch
+    const int seq = args.b0 + b;                 // sequence (state slot)
     const int l = blockIdx.z;                    // layer slot
     const LayerPtrs &L = args.L[l];
     // rep comes precomputed with the head counts: the state address then
@@ -324,7 +326,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     const int tid = threadIdx.x;
     const int c4 = tid % C4, rg = tid / C4;
     const int lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
-    float *S0 = Sl + ((size_t)b * vh + h0) * (KD * VD);
+    float *S0 = Sl + ((size_t)seq * vh + h0) * (KD * VD);
 
     __shared__ __align__(16) float s_q[KD], s_k[KD], s_v[REPMAX * VD], s_z[REPMAX * VD];
     __shared__ float s_gam[REPMAX], s_beta[REPMAX];
@@ -345,7 +347,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     // (1) Prologue: the conv channels of key head hk (q, k) and of its
     // value heads (v), z of the value heads, the gate inputs.  This
     // workgroup owns all of these channels and appends them to the ring.
-    const int ph = L.phase[L.epoch * L.max_seqs + b];
+    const int ph = L.phase[L.epoch * L.max_seqs + seq];
     const float *qkv = args.qkv + tok * args.ld_qkv;
     const int nch = 2 * KD + rep * VD;
     ConvIn<NIT> cin;
@@ -353,7 +355,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
                  return c < KD ? hk * KD + c
                                : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h0 * VD + (c - 2 * KD));
              },
-             nch, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b, ph, K);
+             nch, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, seq, ph, K);
     const float *zrow = args.z + tok * args.ld_z + (size_t)h0 * VD;
     float zin[NZ];
 #pragma unroll
@@ -374,7 +376,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
         if (c < KD) s_q[c] = y;
         else if (c < 2 * KD) s_k[c - KD] = y;
         else s_v[c - 2 * KD] = y;
-        cin.append(it, L.conv_st, conv_dim, b, ph);
+        cin.append(it, L.conv_st, conv_dim, seq, ph);
     }
 #pragma unroll
     for (int it = 0; it < NZ; it++) {
@@ -396,23 +398,23 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     // the two reduction buffers, so a wave that runs ahead into the next
     // head never overwrites sums another wave is still reading.
     float *core = args.core + tok * vdim + (size_t)h0 * VD;
-    const PlaneOut po{args.xb, args.B, vdim};
+    const PlaneOut po{args.xb, args.xb_T, vdim};
     for (int j = 0; j < rep; j += 2) {
         hc.gam = s_gam[j];
         hc.beta = s_beta[j];
         paired_head<KD, VD>(sa, S0 + (size_t)j * KD * VD, core + j * VD, s_q, s_k, s_v + j * VD, s_z + j * VD, hc,
-                            gn, args.eps, s_red[0], wave, lane, c4, rg, po, (int)tok, (h0 + j) * VD);
+                            gn, args.eps, s_red[0], wave, lane, c4, rg, po, args.xb_t0 + b, (h0 + j) * VD);
         if (j + 2 < rep) load_head<KD, VD>(sa, S0 + (size_t)(j + 2) * KD * VD, rg, c4);
         if (REPMAX > 1 && j + 1 < rep) {
             hc.gam = s_gam[j + 1];
             hc.beta = s_beta[j + 1];
             paired_head<KD, VD>(sb, S0 + (size_t)(j + 1) * KD * VD, core + (j + 1) * VD, s_q, s_k,
                                 s_v + (j + 1) * VD, s_z + (j + 1) * VD, hc, gn, args.eps, s_red[1], wave, lane,
-                                c4, rg, po, (int)tok, (h0 + j + 1) * VD);
+                                c4, rg, po, args.xb_t0 + b, (h0 + j + 1) * VD);
             if (j + 3 < rep) load_head<KD, VD>(sb, S0 + (size_t)(j + 3) * KD * VD, rg, c4);
         }
     }
-    advance_phase(L, args.B, b, hk == 0, hk == 0 && b == 0, ph, tid, TPB);
+    advance_phase(L, args.b0, args.B, seq, hk == 0, hk == 0 && b == 0, ph, tid, TPB);
 }
 
 // ------------------------------------------------------------- sliced kernel
@@ -425,7 +427,8 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
 
     const int cs = blockIdx.x % NCS;             // column slice
     const int h = blockIdx.x / NCS;              // value head
-    const int b = blockIdx.y;                    // sequence
+    const int b = blockIdx.y;                    // token row of the launch
+    const int seq = args.b0 + b;                 // sequence (state slot)
     const int l = blockIdx.z;                    // layer slot
     const LayerPtrs &L = args.L[l];
     float *const Sl = L.S;
@@ -439,7 +442,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     const int tid = threadIdx.x;
     const int c4 = tid % C4, rg = tid / C4;
     const int lane = tid % OMH_WAVE, wave = tid / OMH_WAVE;
-    float *Sp = Sl + ((size_t)b * vh + h) * (KD * VD) + col0;
+    float *Sp = Sl + ((size_t)seq * vh + h) * (KD * VD) + col0;
 
     __shared__ __align__(16) float s_q[KD], s_k[KD], s_v[CW];
     __shared__ float s_gam, s_beta;
@@ -450,14 +453,14 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     // hk (recomputed by every workgroup of the key head, appended by its
     // first one) and this slice's value channels.
     constexpr int NIT = (2 * KD + CW + TPB - 1) / TPB;
-    const int ph = L.phase[L.epoch * L.max_seqs + b];
+    const int ph = L.phase[L.epoch * L.max_seqs + seq];
     const float *qkv = args.qkv + tok * args.ld_qkv;
     ConvIn<NIT> cin;
     cin.load([&](int c) {
                  return c < KD ? hk * KD + c
                                : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h * VD + col0 + (c - 2 * KD));
              },
-             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, b, ph, K);
+             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, seq, ph, K);
     const int t4 = tid < VD / 4 ? tid : 0;
     const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + t4 * 4);
     const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + t4 * 4);
@@ -479,7 +482,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
         if (c < KD) { s_q[c] = y; own = own_qk; }
         else if (c < 2 * KD) { s_k[c - KD] = y; own = own_qk; }
         else s_v[c - 2 * KD] = y;
-        if (own) cin.append(it, L.conv_st, conv_dim, b, ph);
+        if (own) cin.append(it, L.conv_st, conv_dim, seq, ph);
     }
     if (tid == 0) {
         // gates (qwen.c:337-338)
@@ -496,7 +499,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     // (3) delta rule on this slice of value head h (qwen.c:339-352)
     const float4 vv = *reinterpret_cast<const float4 *>(&s_v[c4 * 4]);
     const float4 o = delta_rule<KD, VD, RG, RPT, C4, NW>(s, Sp, s_q, s_k, vv, hc, s_red, wave, lane, c4, rg);
-    advance_phase(L, args.B, b, h == 0 && cs == 0, h == 0 && cs == 0 && b == 0, ph, tid, TPB);
+    advance_phase(L, args.b0, args.B, seq, h == 0 && cs == 0, h == 0 && cs == 0 && b == 0, ph, tid, TPB);
 
     // (4) gated RMSNorm over the head's vd columns (qwen.c:353-357)
     float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
@@ -508,7 +511,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
             const float4 y = gated(o, rn, gn, zz);
             *reinterpret_cast<float4 *>(core + c4 * 4) = y;
             if constexpr (VD % 64 == 0)
-                if (args.xb) write_planes(PlaneOut{args.xb, args.B, vdim}, (int)tok, h * VD + c4 * 4, c4, y);
+                if (args.xb) write_planes(PlaneOut{args.xb, args.xb_T, vdim}, args.xb_t0 + b, h * VD + c4 * 4, c4, y);
         }
     } else {
         // Cross-slice exchange with device-coherent (agent-scope) relaxed
@@ -516,7 +519,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
         // needed (an agent-scope fence would write back the whole L2).  Each
         // thread waits for its own stores to complete before the workgroup
         // barrier, and only then is the arrival counted.
-        const size_t hb = (size_t)b * vh + h;
+        const size_t hb = (size_t)seq * vh + h;
         if (rg == 0) {
             float *dst = L.o_raw + hb * VD + col0 + c4 * 4;
             __hip_atomic_store(dst + 0, o.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -599,6 +602,24 @@ int choose_variant(const DecodeArgs &a, int kd, int vd) {
 bool decode_core_supported(int kd, int vd, int rep, int K) {
     if (rep < 1 || K < 2 || K > kConvRing) return false;
     return (kd == vd && (kd == 16 || kd == 32 || kd == 64 || kd == 128)) || (kd == 32 && vd == 16);
+}
+
+// Resident workgroups of the paired kernel per round: two per CU (its
+// registers allow two waves per SIMD), 256 CUs.
+constexpr long kPairedRound = 512;
+
+int decode_seqs_per_launch(int kd, int vd, int kh, int vh, int nl, int B, int variant) {
+    if (nl != 1 || kh < 1) return B;
+    DecodeArgs probe{};
+    probe.nl = nl;
+    probe.B = B;
+    probe.kh = kh;
+    probe.vh = vh;
+    if ((variant == 0 ? choose_variant(probe, kd, vd) : variant) != kDecodePaired) return B;
+    const long wgs = (long)kh * B;
+    if (wgs <= kPairedRound) return B;
+    const int chunks = (int)((wgs + kPairedRound - 1) / kPairedRound);
+    return (B + chunks - 1) / chunks;
 }
 
 bool decode_planes_supported(int vd, int variant) {

@@ -135,7 +135,7 @@ int decode_variant() {
 // out_proj scratch's bf16 planes and block sums (DecodeArgs::xb)
 int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv, const float *z,
                 int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
-                hipStream_t st, uint16_t *planes = nullptr) {
+                hipStream_t st, uint16_t *planes = nullptr, int b0 = 0) {
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
     for (int i = 0; i < nl; i++) {
         if (int rc = check_layer(lis[i])) return rc;
@@ -150,8 +150,8 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
             return fail(OMH_ERR_ARG, "decode_core: layers %d and %d differ in shape", lis[0], lis[i]);
     }
     for (int i = 0; i < nl; i++)
-        if (B < 1 || B > g_L[lis[i]].max_seqs)
-            return fail(OMH_ERR_ARG, "decode_core: B=%d outside [1, %d] for layer %d", B,
+        if (B < 1 || b0 < 0 || b0 + B > g_L[lis[i]].max_seqs)
+            return fail(OMH_ERR_ARG, "decode_core: sequences %d..%d outside [0, %d) for layer %d", b0, b0 + B - 1,
                         g_L[lis[i]].max_seqs, lis[i]);
     if (!decode_core_supported(d.kd, d.vd, d.vh / d.kh, d.conv_k))
         return fail(OMH_ERR_SHAPE, "decode_core: kd=%d vd=%d rep=%d K=%d unsupported", d.kd, d.vd,
@@ -160,21 +160,32 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
     if (!aligned16(z) || !aligned16(core) || (ld_z % 4) != 0)
         return fail(OMH_ERR_ARG, "decode_core: z/core must be 16-byte aligned rows");
     const int vdim = L0.vdim;
+    const int variant = decode_variant();
+    // one layer's large batch as launches that each fit one round of
+    // resident workgroups (one B = 64 launch at the 35B shape: 52.1 us;
+    // two B = 32 launches: 2 x 23.7 us)
+    const int Bc = decode_seqs_per_launch(d.kd, d.vd, d.kh, d.vh, nl, B, variant);
     for (int l0 = 0; l0 < nl; l0 += kMaxDecodeLayers) {
         const int n = nl - l0 < kMaxDecodeLayers ? nl - l0 : kMaxDecodeLayers;
-        DecodeArgs A{};
-        const size_t t0 = (size_t)l0 * B;
-        A.qkv = qkv + t0 * ld_qkv;
-        A.z = z + t0 * ld_z;
-        A.a = a + t0 * ld_ab;
-        A.b = b + t0 * ld_ab;
-        A.core = core + t0 * vdim;
-        A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
-        A.B = B; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.rep = d.vh / d.kh; A.K = d.conv_k; A.eps = d.eps;
-        A.xb = nl == 1 ? planes : nullptr;
-        for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
-        HIP_OK(launch_decode_core(A, d.kd, d.vd, decode_variant(), st));
-        for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
+        for (int c0 = 0; c0 < B; c0 += Bc) {
+            const int len = B - c0 < Bc ? B - c0 : Bc;
+            DecodeArgs A{};
+            const size_t t0 = (size_t)l0 * B + c0;     // (Bc < B only with one layer)
+            A.qkv = qkv + t0 * ld_qkv;
+            A.z = z + t0 * ld_z;
+            A.a = a + t0 * ld_ab;
+            A.b = b + t0 * ld_ab;
+            A.core = core + t0 * vdim;
+            A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
+            A.B = len; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.rep = d.vh / d.kh; A.K = d.conv_k; A.eps = d.eps;
+            A.xb = nl == 1 ? planes : nullptr;
+            A.xb_T = B;
+            A.xb_t0 = c0;
+            A.b0 = b0 + c0;
+            for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
+            HIP_OK(launch_decode_core(A, d.kd, d.vd, variant, st));
+            for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
+        }
     }
     return OMH_OK;
 }

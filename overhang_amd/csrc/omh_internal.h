@@ -52,7 +52,7 @@ struct LayerPtrs {
 };
 constexpr int kMaxSlices = 8;
 
-// Decode-core launch: nl layers x B sequences, one token each.
+// Decode-core launch: nl layers x B sequences (b0 .. b0+B-1), one token each.
 constexpr int kMaxDecodeLayers = 32;
 // Token t = l*B + b reads qkv + t*ld_qkv, z + t*ld_z, a + t*ld_ab, b + t*ld_ab
 // and writes core + t*vh*vd.
@@ -66,7 +66,9 @@ struct DecodeArgs {
     int B, nl, kh, vh, K;
     float eps;
     int rep;            // vh / kh
-    uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's bf16 planes and block sums (T = B, I = vh*vd; xpiece)
+    int b0;             // token row b is sequence (state slot) b0 + b
+    uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's bf16 planes and block sums (xpiece; I = vh*vd)
+    int xb_T, xb_t0;    // the planes' token count, and the planes' token of row 0 of this launch
     LayerPtrs L[kMaxDecodeLayers];
 };
 
@@ -140,5 +142,7 @@ hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int varian
 bool decode_core_supported(int kd, int vd, int rep, int K);
 // whether a launch with this variant request can also write the out_proj planes (DecodeArgs::xb)
 bool decode_planes_supported(int vd, int variant);
+// sequences per launch for one layer's B sequences: B, or chunks that each fit one round of resident workgroups
+int decode_seqs_per_launch(int kd, int vd, int kh, int vh, int nl, int B, int variant);
 
 }  // namespace omh

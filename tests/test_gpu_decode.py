@@ -87,6 +87,38 @@ def test_decode_core_35b_shape_batched_vs_oracle(variant):
     L.free()
 
 
+def test_decode_core_35b_large_batches_run_as_chunks():
+    """At the 35B shape a call with more than 32 sequences runs as several
+    launches (each one round of resident workgroups), with the ring phases
+    carried across them: batch sizes 48, 40, 48, 33 over four steps, every
+    sequence checked against its own oracle run."""
+    d = Q35B
+    w = synth.layer_weights(d, 33, gnorm_std=0.1, projections=False)
+    nmax = 48
+    conv0, S0 = synth.states(d, 33, B=nmax)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=nmax)
+    for s in range(nmax):
+        L.set_state(s, conv0[s], S0[s])
+    plan = [48, 40, 48, 33]
+    inp = synth.core_inputs(d, len(plan), 34, B=nmax)
+    fed = {s: [] for s in range(nmax)}
+    outs = {s: [] for s in range(nmax)}
+    for t, B in enumerate(plan):
+        core = L.decode_core(inp["qkv"][:B, t], inp["z"][:B, t], inp["a"][:B, t], inp["b"][:B, t])
+        for s in range(B):
+            fed[s].append(t)
+            outs[s].append(core[s])
+    for s in (0, 23, 24, 32, 33, 39, 40, 47):
+        ts = fed[s]
+        ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"][s, ts], inp["z"][s, ts], inp["a"][s, ts],
+                                          inp["b"][s, ts], conv0[s], S0[s])
+        conv, S = L.get_state(s)
+        assert_close(np.stack(outs[s]), ref, what=f"seq {s}")
+        assert_close(S, Sref, what=f"seq {s} S")
+        assert np.array_equal(conv, cref), f"seq {s} conv history"
+    L.free()
+
+
 def test_multi_layer_dev_call_equals_per_layer_calls(variant):
     from overhang_amd import hip
     d = CFG1
