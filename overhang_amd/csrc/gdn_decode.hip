@@ -264,7 +264,7 @@ __device__ __forceinline__ void write_planes(const PlaneOut &po, int tok, int co
         mid[j] = (__bf16)r1;
         lo[j] = (__bf16)(r1 - (float)mid[j]);
     }
-    const size_t plane = (size_t)po.T * po.I, o = xpiece(col / 8, tok, po.T) + col % 8;
+    const size_t plane = (size_t)po.T * po.I, o = xpiece(col / 8, tok, po.T, po.I) + col % 8;
     *reinterpret_cast<v4bf *>(po.xb + o) = hi;
     *reinterpret_cast<v4bf *>(po.xb + plane + o) = mid;
     *reinterpret_cast<v4bf *>(po.xb + 2 * plane + o) = lo;

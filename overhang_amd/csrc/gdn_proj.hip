@@ -371,7 +371,7 @@ void proj_split_x_kernel(const float *__restrict__ x, int64_t ldx, uint16_t *__r
     sum += __shfl_xor(sum, 2, OMH_WAVE);
     sum += __shfl_xor(sum, 4, OMH_WAVE);
     if (!live) return;
-    const size_t plane = (size_t)T * I, o = xpiece(k / 8, t, T);
+    const size_t plane = (size_t)T * I, o = xpiece(k / 8, t, T, I);
     *reinterpret_cast<v8bf *>(xb + o) = hi;
     *reinterpret_cast<v8bf *>(xb + plane + o) = mid;
     *reinterpret_cast<v8bf *>(xb + 2 * plane + o) = lo;
@@ -437,7 +437,7 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
             int kq, sp, t, c;
             piece(f, kq, sp, t, c);
             xr[slot][f] = *reinterpret_cast<const v4u *>(
-                p.xb + sp * plane + xpiece((kq * klen + b * KB) / 8 + c, min(t0 + t, p.T - 1), p.T));
+                p.xb + sp * plane + xpiece((kq * klen + b * KB) / 8 + c, min(t0 + t, p.T - 1), p.T, p.I));
         }
     };
     auto x_stage = [&](int buf, auto slot_c) __attribute__((always_inline)) {
@@ -601,8 +601,10 @@ void proj_q8_bf16x3_kernel(const ProjArgs p) {
 // its partial tile, and the last of the G to arrive (arrival counter) sums
 // the G tiles in order, so the result does not depend on arrival order
 // (device-coherent atomic stores and loads, as the sliced decode norm).
-// Operand k order within a 64-wide block: lane (l%16, g) holds
-// k = 16g + 8s + j of step s, j < 8, on both operands.
+// Operand k order within a 128-wide superblock (the x plane layout,
+// xpiece): lane (l%16, g) holds k = 32g + 8s + j of step s < 4, j < 8, on
+// both operands; a weight "block" of the rings below is half a superblock
+// (16 bytes per lane: steps 0-1 or 2-3).
 constexpr int kWvRows = 64, kWvK = 64;
 
 // Rows beside the int8 ones in the same launch: the fp32 rows of the
@@ -654,7 +656,7 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
     const int8_t *wp[RW];
     const uint16_t *xp[TT];
 #pragma unroll
-    for (int rw = 0; rw < RW; rw++) wp[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + k0 + 16 * gq;
+    for (int rw = 0; rw < RW; rw++) wp[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + k0 + 32 * gq;
 #pragma unroll
     for (int tt = 0; tt < TT; tt++) xp[tt] = p.xb + (size_t)min(t0 + 16 * tt + l16, p.T - 1) * 32 + 8 * gq;
     const size_t chunk = (size_t)p.T * 32;        // one 32-value chunk of every token
@@ -678,7 +680,8 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
         constexpr int sl = decltype(slot_c)::value;
         b = min(b, nb - 1);
 #pragma unroll
-        for (int rw = 0; rw < RW; rw++) wq[sl][rw] = *reinterpret_cast<const int4 *>(wp[rw] + b * kWvK);
+        for (int rw = 0; rw < RW; rw++)
+            wq[sl][rw] = *reinterpret_cast<const int4 *>(wp[rw] + (b / 2) * (2 * kWvK) + 16 * (b % 2));
     };
     auto x_load = [&](int q, auto slot_c) __attribute__((always_inline)) {
         constexpr int sl = decltype(slot_c)::value;

@@ -73,16 +73,21 @@ struct DecodeArgs {
 };
 
 // Layout of the bf16 planes of x (the int8 projections' scratch, x as
-// hi + mid + lo): per plane, 32-value chunks [2 * (I / 64)][T][32].  Chunk
-// 2c + s of token t holds, at position 8g + j, the value at
-// k = 64c + 16g + 8s + j (g < 4, j < 8): exactly what lane group g of a
-// 16-token MFMA operand reads in step s of 64-wide k block c (the k order
-// both operands share).  So 16 tokens' operand for one step is one
-// contiguous 1 KiB run, and every 16-byte piece of 8 consecutive k is
-// contiguous.  Element offset of the piece holding k = 8m .. 8m+7 of
-// token t (planes of T * I elements each, then fp32 sums [T][I / 64]):
-__host__ __device__ inline size_t xpiece(int m, int t, int T) {
-    return ((size_t)(2 * (m / 8) + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
+// hi + mid + lo): per plane, 32-value chunks [I / 32][T][32].  Chunk 4c + s
+// of token t holds, at position 8g + j, the value at k = 128c + 32g + 8s + j
+// (g < 4, j < 8): exactly what lane group g of a 16-token MFMA operand
+// reads in step s of 128-wide k superblock c (the k order both operands
+// share: lane group g of a weight fragment then holds 32 consecutive k of
+// its row, two 16-byte loads that together cover whole 128-byte lines).
+// So 16 tokens' operand for one step is one contiguous 1 KiB run, and every
+// 16-byte piece of 8 consecutive k is contiguous.  Element offset of the
+// piece holding k = 8m .. 8m+7 of token t (planes of T * I elements each,
+// then fp32 sums [T][I / 64]).  A trailing 64-wide block (I % 128 == 64)
+// takes the last two chunks, in the 64-wide form of the same order.
+__host__ __device__ inline size_t xpiece(int m, int t, int T, int I) {
+    const int full = I / 128, c = m / 16;
+    if (c < full) return ((size_t)(4 * c + m % 4) * T + t) * 32 + 8 * ((m % 16) / 4);
+    return ((size_t)(4 * full + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
 }
 
 // y[t][o] = sum_i x[t][i] * W[o][i] for t < T, o < O.  Rows o < n_q come
