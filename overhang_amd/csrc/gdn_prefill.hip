@@ -11,15 +11,16 @@
 //     S <- e^{gc_last} S + (K * e^{gc_last - gc})^T v_new
 // Only exp of differences of cumulative decays are formed, never exp(-gc).
 //
-// Four launches, all on the caller's stream:
-//   P1 wy      per (value head, chunk): conv + SiLU, q/k L2 norm, gates,
-//              KK^T, QK^T, (I+L)^-1 blocks, W, U on fp32 MFMA, written as
-//              per-lane fragment panels                            MFMA-bound
-//   P2 commit  conv history ring -> last K-1 inputs, new phase     tiny
+// Three launches, all on the caller's stream:
+//   P1 wy      per (key head, chunk) with its value heads: conv + SiLU, q/k
+//              L2 norm, gates, KK^T, QK^T, (I+L)^-1 blocks, W, U on fp32
+//              MFMA, written as per-lane fragment panels           MFMA-bound
 //   P3 scan    per (value head, 16-column block of S): the chunk
 //              recurrence and the raw outputs, sequential over chunks, on
 //              fp32 MFMA                                           MFMA-bound
 //   P4 norm    gated RMSNorm of the head outputs                   HBM-bound
+//              + P2 commit (extra blocks of the same launch): conv history
+//              ring -> last K-1 inputs, new phase                  tiny
 //
 // MFMA conventions (v_mfma_f32_16x16x4_f32, lane l, g = l / 16):
 //   A[16][4]: lane holds A[l%16][g];  B[4][16]: lane holds B[g][l%16];
@@ -78,10 +79,11 @@ __device__ __forceinline__ size_t panj(size_t hc, int j, int kt, int l) {
 // the new inputs among the last K-1 are written.  Every block reads the
 // phase from phase[epoch]; the new one goes to phase[1 - epoch] (block 0
 // also carries the other sequences' phases over) and the host flips the
-// layer's epoch after the launch, as for decode launches.
-__global__ __launch_bounds__(256)
-void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
+// layer's epoch after the launch, as for decode launches.  Runs as extra
+// 256-thread blocks of the gated-norm launch (after the WY kernel, which
+// reads the old history).
+__device__ __forceinline__ void conv_commit(const PrefillArgs &a, int conv_dim, int blk) {
+    const int c = blk * 256 + threadIdx.x;
     const int K = a.K, T = a.T;
     const int ph = a.L.phase[a.L.epoch * a.L.max_seqs + a.seq];
     const int nph = (ph + T) & (kConvRing - 1);
@@ -93,7 +95,7 @@ void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
                 rs[(size_t)ring_slot(nph, K, j) * conv_dim] = a.qkv[(size_t)(idx - (K - 1)) * a.ld_qkv + c];
         }
     }
-    if (blockIdx.x == 0) {
+    if (blk == 0) {
         int *nxt = a.L.phase + (1 - a.L.epoch) * a.L.max_seqs;
         const int *cur = a.L.phase + a.L.epoch * a.L.max_seqs;
         for (int s = threadIdx.x; s < a.L.max_seqs; s += 256) nxt[s] = s == a.seq ? nph : cur[s];
@@ -101,9 +103,14 @@ void prefill_conv_commit_kernel(const PrefillArgs a, int conv_dim) {
 }
 
 // ---------------------------------------------------------------- P4 norm
+// Blocks nnorm and above: the conv-history commit.
 template <int D>
 __global__ __launch_bounds__(256)
-void prefill_gated_norm_kernel(const PrefillArgs a) {
+void prefill_gated_norm_kernel(const PrefillArgs a, int nnorm, int conv_dim) {
+    if ((int)blockIdx.x >= nnorm) {
+        conv_commit(a, conv_dim, blockIdx.x - nnorm);
+        return;
+    }
     constexpr int LPR = D / 4;                   // lanes per row
     constexpr int RPB = 256 / LPR;               // rows per block
     const int l4 = threadIdx.x % LPR;
@@ -1000,15 +1007,17 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     const int rep = a.vh / a.kh;
     const int nitems = a.kh * (rep % 2 == 0 ? rep / 2 : rep) * a.nc;   // as in the kernel
     const int grid = nitems < wy_grid() ? nitems : wy_grid();
-    // the WY kernel reads the ring for chunk 0 before the commit rewrites it
+    // the WY kernel reads the ring for chunk 0 before the commit (in the
+    // norm launch) rewrites it
     if (a.K == 4) hipLaunchKernelGGL((prefill_wy_kernel<D, 4>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     else if (a.K == 3) hipLaunchKernelGGL((prefill_wy_kernel<D, 3>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     else hipLaunchKernelGGL((prefill_wy_kernel<D, 2>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
-    hipLaunchKernelGGL(prefill_conv_commit_kernel, dim3((conv_dim + 255) / 256), dim3(256), 0, st, a, conv_dim);
     hipLaunchKernelGGL((prefill_scan_kernel<D>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
     constexpr int RPB = 256 / (D / 4);
     const size_t rows = (size_t)a.T * a.vh;
-    hipLaunchKernelGGL((prefill_gated_norm_kernel<D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, a);
+    const int nnorm = (int)((rows + RPB - 1) / RPB), ncommit = (conv_dim + 255) / 256;
+    hipLaunchKernelGGL((prefill_gated_norm_kernel<D>), dim3((unsigned)(nnorm + ncommit)), dim3(256), 0, st, a, nnorm,
+                       conv_dim);
     return hipGetLastError();
 }
 
