@@ -8,19 +8,24 @@
 // one launch: rows below n_q use the int8 matrix, the rest the fp32 one
 // (n_q is a multiple of 16, so a 16-row tile is one or the other).
 //
-// Both kernels stream each weight row from HBM once per launch (the bound
-// for decode batches), with every lane reading 16 consecutive weights per
-// load (16 B of int8 or 64 B of fp32):
+// Every kernel streams each weight row from HBM once per launch and token
+// tile (the bound for decode batches), every lane reading 16 consecutive
+// weights per load (16 B of int8 or 64 B of fp32):
 //   * T <= 4 tokens: GEMV.  A wave takes 8 rows and one k-slice; lane l
 //     covers k = 1024c + 16l + e of it, with the 8 rows' weights in flight
 //     together; the 8 row sums are reduced over the lanes in one butterfly
 //     and the k-slices through LDS.
-//   * T > 4: fp32 MFMA (16x16x4), tokens x rows tiles.  Within a 64-wide
-//     k block, lane (l%16, g) holds x and W at k = 16g + 4j + s for its
-//     token / row l%16, so one 16-byte weight load and four float4 x loads
-//     feed 16 MFMAs (the k order is permuted identically on both operands).
-//     A workgroup is RT row tiles x KS k-slices (RT * KS = 4 waves); the
-//     k-slices are summed through LDS.
+//   * T > 4, int8 rows: exact bf16 x 3 products on the bf16 matrix cores
+//     (proj_q8_wave_kernel: 64-row x 16 TT-token tiles per wave, operands
+//     straight into registers; proj_q8_bf16x3_kernel for the shapes its
+//     plan does not take), see the section further down.
+//   * T > 4, fp32 rows: fp32 MFMA (16x16x4), tokens x rows tiles.  Within a
+//     64-wide k block, lane (l%16, g) holds x and W at k = 16g + 4j + s for
+//     its token / row l%16, so one 16-byte weight load and four float4 x
+//     loads feed 16 MFMAs (the k order is permuted identically on both
+//     operands).  A workgroup is RT row tiles x KS k-slices (RT * KS = 4
+//     waves); the k-slices are summed through LDS.  Beside int8 rows the
+//     fp32 rows run as extra workgroups of the int8 launch where they can.
 #include "omh_device.h"
 #include "omh_internal.h"
 #include <type_traits>
