@@ -39,6 +39,12 @@
 // the K-1 history slots, the single owner of a channel writes the new input
 // into the free slot.
 //
+// When the step feeds an int8 out_proj, the epilogue also writes the gated
+// output as that projection's exact bf16 x 3 planes and 64-wide block sums
+// (write_planes), so the projection needs no split launch.  A launch covers
+// sequences b0 .. b0+B-1; the host runs one layer's large batch as several
+// launches that each fit one round of resident workgroups.
+//
 // Thread layout: TPB threads hold RPT rows x 4 adjacent columns (a float4)
 // of a head (or slice); a wavefront's loads cover whole consecutive row
 // segments.  Column sums over rows are butterflies across the row groups of
