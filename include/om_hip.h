@@ -125,6 +125,45 @@ int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void
 /* Wait for all work this library enqueued on `stream`. */
 int omh_sync(void *stream);
 
+/* ---- gated full-attention layer (the 1-in-4 non-GDN layer) ---- */
+
+/* Dimensions as the engine reads them from config.json: num_attention_heads,
+ * num_key_value_heads, head_dim, rot_dim = head_dim * partial_rotary_factor,
+ * rope_theta, rms_norm_eps (engines/qwen.c:367-369), plus the KV cache
+ * length max_t (the engine's m->max_t, qwen.c:257-258). */
+typedef struct {
+    int hidden;
+    int n_heads, n_kv, head_dim, rot_dim;
+    float theta, eps;
+    int max_t;
+} omh_attn_dims;
+
+/* The layer's tensors (engines/qwen.c:244-255): q_proj [2*H*hd][hidden]
+ * (per head [hd q | hd gate], qwen.c:376-382), k_proj and v_proj
+ * [KV*hd][hidden], o_proj [hidden][H*hd], each fp32 or int8 + per-row
+ * scale (all three of q/k/v in one form); q_norm, k_norm [hd]. */
+typedef struct {
+    const float *W_q, *W_k, *W_v, *W_o;
+    const int8_t *Q_q, *Q_k, *Q_v, *Q_o;
+    const float *S_q, *S_k, *S_v, *S_o;
+    const float *q_norm, *k_norm;
+} omh_attn_weights;
+
+/* Attention layer ids are a namespace of their own, separate from the GDN
+ * layer ids.  The K and V caches ([max_seqs][n_kv][max_t][head_dim] each,
+ * the engine's m->K[li] / m->V[li] per sequence) live on the device. */
+int omh_attn_layer_init(int li, const omh_attn_dims *d, const omh_attn_weights *w, int max_seqs);
+int omh_attn_layer_free(int li);
+
+/* T tokens x[T][hidden] of sequence seq at positions pos .. pos+T-1 ->
+ * out[T][hidden]; writes their K and V into the cache and attends causally
+ * over positions 0 .. pos+t, which earlier calls must have written.  T = 1
+ * replaces attn_step(m, l, li, x, pos, out) (engines/qwen.c:367); T > 1 is
+ * the batched prompt step the engine runs token by token
+ * (qwen.c:588, 637).  Requires pos + T <= max_t. */
+int omh_attn_forward(int li, int seq, int pos, int T, const float *x, float *out);
+int omh_attn_forward_dev(int li, int seq, int pos, int T, const float *x, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -280,6 +280,82 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     return OMH_OK;
 }
 
+// ---- gated full-attention layers (engines/qwen.c:366-425) ----
+struct AttnLayer {
+    bool live = false;
+    omh_attn_dims d{};
+    int max_seqs = 0, rows = 0, nq = 0, qdim = 0;   // projection rows [H x (q|gate), KV x k, KV x v]; int8 rows; H*hd
+    int8_t *Qin = nullptr;
+    float *Sin = nullptr, *Win = nullptr;
+    int out_nq = 0;
+    int8_t *Qout = nullptr;
+    float *Sout = nullptr, *Wout = nullptr;
+    float *qn = nullptr, *kn = nullptr, *inv = nullptr;
+    float *Kc = nullptr, *Vc = nullptr;
+};
+AttnLayer g_A[kMaxLayers];
+Scratch g_arow, g_aqb, g_actx, g_apo, g_apml;
+
+void free_attn(AttnLayer &A) {
+    void *ps[] = {A.Qin, A.Sin, A.Win, A.Qout, A.Sout, A.Wout, A.qn, A.kn, A.inv, A.Kc, A.Vc};
+    for (void *p : ps)
+        if (p) (void)hipFree(p);
+    A = AttnLayer{};
+}
+
+int check_attn(int li) {
+    if (li < 0 || li >= kMaxLayers || !g_A[li].live) return fail(OMH_ERR_ARG, "attention layer %d not initialised", li);
+    return OMH_OK;
+}
+
+int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hipStream_t st) {
+    if (int rc = check_attn(li)) return rc;
+    const AttnLayer &A = g_A[li];
+    const omh_attn_dims &d = A.d;
+    if (seq < 0 || seq >= A.max_seqs) return fail(OMH_ERR_ARG, "attn: seq %d outside [0, %d)", seq, A.max_seqs);
+    if (T < 0 || pos < 0 || (long)pos + T > d.max_t)
+        return fail(OMH_ERR_ARG, "attn: positions %d..%d outside the cache of %d", pos, pos + T - 1, d.max_t);
+    if (T == 0) return OMH_OK;
+    if (!x || !out || !aligned16(x) || !aligned16(out)) return fail(OMH_ERR_ARG, "attn: x/out must be 16-byte aligned");
+    const int D = d.hidden, hd = d.head_dim, H = d.n_heads;
+    int ns = 0, kps = 0;
+    attn_plan(pos, T, d.n_kv, ns, kps);
+    const size_t nth = (size_t)T * H;
+    if (int rc = ensure(g_arow, (size_t)T * A.rows * sizeof(float))) return rc;
+    if (int rc = ensure(g_aqb, nth * hd * sizeof(float))) return rc;
+    if (int rc = ensure(g_actx, nth * hd * sizeof(float))) return rc;
+    if (int rc = ensure(g_apo, nth * ns * hd * sizeof(float))) return rc;
+    if (int rc = ensure(g_apml, nth * ns * 2 * sizeof(float))) return rc;
+    uint16_t *xb = nullptr;
+    if (T > 4 && (A.nq > 0 || A.out_nq > 0)) {
+        const size_t xbn = std::max(proj_xb_bytes(T, D, A.nq), proj_xb_bytes(T, A.qdim, A.out_nq));
+        if (int rc = ensure(g_xb, xbn)) return rc;
+        xb = static_cast<uint16_t *>(g_xb.p);
+    }
+    float *rowb = static_cast<float *>(g_arow.p), *ctx = static_cast<float *>(g_actx.p);
+    ProjArgs p{};
+    p.x = x; p.ldx = D; p.y = rowb; p.ldy = A.rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
+    p.Q = A.Qin; p.scale = A.Sin; p.W = A.Win; p.T = T; p.I = D; p.O = A.rows; p.n_q = A.nq;
+    HIP_OK(launch_proj(p, st));
+    AttnArgs a{};
+    a.qkv = rowb; a.ld_qkv = A.rows;
+    a.qn = A.qn; a.kn = A.kn; a.inv = A.inv; a.Kc = A.Kc; a.Vc = A.Vc;
+    a.qb = static_cast<float *>(g_aqb.p);
+    a.po = static_cast<float *>(g_apo.p);
+    a.pml = static_cast<float *>(g_apml.p);
+    a.ctx = ctx;
+    a.seq = seq; a.pos = pos; a.T = T; a.H = H; a.KV = d.n_kv; a.rot = d.rot_dim; a.max_t = d.max_t;
+    a.ns = ns; a.kps = kps;
+    a.eps = d.eps;
+    a.scale = 1.f / sqrtf((float)hd);                // qwen.c:405
+    HIP_OK(launch_attn(a, hd, st));
+    ProjArgs q{};
+    q.x = ctx; q.ldx = A.qdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
+    q.Q = A.Qout; q.scale = A.Sout; q.W = A.Wout; q.T = T; q.I = A.qdim; q.O = D; q.n_q = A.out_nq;
+    HIP_OK(launch_proj(q, st));
+    return OMH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -580,6 +656,110 @@ int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void
 int omh_sync(void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;
     HIP_OK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return OMH_OK;
+}
+
+int omh_attn_layer_init(int li, const omh_attn_dims *d, const omh_attn_weights *w, int max_seqs) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (li < 0 || li >= kMaxLayers) return fail(OMH_ERR_ARG, "attention layer id %d outside [0, %d)", li, kMaxLayers);
+    if (!d || !w || max_seqs < 1) return fail(OMH_ERR_ARG, "attn_layer_init: null dims/weights or max_seqs < 1");
+    if (d->hidden < 1 || d->n_heads < 1 || d->n_kv < 1 || d->head_dim < 1 || d->max_t < 1)
+        return fail(OMH_ERR_ARG, "attn_layer_init: bad dims hidden=%d H=%d KV=%d hd=%d max_t=%d", d->hidden,
+                    d->n_heads, d->n_kv, d->head_dim, d->max_t);
+    if (!attn_supported(d->head_dim, d->n_heads, d->n_kv, d->rot_dim))
+        return fail(OMH_ERR_SHAPE, "attn_layer_init: hd=%d H=%d KV=%d rot=%d unsupported", d->head_dim, d->n_heads,
+                    d->n_kv, d->rot_dim);
+    const bool q8 = w->Q_q != nullptr;
+    if (q8 && (!w->Q_k || !w->Q_v || !w->S_q || !w->S_k || !w->S_v))
+        return fail(OMH_ERR_ARG, "attn_layer_init: int8 q/k/v need Q_q, Q_k, Q_v and their scales");
+    if (!q8 && (!w->W_q || !w->W_k || !w->W_v)) return fail(OMH_ERR_ARG, "attn_layer_init: fp32 q/k/v need W_q, W_k, W_v");
+    if (!w->Q_o && !w->W_o) return fail(OMH_ERR_ARG, "attn_layer_init: o_proj missing");
+    if (w->Q_o && !w->S_o) return fail(OMH_ERR_ARG, "attn_layer_init: o_proj scales missing");
+    if (!w->q_norm || !w->k_norm) return fail(OMH_ERR_ARG, "attn_layer_init: q_norm and k_norm are required");
+    const int D = d->hidden, H = d->n_heads, KV = d->n_kv, hd = d->head_dim;
+    AttnLayer A;
+    A.d = *d;
+    A.max_seqs = max_seqs;
+    A.qdim = H * hd;
+    A.rows = 2 * H * hd + 2 * KV * hd;
+    A.nq = q8 ? A.rows : 0;
+    A.out_nq = w->Q_o ? D : 0;
+    if (!proj_supported(D, A.nq) || !proj_supported(A.qdim, A.out_nq))
+        return fail(OMH_ERR_SHAPE, "attn_layer_init: projections need hidden and H*hd multiples of 64 (got %d, %d)", D, A.qdim);
+    if (g_A[li].live) free_attn(g_A[li]);
+    int rc = OMH_OK;
+#define UPA(dst, n, src) do { if ((rc = upload(&(dst), (size_t)(n), (src))) != OMH_OK) { free_attn(A); return rc; } } while (0)
+    const size_t Dz = (size_t)D, nqr = (size_t)2 * H * hd, nkr = (size_t)KV * hd;
+    if (q8) {
+        std::vector<int8_t> q((size_t)A.rows * Dz);
+        memcpy(q.data(), w->Q_q, nqr * Dz);
+        memcpy(q.data() + nqr * Dz, w->Q_k, nkr * Dz);
+        memcpy(q.data() + (nqr + nkr) * Dz, w->Q_v, nkr * Dz);
+        std::vector<float> s(A.rows);
+        memcpy(s.data(), w->S_q, nqr * sizeof(float));
+        memcpy(s.data() + nqr, w->S_k, nkr * sizeof(float));
+        memcpy(s.data() + nqr + nkr, w->S_v, nkr * sizeof(float));
+        UPA(A.Qin, q.size(), q.data());
+        UPA(A.Sin, s.size(), s.data());
+    } else {
+        std::vector<float> f((size_t)A.rows * Dz);
+        memcpy(f.data(), w->W_q, nqr * Dz * sizeof(float));
+        memcpy(f.data() + nqr * Dz, w->W_k, nkr * Dz * sizeof(float));
+        memcpy(f.data() + (nqr + nkr) * Dz, w->W_v, nkr * Dz * sizeof(float));
+        UPA(A.Win, f.size(), f.data());
+    }
+    if (w->Q_o) {
+        UPA(A.Qout, (size_t)D * A.qdim, w->Q_o);
+        UPA(A.Sout, D, w->S_o);
+    } else {
+        UPA(A.Wout, (size_t)D * A.qdim, w->W_o);
+    }
+    UPA(A.qn, hd, w->q_norm);
+    UPA(A.kn, hd, w->k_norm);
+    {
+        // RoPE inverse frequencies, the engine's expression (qwen.c:392)
+        const int half = d->rot_dim / 2;
+        std::vector<float> inv(half > 0 ? half : 1, 0.f);
+        for (int j = 0; j < half; j++) inv[j] = powf(d->theta, -(float)(2 * j) / (float)d->rot_dim);
+        UPA(A.inv, inv.size(), inv.data());
+    }
+    const size_t nc = (size_t)max_seqs * KV * d->max_t * hd;
+    UPA(A.Kc, nc, (const float *)nullptr);
+    UPA(A.Vc, nc, (const float *)nullptr);
+    if (hipMemset(A.Kc, 0, nc * sizeof(float)) != hipSuccess || hipMemset(A.Vc, 0, nc * sizeof(float)) != hipSuccess) {
+        free_attn(A);
+        return fail(OMH_ERR_DEVICE, "attn_layer_init: cache clear failed");
+    }
+#undef UPA
+    A.live = true;
+    g_A[li] = A;
+    return OMH_OK;
+}
+
+int omh_attn_layer_free(int li) {
+    if (int rc = check_attn(li)) return rc;
+    if (hipDeviceSynchronize() != hipSuccess) return fail(OMH_ERR_DEVICE, "attn_layer_free: sync failed");
+    free_attn(g_A[li]);
+    return OMH_OK;
+}
+
+int omh_attn_forward_dev(int li, int seq, int pos, int T, const float *x, float *out, void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    return attn_forward(li, seq, pos, T, x, out, static_cast<hipStream_t>(stream));
+}
+
+int omh_attn_forward(int li, int seq, int pos, int T, const float *x, float *out) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_attn(li)) return rc;
+    if (T < 0 || (T > 0 && (!x || !out))) return fail(OMH_ERR_ARG, "attn: bad arguments");
+    if (T == 0) return OMH_OK;
+    const size_t n = (size_t)T * g_A[li].d.hidden;
+    if (int rc = ensure(g_x, n * 4)) return rc;
+    if (int rc = ensure(g_out, n * 4)) return rc;
+    HIP_OK(hipMemcpyAsync(g_x.p, x, n * 4, hipMemcpyHostToDevice, g_stream));
+    if (int rc = attn_forward(li, seq, pos, T, (const float *)g_x.p, (float *)g_out.p, g_stream)) return rc;
+    HIP_OK(hipMemcpyAsync(out, g_out.p, n * 4, hipMemcpyDeviceToHost, g_stream));
+    HIP_OK(hipStreamSynchronize(g_stream));
     return OMH_OK;
 }
 

@@ -138,6 +138,26 @@ void prefill_bind_scratch(PrefillArgs &a, int D, void *base);
 bool prefill_supported(int kd, int vd, int rep, int K);
 hipError_t launch_prefill_core(const PrefillArgs &a, int D, hipStream_t st);
 
+// Gated full attention (engines/qwen.c:366-425) for T tokens of sequence
+// seq at positions pos .. pos+T-1, after the qkv projection.
+constexpr int kAttnMaxGroup = 16;     // query heads per kv head
+struct AttnArgs {
+    const float *qkv; int64_t ld_qkv;  // [T] rows: H x (hd q, hd gate), KV x hd k, KV x hd v
+    const float *qn, *kn;              // [hd] RMSNorm weights of q and k (applied as 1 + w)
+    const float *inv;                  // [rot / 2] RoPE inverse frequencies
+    float *Kc, *Vc;                    // [max_seqs][KV][max_t][hd] caches
+    float *qb;                         // [T][H][hd] scratch: q after norm and RoPE
+    float *po, *pml;                   // [T][H][ns][hd] partial outputs, [T][H][ns][2] running max and sum
+    float *ctx;                        // [T][H * hd] gated attention output
+    int seq, pos, T, H, KV, rot, max_t;
+    int ns, kps;                       // key splits and keys per split (attn_plan)
+    float eps, scale;                  // RMSNorm eps, hd^-1/2
+};
+bool attn_supported(int hd, int H, int KV, int rot);
+// splits for pos + T visible keys: ns * KV * T >= 512 workgroups where the keys allow
+void attn_plan(int pos, int T, int KV, int &ns, int &kps);
+hipError_t launch_attn(const AttnArgs &a, int hd, hipStream_t st);
+
 // Returns hipSuccess, or hipErrorInvalidValue for an unsupported shape.
 // variant: 0 = chosen by launch size; kDecodePaired = one workgroup per key
 // head streaming its value heads; 1, 2, 4, 8 = one workgroup per column

@@ -27,6 +27,7 @@ EXPORTS = (
     "omh_gdn_decode", "omh_gdn_prefill", "omh_gdn_decode_core", "omh_gdn_prefill_core",
     "omh_gdn_decode_core_dev", "omh_gdn_prefill_core_dev", "omh_gdn_decode_dev",
     "omh_gdn_prefill_dev", "omh_sync",
+    "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
 )
 
 
@@ -47,6 +48,19 @@ _WFIELDS = ("W_qkv", "W_z", "W_b", "W_a", "W_out", "Q_qkv", "Q_z", "Q_out",
 
 class _Weights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in _WFIELDS]
+
+
+class _AttnDims(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv", C.c_int), ("head_dim", C.c_int),
+                ("rot_dim", C.c_int), ("theta", C.c_float), ("eps", C.c_float), ("max_t", C.c_int)]
+
+
+_AFIELDS = ("W_q", "W_k", "W_v", "W_o", "Q_q", "Q_k", "Q_v", "Q_o",
+            "S_q", "S_k", "S_v", "S_o", "q_norm", "k_norm")
+
+
+class _AttnWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _AFIELDS]
 
 
 _LIB = None
@@ -76,6 +90,10 @@ def lib() -> C.CDLL:
         L.omh_gdn_decode_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_gdn_prefill_dev.argtypes = [i, i, i, vp, vp, vp]
         L.omh_sync.argtypes = [vp]
+        L.omh_attn_layer_init.argtypes = [i, C.POINTER(_AttnDims), C.POINTER(_AttnWeights), i]
+        L.omh_attn_layer_free.argtypes = [i]
+        L.omh_attn_forward.argtypes = [i, i, i, i, vp, vp]
+        L.omh_attn_forward_dev.argtypes = [i, i, i, i, vp, vp, vp]
         _LIB = L
     return _LIB
 
@@ -224,3 +242,41 @@ def prefill_dev(li: int, seq: int, T: int, x, out, stream=None) -> None:
 
 def sync(stream=None) -> None:
     check(lib().omh_sync(_stream(stream)))
+
+
+class AttnLayer:
+    """One gated full-attention layer (engines/qwen.c:366-425) held by the
+    library under attention id ``li`` (a namespace apart from the GDN ids),
+    with a K/V cache of ``max_t`` positions for each of ``max_seqs``
+    sequences.
+
+    ``weights`` holds numpy arrays named as in omh_attn_weights (W_q, W_k,
+    W_v, W_o, q_norm, k_norm); with ``int8=True`` the four projections are
+    quantised per row here (the engine's load-time step, qwen.c:252-255)."""
+
+    def __init__(self, li: int, hidden: int, n_heads: int, n_kv: int, head_dim: int, rot_dim: int,
+                 theta: float, eps: float, max_t: int, weights: dict, max_seqs: int = 1, int8: bool = False):
+        require_gpu()
+        self.li, self.hidden = li, hidden
+        keep = {k: (v if k.startswith(("Q_", "S_")) else _f32(v)) for k, v in weights.items()}
+        if int8:
+            for nm in ("q", "k", "v", "o"):
+                keep["Q_" + nm], keep["S_" + nm] = quantize_rows(keep.pop("W_" + nm))
+        self._keep = keep
+        w = _AttnWeights(**{k: (_ptr(keep[k]) if k in keep else None) for k in _AFIELDS})
+        d = _AttnDims(hidden, n_heads, n_kv, head_dim, rot_dim, theta, eps, max_t)
+        check(lib().omh_attn_layer_init(li, C.byref(d), C.byref(w), max_seqs))
+
+    def free(self) -> None:
+        check(lib().omh_attn_layer_free(self.li))
+
+    def forward(self, seq: int, pos: int, x: np.ndarray) -> np.ndarray:
+        """x [T][hidden] at positions pos .. pos+T-1 -> [T][hidden]."""
+        x = _f32(x)
+        out = np.empty_like(x)
+        check(lib().omh_attn_forward(self.li, seq, pos, x.shape[0], _ptr(x), _ptr(out)))
+        return out
+
+
+def attn_forward_dev(li: int, seq: int, pos: int, T: int, x, out, stream=None) -> None:
+    check(lib().omh_attn_forward_dev(li, seq, pos, T, _ptr(x), _ptr(out), _stream(stream)))

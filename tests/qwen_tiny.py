@@ -119,11 +119,60 @@ class HipGdn:
             L.free()
 
 
+_ATTN_W = ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
+
+
+def gated_attention(x, W, Kl, Vl, pos, H, KV, hd, rot, theta, eps):
+    """The engine's attn_step (qwen.c:366-425) for T tokens x [T][D] at
+    positions pos..pos+T-1, in float32: q/gate split per head (qwen.c:376-382),
+    RMSNorm of q and k with (1 + w) (385-386), partial RoPE over the first rot
+    dims as two halves (388-398), causal softmax attention over the cache
+    (405-419), output gate and o_proj (421-422).  W maps q_proj, k_proj,
+    v_proj, o_proj, q_norm, k_norm to arrays; Kl / Vl are the lists of
+    [t][KV][hd] cache blocks, appended to here."""
+    T = x.shape[0]
+    qg = (x @ W["q_proj"].T).reshape(T, H, 2 * hd)
+    q, gate = qg[:, :, :hd], qg[:, :, hd:].reshape(T, H * hd)
+    k = (x @ W["k_proj"].T).reshape(T, KV, hd)
+    v = (x @ W["v_proj"].T).reshape(T, KV, hd)
+    q = rmsnorm(q, W["q_norm"], eps)
+    k = rmsnorm(k, W["k_norm"], eps)
+    half = rot // 2
+    j = np.arange(half)
+    inv = np.power(f32(theta), -(2.0 * j).astype(f32) / f32(rot)).astype(f32)
+    ps = np.arange(pos, pos + T, dtype=f32)[:, None]
+    ang = (ps * inv[None, :]).astype(f32)
+    cs, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+
+    def rope(vec):
+        a0, b0 = vec[..., :half].copy(), vec[..., half:rot].copy()
+        vec = vec.copy()
+        vec[..., :half] = a0 * cs - b0 * sn
+        vec[..., half:rot] = b0 * cs + a0 * sn
+        return vec.astype(f32)
+
+    q, k = rope(q), rope(k)
+    Kl.append(k)
+    Vl.append(v)
+    Kc, Vc = np.concatenate(Kl), np.concatenate(Vl)                      # [pos+T][KV][hd]
+    n = Kc.shape[0]
+    grp = H // KV
+    ctx = np.empty((T, H, hd), f32)
+    scale = f32(1.0) / np.sqrt(f32(hd))
+    for h in range(H):
+        sc = (q[:, h, :] @ Kc[:, h // grp, :].T).astype(f32) * scale        # [T][n]
+        mask = np.arange(n)[None, :] > (pos + np.arange(T))[:, None]
+        sc[mask] = -np.inf
+        ctx[:, h, :] = softmax(sc) @ Vc[:, h // grp, :]
+    ctx = ctx.reshape(T, H * hd) * sigmoid(gate)
+    return (ctx @ W["o_proj"].T).astype(f32)
+
+
 class TinyQwen:
     """The reference engine's forward (qwen.c:507-528) with the GDN layers
     delegated to ``backend(d, {layer: weights})``."""
 
-    def __init__(self, backend_cls, path: str = TINY_DIR, **kw):
+    def __init__(self, backend_cls, path: str = TINY_DIR, gpu_attn_li=None, **kw):
         self.cfg, self.W, self.ref = load_tiny(path)
         c = self.cfg
         self.D, self.eps = c["hidden_size"], c.get("rms_norm_eps", 1e-6)
@@ -141,51 +190,31 @@ class TinyQwen:
         self.K = {i: [] for i in range(self.nl) if self.is_full[i]}
         self.V = {i: [] for i in range(self.nl) if self.is_full[i]}
         self.pos = 0
+        self.attn_gpu = None
+        if gpu_attn_li is not None:                 # attention layers on libom_hip.so too
+            from overhang_amd import gdn
+            self.attn_gpu = {}
+            for i in self.K:
+                p = f"model.layers.{i}.self_attn."
+                w = {"W_q": self.W[p + "q_proj.weight"], "W_k": self.W[p + "k_proj.weight"],
+                     "W_v": self.W[p + "v_proj.weight"], "W_o": self.W[p + "o_proj.weight"],
+                     "q_norm": self.W[p + "q_norm.weight"], "k_norm": self.W[p + "k_norm.weight"]}
+                self.attn_gpu[i] = gdn.AttnLayer(gpu_attn_li + i, self.D, self.H, self.KV, self.hd, self.rot,
+                                                 self.theta, self.eps, 64, w)
         self.lm_head = self.W.get("lm_head.weight", self.W["model.embed_tokens.weight"])
 
     def close(self):
         self.gdn.close()
+        for L in (self.attn_gpu or {}).values():
+            L.free()
 
     # -- gated full attention over T new tokens at positions pos..pos+T-1 (qwen.c:366-425)
     def attn(self, i, x):
-        T = x.shape[0]
+        if self.attn_gpu is not None:
+            return self.attn_gpu[i].forward(0, self.pos, x)
         p = f"model.layers.{i}.self_attn."
-        H, KV, hd, rot = self.H, self.KV, self.hd, self.rot
-        qg = (x @ self.W[p + "q_proj.weight"].T).reshape(T, H, 2 * hd)
-        q, gate = qg[:, :, :hd], qg[:, :, hd:].reshape(T, H * hd)
-        k = (x @ self.W[p + "k_proj.weight"].T).reshape(T, KV, hd)
-        v = (x @ self.W[p + "v_proj.weight"].T).reshape(T, KV, hd)
-        q = rmsnorm(q, self.W[p + "q_norm.weight"], self.eps)
-        k = rmsnorm(k, self.W[p + "k_norm.weight"], self.eps)
-        half = rot // 2
-        j = np.arange(half)
-        inv = np.power(f32(self.theta), -(2.0 * j).astype(f32) / f32(rot)).astype(f32)
-        pos = np.arange(self.pos, self.pos + T, dtype=f32)[:, None]
-        ang = (pos * inv[None, :]).astype(f32)
-        cs, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
-
-        def rope(vec):
-            a0, b0 = vec[..., :half].copy(), vec[..., half:rot].copy()
-            vec = vec.copy()
-            vec[..., :half] = a0 * cs - b0 * sn
-            vec[..., half:rot] = b0 * cs + a0 * sn
-            return vec.astype(f32)
-
-        q, k = rope(q), rope(k)
-        self.K[i].append(k)
-        self.V[i].append(v)
-        Kc, Vc = np.concatenate(self.K[i]), np.concatenate(self.V[i])     # [pos+T][KV][hd]
-        n = Kc.shape[0]
-        grp = H // KV
-        ctx = np.empty((T, H, hd), f32)
-        scale = f32(1.0) / np.sqrt(f32(hd))
-        for h in range(H):
-            sc = (q[:, h, :] @ Kc[:, h // grp, :].T).astype(f32) * scale        # [T][n]
-            mask = np.arange(n)[None, :] > (self.pos + np.arange(T))[:, None]
-            sc[mask] = -np.inf
-            ctx[:, h, :] = softmax(sc) @ Vc[:, h // grp, :]
-        ctx = ctx.reshape(T, H * hd) * sigmoid(gate)
-        return (ctx @ self.W[p + "o_proj.weight"].T).astype(f32)
+        return gated_attention(x, {n: self.W[p + n + ".weight"] for n in _ATTN_W}, self.K[i], self.V[i],
+                               self.pos, self.H, self.KV, self.hd, self.rot, self.theta, self.eps)
 
     # -- MoE (qwen.c:461-505)
     def moe(self, i, x):

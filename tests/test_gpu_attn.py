@@ -1,0 +1,159 @@
+"""GPU parity of the gated full-attention layer (engines/qwen.c:366-425,
+attn_step) through the C-ABI (omh_attn_forward).
+
+The checker is tests/qwen_tiny.gated_attention, the float32 restatement of
+attn_step that the host model runs; with it the host model reproduces the
+reference's own golden tokens (greedy `full_ids` 20/20, teacher-forced
+`tf_argmax` 28/28, test_e2e_tiny.py), and the closed-form cases in
+test_attn_ref.py pin its parts.  Here the GPU layer must match it:
+  - on the reference tiny model, as the model's attention layers, to the
+    same golden tokens (GDN layers on the GPU as well);
+  - at the Qwen3.6-35B-A3B attention shape (hidden 2048, 16 query heads,
+    2 kv heads, head_dim 256, rot 64) through prompt steps (one key split)
+    and decode steps (up to 47 key splits of 64 keys);
+  - over the other head widths and group sizes the kernels take, int8
+    projections, several sequences, and the argument checks.
+Tolerance: tests/tol.py (max-abs 2e-3 / rel 1e-3)."""
+import numpy as np
+import pytest
+
+from overhang_amd import gdn
+from tests import qwen_tiny as q
+from tests.tol import assert_close
+
+pytestmark = pytest.mark.gpu
+
+_next = [1200]
+
+
+def new_li():
+    _next[0] += 1
+    return _next[0]
+
+
+def _weights(rng, D, H, KV, hd, scale=0.02):
+    return {"W_q": rng.normal(0, scale, (2 * H * hd, D)).astype(np.float32),
+            "W_k": rng.normal(0, scale, (KV * hd, D)).astype(np.float32),
+            "W_v": rng.normal(0, scale, (KV * hd, D)).astype(np.float32),
+            "W_o": rng.normal(0, scale, (D, H * hd)).astype(np.float32),
+            "q_norm": rng.normal(0, 0.1, hd).astype(np.float32),
+            "k_norm": rng.normal(0, 0.1, hd).astype(np.float32)}
+
+
+def _ref_w(w):
+    return {"q_proj": w["W_q"], "k_proj": w["W_k"], "v_proj": w["W_v"], "o_proj": w["W_o"],
+            "q_norm": w["q_norm"], "k_norm": w["k_norm"]}
+
+
+def _dequant(w):
+    """The weights the int8 path computes with: q * s per row (qwen.c:116-121)."""
+    out = dict(w)
+    for nm in ("q", "k", "v", "o"):
+        Q, S = gdn.quantize_rows(w["W_" + nm])
+        out["W_" + nm] = (Q.astype(np.float32) * S[:, None]).astype(np.float32)
+    return out
+
+
+def _run(shape, steps, seed=0, int8=False, max_t=None, x_scale=1.0):
+    """steps: token counts of consecutive calls on sequence 0."""
+    D, H, KV, hd, rot = shape
+    rng = np.random.default_rng(seed)
+    w = _weights(rng, D, H, KV, hd)
+    total = sum(steps)
+    L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, max_t or total, w, int8=int8)
+    rw = _ref_w(_dequant(w) if int8 else w)
+    Kl, Vl = [], []
+    pos = 0
+    try:
+        for T in steps:
+            x = (rng.normal(0, 1, (T, D)) * x_scale).astype(np.float32)
+            got = L.forward(0, pos, x)
+            ref = q.gated_attention(x, rw, Kl, Vl, pos, H, KV, hd, rot, 1e7, 1e-6)
+            assert_close(got, ref, what=f"shape {shape} pos {pos} T {T}")
+            pos += T
+    finally:
+        L.free()
+
+
+Q35B_ATTN = (2048, 16, 2, 256, 64)
+
+
+def test_tiny_greedy_with_gpu_attention_and_gdn():
+    m = q.TinyQwen(q.HipGdn, first_li=960, gpu_attn_li=1100)
+    try:
+        got, exp = q.greedy(m)
+    finally:
+        m.close()
+    assert got == exp, f"greedy {sum(int(a == b) for a, b in zip(got, exp))}/20: {got} vs {exp}"
+
+
+def test_tiny_teacher_forced_with_gpu_attention_prompt_step():
+    """All 28 positions in one forward: each attention layer is one T = 28
+    call, each GDN layer one chunked prefill."""
+    m = q.TinyQwen(q.HipGdn, first_li=980, batched=True, gpu_attn_li=1150)
+    try:
+        got, exp = q.teacher_forced(m)
+    finally:
+        m.close()
+    assert got == exp, f"teacher-forced {sum(int(a == b) for a, b in zip(got, exp))}/28"
+
+
+@pytest.mark.parametrize("steps", [[1, 1, 1], [37, 1, 1], [200, 1, 64, 1]], ids=["decode", "prompt37", "prompt200"])
+def test_35b_shape_prompt_then_decode(steps):
+    _run(Q35B_ATTN, steps)
+
+
+def test_35b_shape_long_context_many_splits():
+    """A 3000-token prompt in one call, then decode steps at n = 3001..3003:
+    47 key splits of 64 keys per kv head."""
+    _run(Q35B_ATTN, [3000, 1, 1, 1], seed=3)
+
+
+@pytest.mark.parametrize("shape", [(256, 8, 8, 32, 32), (128, 4, 1, 64, 16), (512, 16, 1, 128, 128),
+                                   (256, 2, 2, 128, 0), (1024, 4, 4, 256, 256)],
+                         ids=["hd32-grp1", "hd64-grp4", "hd128-grp16", "hd128-norope", "hd256-fullrope"])
+def test_head_widths_and_groups(shape):
+    _run(shape, [70, 1, 5, 1], seed=7)
+
+
+@pytest.mark.parametrize("steps", [[1, 1], [64, 1]], ids=["decode", "prompt64"])
+def test_int8_projections(steps):
+    _run(Q35B_ATTN, steps, seed=11, int8=True)
+
+
+def test_sequences_are_isolated():
+    D, H, KV, hd, rot = 256, 4, 2, 64, 16
+    rng = np.random.default_rng(5)
+    w = _weights(rng, D, H, KV, hd)
+    L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 64, w, max_seqs=3)
+    rw = _ref_w(w)
+    try:
+        caches = {s: ([], []) for s in (0, 2)}
+        pos = {0: 0, 2: 0}
+        for s, T in [(0, 10), (2, 7), (0, 1), (2, 3), (0, 1), (2, 1)]:
+            x = rng.normal(0, 1, (T, D)).astype(np.float32)
+            got = L.forward(s, pos[s], x)
+            ref = q.gated_attention(x, rw, *caches[s], pos[s], H, KV, hd, rot, 1e7, 1e-6)
+            assert_close(got, ref, what=f"seq {s} pos {pos[s]}")
+            pos[s] += T
+    finally:
+        L.free()
+
+
+def test_argument_checks():
+    D, H, KV, hd, rot = 128, 2, 1, 64, 16
+    rng = np.random.default_rng(1)
+    w = _weights(rng, D, H, KV, hd)
+    with pytest.raises(gdn.OmhError) as e:
+        gdn.AttnLayer(new_li(), D, H, KV, 96, rot, 1e7, 1e-6, 8, _weights(rng, D, H, KV, 96))
+    assert e.value.code == gdn.OMH_ERR_SHAPE
+    L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 8, w)
+    try:
+        x = np.zeros((4, D), np.float32)
+        with pytest.raises(gdn.OmhError):
+            L.forward(0, 5, x)                   # positions 5..8 past max_t = 8
+        with pytest.raises(gdn.OmhError):
+            L.forward(1, 0, x)                   # one sequence only
+        assert L.forward(0, 4, x).shape == (4, D)
+    finally:
+        L.free()
