@@ -307,6 +307,56 @@ def bench_block(hip, gdn, synth, B, steps, warmup):
     return res
 
 
+ATTN_SHAPE = (2048, 16, 2, 256, 64)         # hidden, query heads, kv heads, head_dim, rot_dim (35B-A3B)
+
+
+def attn_bytes(n, int8=True):
+    """Compulsory HBM bytes of one decode token of the gated attention layer
+    at n visible positions: the q/k/v and o projection weights (int8 + per-row
+    scales), the K and V cache rows read, x in and out."""
+    D, H, KV, hd, _ = ATTN_SHAPE
+    rows = 2 * H * hd + 2 * KV * hd
+    eb = 1 if int8 else 4
+    w = (rows * D + D * H * hd) * eb + (4 * (rows + D) if int8 else 0)
+    return w + 2 * KV * n * hd * 4 + 2 * D * 4
+
+
+def bench_attn(hip, gdn, n, steps, warmup, nseq=8):
+    """One decode token of the gated full-attention layer (engines/qwen.c:366-425)
+    at the 35B-A3B attention shape with int8 projections, at position n - 1
+    (n visible keys), rotating over nseq sequences' caches (> 1 GiB at
+    n = 32768) so no step finds its cache in the last-level cache.  The
+    caches hold zeros outside the rows the steps write; the kernels' work
+    does not depend on the values."""
+    D, H, KV, hd, rot = ATTN_SHAPE
+    rng = np.random.default_rng(9)
+    w = {"W_q": rng.normal(0, 0.02, (2 * H * hd, D)).astype(np.float32),
+         "W_k": rng.normal(0, 0.02, (KV * hd, D)).astype(np.float32),
+         "W_v": rng.normal(0, 0.02, (KV * hd, D)).astype(np.float32),
+         "W_o": rng.normal(0, 0.02, (D, H * hd)).astype(np.float32),
+         "q_norm": rng.normal(0, 0.1, hd).astype(np.float32),
+         "k_norm": rng.normal(0, 0.1, hd).astype(np.float32)}
+    L = gdn.AttnLayer(4000, D, H, KV, hd, rot, 1e7, 1e-6, n, w, max_seqs=nseq, int8=True)
+    x = hip.Buffer.from_numpy(rng.normal(0, 1, (1, D)).astype(np.float32))
+    out = hip.Buffer(D * 4)
+    st = hip.Stream()
+
+    def one(k):
+        gdn.attn_forward_dev(L.li, k % nseq, n - 1, 1, x, out, stream=st)
+
+    el, durs, _ = time_launches(hip, st, one, steps, warmup)
+    L.free()
+    t = el / steps
+    by = attn_bytes(n)
+    gbs = by / t / 1e9
+    res = {"n": n, "us_per_step": 1e6 * t, "tok_s": 1 / t, "alg_bytes": by, "achieved_GBs": gbs,
+           "frac_hbm": gbs / HBM_PEAK_GBS,
+           "note": "gated full-attention layer, one decode token at n visible positions, hidden 2048, "
+                   "16 query / 2 kv heads of 256, int8 q/k/v/o projections; 5 launches per token"}
+    log(f"attn n={n}: {1e6 * t:.1f} us/step, {gbs:.0f} GB/s ({100 * res['frac_hbm']:.1f}% of HBM peak)")
+    return res
+
+
 def cpu_prefill_baseline(synth, T=256, budget_s=8.0):
     """The oracle prefills token by token (the reference has no chunked CPU
     path): one layer core at the 35B shape over a bounded sample of T tokens."""
@@ -394,9 +444,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=("all", "decode", "prefill", "block"), default="all",
+    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn"), default="all",
                     help="decode: the headline only (for profiling); prefill: the T=4096 and T=32768 "
-                         "prefills only; block: the config 5 int8 block at B=64 only")
+                         "prefills only; block: the config 5 int8 block at B=64 only; attn: the gated "
+                         "attention layer's decode token at 32768 positions only")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN layer needs no collectives and this build "
@@ -410,14 +461,19 @@ def main():
         warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 3, 1)
         print(json.dumps({"prefill": pre, "prefill_T32768_warm": warm}), flush=True)
         return
+    if a.part == "attn":
+        print(json.dumps({"attn_decode_n32768": bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)}),
+              flush=True)
+        return
     if a.part == "block":
         print(json.dumps({"block_int8_B64": bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)}),
               flush=True)
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = warm = block = None
+    pre = warm = block = attn = None
     if a.part == "all":
+        attn = bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
         warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 5, 1)
         block = bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)
@@ -462,6 +518,7 @@ def main():
         "prefill_T4096": pre,
         "prefill_T32768_warm": warm,
         "block_int8_B64": block,
+        "attn_decode_n32768": attn,
         "decode_engine_order": engine,
         "decode_batch_sweep": sweep,
     }

@@ -15,13 +15,14 @@
 //     the query heads of its group (GQA, qwen.c:408-409), keeps a running
 //     max and sum per head (online softmax) and writes unnormalised
 //     partials.  Lane = key for the scores (q broadcast from LDS), lane =
-//     4 output columns for P.V (p broadcast from LDS).
-//  3. attn_combine_kernel, one wave per (token, head): merges the splits,
+//     4 output columns for P.V (each key's weight broadcast by readlane).
+//  3. attn_combine_kernel, per (token, head, 64 columns): merges the splits,
 //     normalises, and applies the output gate sigmoid(gate) (qwen.c:421).
 // The o_proj is a second launch_proj.
 //
 // Decode is HBM-bound on the visible cache: 2 * KV * n * hd * 4 bytes for
-// n = pos + 1 keys; the splits give >= 512 workgroups (two per CU).  Token t
+// n = pos + 1 keys; the splits give >= 256 workgroups (one per CU, as the
+// LDS footprint allows).  Token t
 // sees keys 0 .. pos+t (causal), and the key tiles beyond that are masked.
 #include "omh_internal.h"
 #include "omh_device.h"
@@ -38,8 +39,7 @@ struct AttnShape {
     static constexpr int NG4 = HD / 4;            // float4 groups per row
     static constexpr int R4 = (NG4 + OMH_WAVE - 1) / OMH_WAVE;   // groups per lane in P.V
     static constexpr int NW = 4;                  // waves
-    static constexpr int GP = kAttnMaxGroup / NW; // query heads per wave, at most
-    static constexpr size_t LDS = (size_t)(kAttnMaxGroup * HD + KT * KS + KT * HD + kAttnMaxGroup * KT) * sizeof(float);
+    static constexpr size_t LDS = (size_t)(kAttnMaxGroup * HD + KT * KS + KT * HD) * sizeof(float);
 };
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -113,15 +113,20 @@ __global__ __launch_bounds__(OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
     }
 }
 
-template <int HD>
-__global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) void attn_split_kernel(const AttnArgs a) {
+// GPW = query heads per wave (the group's heads grp spread over the NW
+// waves: head wave + NW*i).  The hot loops carry no per-head conditions (a
+// branch there serialises every LDS read behind its own wait): a wave
+// whose head index runs past grp computes a copy of head grp-1 and does not
+// write it.
+template <int HD, int GPW>
+__global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all of each SIMD's registers
     using S = AttnShape<HD>;
-    constexpr int GP = S::GP, R4 = S::R4, NG4 = S::NG4, KT = S::KT, NT = S::NW * OMH_WAVE;
+    constexpr int R4 = S::R4, NG4 = S::NG4, KT = S::KT, NW = S::NW, NT = NW * OMH_WAVE;
     extern __shared__ float smem[];
     float *qs = smem;                              // [group heads][HD]
     float *Ks = qs + kAttnMaxGroup * HD;           // [KT][KS]
     float *Vs = Ks + KT * S::KS;                   // [KT][HD]
-    float *ps = Vs + KT * HD;                      // [group heads][KT]
 
     const int H = a.H, KV = a.KV, grp = H / KV, ns = a.ns;
     const int s = blockIdx.x % ns, g = (blockIdx.x / ns) % KV, t = blockIdx.x / (ns * KV);
@@ -143,10 +148,13 @@ __global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) void attn_split_kerne
         *reinterpret_cast<float4 *>(qs + i * HD + 4 * c) =
             *reinterpret_cast<const float4 *>(a.qb + ((size_t)t * H + (size_t)g * grp + i) * HD + 4 * c);
     }
-    float m[GP], l[GP];
-    float4 o[GP][R4];
+    const float *qh[GPW];                          // this wave's heads' q rows in LDS
 #pragma unroll
-    for (int i = 0; i < GP; i++) {
+    for (int i = 0; i < GPW; i++) qh[i] = qs + min(wave + NW * i, grp - 1) * HD;
+    float m[GPW], l[GPW];
+    float4 o[GPW][R4];
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
         m[i] = -INFINITY;
         l[i] = 0.f;
 #pragma unroll
@@ -155,79 +163,89 @@ __global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) void attn_split_kerne
     const size_t cache0 = ((size_t)a.seq * KV + g) * a.max_t;
     const float *Kg = a.Kc + cache0 * HD, *Vg = a.Vc + cache0 * HD;
 
+    // K and V tiles go HBM -> registers -> LDS: every thread's PER pieces of
+    // a tile are in flight at once, and the next tile's loads are issued as
+    // soon as the current one is in LDS, so they overlap its compute.  Rows
+    // past the split's end repeat the tile's first row, so every LDS row
+    // holds finite values (their weights are zero).
+    constexpr int PER = KT * NG4 / NT;
+    static_assert(KT * NG4 % NT == 0, "tile pieces per thread");
+    omh_v4f kr[PER], vr[PER];                      // native vectors: HIP's float4 copies stay in scratch
+#define OMH_ATTN_LOAD_TILE(KT0, NK)                                                       \
+    _Pragma("unroll") for (int i = 0; i < PER; i++) {                                     \
+        const int e = tid + NT * i, kk = e / NG4, c = e % NG4;                            \
+        const size_t off = (size_t)((KT0) + (kk < (NK) ? kk : 0)) * HD + 4 * c;           \
+        kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + off);                             \
+        vr[i] = *reinterpret_cast<const omh_v4f *>(Vg + off);                             \
+    }
+    OMH_ATTN_LOAD_TILE(k0, min(KT, k1 - k0))
     for (int kt = k0; kt < k1; kt += KT) {
         const int nk = min(KT, k1 - kt);
         omh_lds_barrier();                         // the previous tile's readers are done
-        for (int e = tid; e < nk * NG4; e += NT) {
-            const int kk = e / NG4, c = e % NG4;
-            const float4 kv = *reinterpret_cast<const float4 *>(Kg + (size_t)(kt + kk) * HD + 4 * c);
-            const float4 vv = *reinterpret_cast<const float4 *>(Vg + (size_t)(kt + kk) * HD + 4 * c);
-            *reinterpret_cast<float4 *>(Ks + kk * S::KS + 4 * c) = kv;
-            *reinterpret_cast<float4 *>(Vs + kk * HD + 4 * c) = vv;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = tid + NT * i, kk = e / NG4, c = e % NG4;
+            *reinterpret_cast<omh_v4f *>(Ks + kk * S::KS + 4 * c) = kr[i];
+            *reinterpret_cast<omh_v4f *>(Vs + kk * HD + 4 * c) = vr[i];
         }
         omh_lds_barrier();
+        if (kt + KT < k1) {
+            OMH_ATTN_LOAD_TILE(kt + KT, min(KT, k1 - kt - KT))
+        }
 
         // scores q.k * hd^-1/2 (qwen.c:410-414), lane = key
         const bool valid = lane < nk;
-        const float *kr = Ks + (valid ? lane : 0) * S::KS;
-        float acc[GP];
+        const float *kr_l = Ks + lane * S::KS;
+        float acc[GPW], pl[GPW];
 #pragma unroll
-        for (int i = 0; i < GP; i++) acc[i] = 0.f;
-#pragma unroll 4
+        for (int i = 0; i < GPW; i++) acc[i] = 0.f;
+#pragma unroll 8
         for (int c = 0; c < NG4; c++) {
-            const float4 kv = *reinterpret_cast<const float4 *>(kr + 4 * c);
+            const float4 kv = *reinterpret_cast<const float4 *>(kr_l + 4 * c);
 #pragma unroll
-            for (int i = 0; i < GP; i++) {
-                const int h = wave + S::NW * i;
-                if (h < grp) {
-                    const float4 q = *reinterpret_cast<const float4 *>(qs + h * HD + 4 * c);
-                    acc[i] = fmaf(q.x, kv.x, acc[i]);
-                    acc[i] = fmaf(q.y, kv.y, acc[i]);
-                    acc[i] = fmaf(q.z, kv.z, acc[i]);
-                    acc[i] = fmaf(q.w, kv.w, acc[i]);
-                }
+            for (int i = 0; i < GPW; i++) {
+                const float4 q = *reinterpret_cast<const float4 *>(qh[i] + 4 * c);
+                acc[i] = fmaf(q.x, kv.x, acc[i]);
+                acc[i] = fmaf(q.y, kv.y, acc[i]);
+                acc[i] = fmaf(q.z, kv.z, acc[i]);
+                acc[i] = fmaf(q.w, kv.w, acc[i]);
             }
         }
         // online softmax (qwen.c:413 softmax_ over all keys, merged per tile)
 #pragma unroll
-        for (int i = 0; i < GP; i++) {
-            const int h = wave + S::NW * i;
-            if (h < grp) {
-                const float sc = valid ? acc[i] * a.scale : -INFINITY;
-                const float mn = fmaxf(m[i], wave_max(sc));
-                const float corr = expf(m[i] - mn);
-                const float pe = valid ? expf(sc - mn) : 0.f;
-                l[i] = l[i] * corr + omh_xor_sum_from<1>(pe);
+        for (int i = 0; i < GPW; i++) {
+            const float sc = valid ? acc[i] * a.scale : -INFINITY;
+            const float mn = fmaxf(m[i], wave_max(sc));
+            const float corr = expf(m[i] - mn);
+            const float pe = valid ? expf(sc - mn) : 0.f;
+            l[i] = l[i] * corr + omh_xor_sum_from<1>(pe);
 #pragma unroll
-                for (int r = 0; r < R4; r++) o[i][r] = f4_scale(o[i][r], corr);
-                ps[h * KT + lane] = pe;
-                m[i] = mn;
-            }
+            for (int r = 0; r < R4; r++) o[i][r] = f4_scale(o[i][r], corr);
+            pl[i] = pe;
+            m[i] = mn;
         }
-        // ps rows are written and read by the same wave
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // P.V (qwen.c:415-419), lane = 4 columns
-        for (int kk = 0; kk < nk; kk++) {
+        // P.V (qwen.c:415-419), lane = 4 columns; the weight of key kk is
+        // lane kk's pl (zero past nk), broadcast by readlane
+#pragma unroll 8
+        for (int kk = 0; kk < KT; kk++) {
+            float4 vv[R4];
 #pragma unroll
-            for (int i = 0; i < GP; i++) {
-                const int h = wave + S::NW * i;
-                if (h < grp) {
-                    const float pv = ps[h * KT + kk];
+            for (int r = 0; r < R4; r++) {
+                const int c = min(lane + OMH_WAVE * r, NG4 - 1);
+                vv[r] = *reinterpret_cast<const float4 *>(Vs + kk * HD + 4 * c);
+            }
 #pragma unroll
-                    for (int r = 0; r < R4; r++) {
-                        const int c = lane + OMH_WAVE * r;
-                        if (c < NG4) o[i][r] = f4_fma(*reinterpret_cast<const float4 *>(Vs + kk * HD + 4 * c), pv, o[i][r]);
-                    }
-                }
+            for (int i = 0; i < GPW; i++) {
+                const float pv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pl[i]), kk));
+#pragma unroll
+                for (int r = 0; r < R4; r++) o[i][r] = f4_fma(vv[r], pv, o[i][r]);
             }
         }
     }
 #pragma unroll
-    for (int i = 0; i < GP; i++) {
-        const int h = wave + S::NW * i;
+    for (int i = 0; i < GPW; i++) {
+        const int h = wave + NW * i;
         if (h < grp) {
             const size_t pi = pb + (size_t)h * ns;
 #pragma unroll
@@ -242,48 +260,66 @@ __global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) void attn_split_kerne
         }
     }
 }
+#undef OMH_ATTN_LOAD_TILE
 
+// One workgroup per (token, head, 64 columns): the four waves take every
+// fourth split, lane = column, then sum through LDS.
 template <int HD>
-__global__ __launch_bounds__(OMH_WAVE) void attn_combine_kernel(const AttnArgs a) {
-    constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
-    const int th = blockIdx.x, t = th / a.H, h = th % a.H, lane = threadIdx.x, ns = a.ns;
+__global__ __launch_bounds__(4 * OMH_WAVE) void attn_combine_kernel(const AttnArgs a) {
+    constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;     // column blocks per head
+    __shared__ float so[4][OMH_WAVE], sl[4];
+    const int th = blockIdx.x / NCB, cb = blockIdx.x % NCB;
+    const int t = th / a.H, h = th % a.H, ns = a.ns;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int j = cb * OMH_WAVE + lane;
     const size_t pb = (size_t)th * ns;
     float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, a.pml[2 * (pb + s)]);
-    float L = 0.f, o[NE];
-#pragma unroll
-    for (int i = 0; i < NE; i++) o[i] = 0.f;
-    for (int s = 0; s < ns; s++) {
+    for (int s = lane; s < ns; s += OMH_WAVE) M = fmaxf(M, a.pml[2 * (pb + s)]);
+    M = wave_max(M);
+    float L = 0.f, o = 0.f;
+#pragma unroll 4
+    for (int s = wave; s < ns; s += 4) {
         const float ms = a.pml[2 * (pb + s)];
-        if (ms == -INFINITY) continue;             // empty split, partial never written
-        const float wgt = expf(ms - M);
-        L = fmaf(a.pml[2 * (pb + s) + 1], wgt, L);
-#pragma unroll
-        for (int i = 0; i < NE; i++) {
-            const int j = lane + OMH_WAVE * i;
-            if (j < HD) o[i] = fmaf(a.po[(pb + s) * HD + j], wgt, o[i]);
+        if (ms != -INFINITY) {                     // an empty split's partial is never written
+            const float wgt = expf(ms - M);
+            L = fmaf(a.pml[2 * (pb + s) + 1], wgt, L);
+            if (j < HD) o = fmaf(a.po[(pb + s) * HD + j], wgt, o);
         }
     }
-    const float rl = 1.f / L;                      // split 0 always holds key 0: L > 0
-    const float *gate = a.qkv + (size_t)t * a.ld_qkv + (size_t)h * 2 * HD + HD;
-    float *dst = a.ctx + ((size_t)t * a.H + h) * HD;
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int j = lane + OMH_WAVE * i;
-        if (j < HD) dst[j] = o[i] * rl * omh_sigmoid(gate[j]);
+    so[wave][lane] = o;
+    if (lane == 0) sl[wave] = L;
+    __syncthreads();
+    if (wave == 0 && j < HD) {
+        const float ls = (sl[0] + sl[1]) + (sl[2] + sl[3]);   // split 0 always holds key 0: ls > 0
+        const float os = (so[0][lane] + so[1][lane]) + (so[2][lane] + so[3][lane]);
+        const float g = a.qkv[(size_t)t * a.ld_qkv + (size_t)h * 2 * HD + HD + j];
+        a.ctx[((size_t)t * a.H + h) * HD + j] = os / ls * omh_sigmoid(g);
     }
 }
 
 template <int HD>
 hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
-    static const bool lds_ok = hipFuncSetAttribute((const void *)attn_split_kernel<HD>,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   (int)AttnShape<HD>::LDS) == hipSuccess;
+    static const bool lds_ok = [] {
+        bool ok = true;
+        for (const void *f : {(const void *)attn_split_kernel<HD, 1>, (const void *)attn_split_kernel<HD, 2>,
+                              (const void *)attn_split_kernel<HD, 3>, (const void *)attn_split_kernel<HD, 4>})
+            ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)AttnShape<HD>::LDS) == hipSuccess;
+        return ok;
+    }();
     if (!lds_ok) return hipErrorInvalidValue;
+    static_assert(kAttnMaxGroup <= 4 * AttnShape<HD>::NW, "heads per wave");
     hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
-    hipLaunchKernelGGL((attn_split_kernel<HD>), dim3((unsigned)(a.ns * a.KV * a.T)),
-                       dim3(AttnShape<HD>::NW * OMH_WAVE), AttnShape<HD>::LDS, st, a);
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)(a.T * a.H)), dim3(OMH_WAVE), 0, st, a);
+    const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(AttnShape<HD>::NW * OMH_WAVE);
+    const size_t lds = AttnShape<HD>::LDS;
+    switch ((a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, blk, lds, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, blk, lds, st, a); break;
+    case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3>), grid, blk, lds, st, a); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
+    }
+    constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)(a.T * a.H * NCB)), dim3(4 * OMH_WAVE), 0, st, a);
     return hipGetLastError();
 }
 
@@ -297,7 +333,7 @@ bool attn_supported(int hd, int H, int KV, int rot) {
 void attn_plan(int pos, int T, int KV, int &ns, int &kps) {
     const long nmax = (long)pos + T;                       // keys the last token sees
     const long per = (long)KV * T;
-    const long want = per >= 512 ? 1 : (512 + per - 1) / per;   // splits for >= 512 workgroups
+    const long want = per >= 256 ? 1 : (256 + per - 1) / per;   // splits for >= 256 workgroups (one per CU)
     long k = (nmax + want - 1) / want;
     k = (k + 63) / 64 * 64;
     kps = (int)k;
