@@ -137,9 +137,13 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
     // partial of query head g*grp + i: index pb + i*ns
     const size_t pb = ((size_t)t * H + (size_t)g * grp) * ns + s;
     if (k0 >= k1) {                                // an empty split: weight zero in the merge
-        if (tid < grp) {
-            a.pml[2 * (pb + (size_t)tid * ns)] = -INFINITY;
-            a.pml[2 * (pb + (size_t)tid * ns) + 1] = 0.f;
+        for (int e = tid; e < grp * NG4; e += NT) {
+            const size_t pi = pb + (size_t)(e / NG4) * ns;
+            *reinterpret_cast<float4 *>(a.po + pi * HD + 4 * (e % NG4)) = f4_zero();
+            if (e % NG4 == 0) {
+                a.pml[2 * pi] = -INFINITY;
+                a.pml[2 * pi + 1] = 0.f;
+            }
         }
         return;
     }
@@ -171,14 +175,15 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
     constexpr int PER = KT * NG4 / NT;
     static_assert(KT * NG4 % NT == 0, "tile pieces per thread");
     omh_v4f kr[PER], vr[PER];                      // native vectors: HIP's float4 copies stay in scratch
-#define OMH_ATTN_LOAD_TILE(KT0, NK)                                                       \
-    _Pragma("unroll") for (int i = 0; i < PER; i++) {                                     \
-        const int e = tid + NT * i, kk = e / NG4, c = e % NG4;                            \
+#define OMH_ATTN_LOAD_PIECE(I, KT0, NK)                                                   \
+    {                                                                                     \
+        const int e = tid + NT * (I), kk = e / NG4, c = e % NG4;                          \
         const size_t off = (size_t)((KT0) + (kk < (NK) ? kk : 0)) * HD + 4 * c;           \
-        kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + off);                             \
-        vr[i] = *reinterpret_cast<const omh_v4f *>(Vg + off);                             \
+        kr[I] = *reinterpret_cast<const omh_v4f *>(Kg + off);                             \
+        vr[I] = *reinterpret_cast<const omh_v4f *>(Vg + off);                             \
     }
-    OMH_ATTN_LOAD_TILE(k0, min(KT, k1 - k0))
+#pragma unroll
+    for (int i = 0; i < PER; i++) OMH_ATTN_LOAD_PIECE(i, k0, min(KT, k1 - k0))
     for (int kt = k0; kt < k1; kt += KT) {
         const int nk = min(KT, k1 - kt);
         omh_lds_barrier();                         // the previous tile's readers are done
@@ -189,9 +194,10 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
             *reinterpret_cast<omh_v4f *>(Vs + kk * HD + 4 * c) = vr[i];
         }
         omh_lds_barrier();
-        if (kt + KT < k1) {
-            OMH_ATTN_LOAD_TILE(kt + KT, min(KT, k1 - kt - KT))
-        }
+        // the next tile's pieces are issued spread over the score blocks
+        // below; after the last tile they re-read this one (cache hits)
+        const bool more = kt + KT < k1;
+        const int kn = more ? kt + KT : kt, nkn = more ? min(KT, k1 - kt - KT) : nk;
 
         // scores q.k * hd^-1/2 (qwen.c:410-414), lane = key
         const bool valid = lane < nk;
@@ -199,16 +205,25 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
         float acc[GPW], pl[GPW];
 #pragma unroll
         for (int i = 0; i < GPW; i++) acc[i] = 0.f;
-#pragma unroll 8
-        for (int c = 0; c < NG4; c++) {
-            const float4 kv = *reinterpret_cast<const float4 *>(kr_l + 4 * c);
+        constexpr int CB = 8, NB = NG4 / CB, PPB = (PER + NB - 1) / NB;
+        static_assert(NG4 % CB == 0, "score blocks");
 #pragma unroll
-            for (int i = 0; i < GPW; i++) {
-                const float4 q = *reinterpret_cast<const float4 *>(qh[i] + 4 * c);
-                acc[i] = fmaf(q.x, kv.x, acc[i]);
-                acc[i] = fmaf(q.y, kv.y, acc[i]);
-                acc[i] = fmaf(q.z, kv.z, acc[i]);
-                acc[i] = fmaf(q.w, kv.w, acc[i]);
+        for (int b = 0; b < NB; b++) {
+#pragma unroll
+            for (int u = 0; u < PPB; u++)
+                if (b * PPB + u < PER) OMH_ATTN_LOAD_PIECE(b * PPB + u, kn, nkn)
+#pragma unroll
+            for (int cc = 0; cc < CB; cc++) {
+                const int c = b * CB + cc;
+                const float4 kv = *reinterpret_cast<const float4 *>(kr_l + 4 * c);
+#pragma unroll
+                for (int i = 0; i < GPW; i++) {
+                    const float4 q = *reinterpret_cast<const float4 *>(qh[i] + 4 * c);
+                    acc[i] = fmaf(q.x, kv.x, acc[i]);
+                    acc[i] = fmaf(q.y, kv.y, acc[i]);
+                    acc[i] = fmaf(q.z, kv.z, acc[i]);
+                    acc[i] = fmaf(q.w, kv.w, acc[i]);
+                }
             }
         }
         // online softmax (qwen.c:413 softmax_ over all keys, merged per tile)
@@ -260,7 +275,7 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
         }
     }
 }
-#undef OMH_ATTN_LOAD_TILE
+#undef OMH_ATTN_LOAD_PIECE
 
 // One workgroup per (token, head, 64 columns): the four waves take every
 // fourth split, lane = column, then sum through LDS.
@@ -278,14 +293,12 @@ __global__ __launch_bounds__(4 * OMH_WAVE) void attn_combine_kernel(const AttnAr
     for (int s = lane; s < ns; s += OMH_WAVE) M = fmaxf(M, a.pml[2 * (pb + s)]);
     M = wave_max(M);
     float L = 0.f, o = 0.f;
-#pragma unroll 4
-    for (int s = wave; s < ns; s += 4) {
-        const float ms = a.pml[2 * (pb + s)];
-        if (ms != -INFINITY) {                     // an empty split's partial is never written
-            const float wgt = expf(ms - M);
-            L = fmaf(a.pml[2 * (pb + s) + 1], wgt, L);
-            if (j < HD) o = fmaf(a.po[(pb + s) * HD + j], wgt, o);
-        }
+    const int jc = j < HD ? j : HD - 1;
+#pragma unroll 8
+    for (int s = wave; s < ns; s += 4) {           // an empty split: m = -inf, weight 0, zero partial
+        const float wgt = expf(a.pml[2 * (pb + s)] - M);
+        L = fmaf(a.pml[2 * (pb + s) + 1], wgt, L);
+        o = fmaf(a.po[(pb + s) * HD + jc], wgt, o);
     }
     so[wave][lane] = o;
     if (lane == 0) sl[wave] = L;
