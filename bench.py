@@ -357,6 +357,35 @@ def bench_attn(hip, gdn, n, steps, warmup, nseq=8):
     return res
 
 
+def bench_snapshot(hip, gdn, synth, steps, warmup):
+    """Speculative-decoding snapshot of one sequence's GDN state across the
+    30 GDN layers of the 35B shape copied device to device into a spare
+    sequence slot, one omh_gdn_state_copy_dev call (one launch)."""
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = synth.layer_weights(d, 0, projections=False)
+    lays = [gdn.GdnLayer(3500 + i, d, w, max_seqs=2) for i in range(N_LAYERS)]
+    st = hip.Stream()
+
+    lis = [L.li for L in lays]
+
+    def one(k):
+        gdn.state_copy_dev(lis, 0, 1, stream=st)
+
+    el, _, _ = time_launches(hip, st, one, steps, warmup)
+    for L in lays:
+        L.free()
+    t = el / steps
+    per_layer = d.state_bytes + 4 * d.conv_dim * 4 + 4              # S, the conv ring, the phase
+    by = 2 * N_LAYERS * per_layer                                   # read + write
+    gbs = by / t / 1e9
+    res = {"us_per_snapshot": 1e6 * t, "bytes": by, "achieved_GBs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
+           "note": "one sequence's state across 30 GDN layers (35B shape) copied device to device into a "
+                   "spare slot: the snapshot (or rollback) of a speculative-decoding step"}
+    log(f"state snapshot x {N_LAYERS} layers: {1e6 * t:.1f} us, {gbs:.0f} GB/s")
+    return res
+
+
 def cpu_prefill_baseline(synth, T=256, budget_s=8.0):
     """The oracle prefills token by token (the reference has no chunked CPU
     path): one layer core at the 35B shape over a bounded sample of T tokens."""
@@ -471,9 +500,10 @@ def main():
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = warm = block = attn = None
+    pre = warm = block = attn = snap = None
     if a.part == "all":
         attn = bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)
+        snap = bench_snapshot(hip, gdn, synth, max(a.steps // 2, 10), a.warmup)
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
         warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 5, 1)
         block = bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)
@@ -519,6 +549,7 @@ def main():
         "prefill_T32768_warm": warm,
         "block_int8_B64": block,
         "attn_decode_n32768": attn,
+        "gdn_state_snapshot_30layers": snap,
         "decode_engine_order": engine,
         "decode_batch_sweep": sweep,
     }

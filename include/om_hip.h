@@ -100,6 +100,18 @@ int omh_gdn_decode(int li, int B, const float *x, float *out);
  * the engine prefills token by token (engines/qwen.c:588, 637). */
 int omh_gdn_prefill(int li, int seq, int T, const float *x, float *out);
 
+/* Device-side snapshot / rollback for speculative decoding: for each of
+ * the nl layers lis[] (all of one shape), copy sequence src_seq's whole GDN
+ * state (recurrent state, conv history and its ring position) over sequence
+ * dst_seq's, device to device, in one launch.  Snapshot = copy into a spare
+ * sequence slot before the speculative tokens; rollback = copy it back after
+ * a rejection.  The reference has no counterpart: its worklog records
+ * rollback as infeasible for the deltanet state as implemented
+ * (WORKLOG.md:157-158), and multi-token prediction is on its roadmap
+ * (ROADMAP.md:10).  The _dev variant enqueues on `stream`. */
+int omh_gdn_state_copy(int nl, const int *lis, int src_seq, int dst_seq);
+int omh_gdn_state_copy_dev(int nl, const int *lis, int src_seq, int dst_seq, void *stream);
+
 /* Core only (no projections): pre-projected mixed_qkv[B][conv_dim],
  * z[B][vh*vd], a[B][vh], b[B][vh] -> core[B][vh*vd], the gated-normed head
  * outputs that out_proj consumes (engines/qwen.c:307-358). */

@@ -543,6 +543,48 @@ int omh_gdn_state_set(int li, int seq, const float *conv, const float *S) {
     return OMH_OK;
 }
 
+int omh_gdn_state_copy_dev(int nl, const int *lis, int src_seq, int dst_seq, void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "state_copy: nl=%d", nl);
+    for (int i = 0; i < nl; i++) {
+        if (int rc = check_layer(lis[i])) return rc;
+        const DevLayer &L = g_L[lis[i]];
+        if (src_seq < 0 || src_seq >= L.max_seqs || dst_seq < 0 || dst_seq >= L.max_seqs)
+            return fail(OMH_ERR_ARG, "state_copy: sequences %d -> %d outside [0, %d) for layer %d", src_seq, dst_seq,
+                        L.max_seqs, lis[i]);
+        if (L.d.kh != g_L[lis[0]].d.kh || L.d.vh != g_L[lis[0]].d.vh || L.d.kd != g_L[lis[0]].d.kd ||
+            L.d.vd != g_L[lis[0]].d.vd || L.conv_dim != g_L[lis[0]].conv_dim)
+            return fail(OMH_ERR_ARG, "state_copy: layers %d and %d differ in shape", lis[0], lis[i]);
+    }
+    if (src_seq == dst_seq) return OMH_OK;
+    const DevLayer &L0 = g_L[lis[0]];
+    if ((L0.d.vh * L0.d.kd * L0.d.vd) % 4 != 0)
+        return fail(OMH_ERR_SHAPE, "state_copy: vh*kd*vd = %d is not a multiple of 4", L0.d.vh * L0.d.kd * L0.d.vd);
+    StateCopyArgs c{};
+    c.n4 = (size_t)L0.d.vh * L0.d.kd * L0.d.vd / 4;
+    c.r4 = (size_t)L0.conv_dim * kConvRing / 4;
+    for (int l0 = 0; l0 < nl; l0 += kMaxDecodeLayers) {
+        c.nl = nl - l0 < kMaxDecodeLayers ? nl - l0 : kMaxDecodeLayers;
+        for (int j = 0; j < c.nl; j++) {
+            const DevLayer &L = g_L[lis[l0 + j]];
+            c.S_src[j] = L.S + (size_t)src_seq * c.n4 * 4;
+            c.S_dst[j] = L.S + (size_t)dst_seq * c.n4 * 4;
+            c.R_src[j] = L.conv_st + (size_t)src_seq * c.r4 * 4;
+            c.R_dst[j] = L.conv_st + (size_t)dst_seq * c.r4 * 4;
+            c.P_src[j] = L.phase + (size_t)L.epoch * L.max_seqs + src_seq;
+            c.P_dst[j] = L.phase + (size_t)L.epoch * L.max_seqs + dst_seq;
+        }
+        HIP_OK(launch_state_copy(c, static_cast<hipStream_t>(stream)));
+    }
+    return OMH_OK;
+}
+
+int omh_gdn_state_copy(int nl, const int *lis, int src_seq, int dst_seq) {
+    if (int rc = omh_gdn_state_copy_dev(nl, lis, src_seq, dst_seq, g_stream)) return rc;
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
+}
+
 int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
                             const float *a, const float *b, float *core, void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;

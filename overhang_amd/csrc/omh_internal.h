@@ -138,6 +138,18 @@ void prefill_bind_scratch(PrefillArgs &a, int D, void *base);
 bool prefill_supported(int kd, int vd, int rep, int K);
 hipError_t launch_prefill_core(const PrefillArgs &a, int D, hipStream_t st);
 
+// Copy of one sequence's whole state (S block, conv ring, ring phase of the
+// epoch the next launch reads) over another's, for nl layers of one shape.
+struct StateCopyArgs {
+    const float *S_src[kMaxDecodeLayers], *R_src[kMaxDecodeLayers];
+    float *S_dst[kMaxDecodeLayers], *R_dst[kMaxDecodeLayers];
+    const int *P_src[kMaxDecodeLayers];
+    int *P_dst[kMaxDecodeLayers];
+    size_t n4, r4;                     // float4s of S and of the ring per sequence
+    int nl;
+};
+hipError_t launch_state_copy(const StateCopyArgs &c, hipStream_t st);
+
 // Gated full attention (engines/qwen.c:366-425) for T tokens of sequence
 // seq at positions pos .. pos+T-1, after the qkv projection.
 constexpr int kAttnMaxGroup = 16;     // query heads per kv head

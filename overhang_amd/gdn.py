@@ -28,6 +28,7 @@ EXPORTS = (
     "omh_gdn_decode_core_dev", "omh_gdn_prefill_core_dev", "omh_gdn_decode_dev",
     "omh_gdn_prefill_dev", "omh_sync",
     "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
+    "omh_gdn_state_copy", "omh_gdn_state_copy_dev",
 )
 
 
@@ -90,6 +91,8 @@ def lib() -> C.CDLL:
         L.omh_gdn_decode_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_gdn_prefill_dev.argtypes = [i, i, i, vp, vp, vp]
         L.omh_sync.argtypes = [vp]
+        L.omh_gdn_state_copy.argtypes = [i, C.POINTER(C.c_int), i, i]
+        L.omh_gdn_state_copy_dev.argtypes = [i, C.POINTER(C.c_int), i, i, vp]
         L.omh_attn_layer_init.argtypes = [i, C.POINTER(_AttnDims), C.POINTER(_AttnWeights), i]
         L.omh_attn_layer_free.argtypes = [i]
         L.omh_attn_forward.argtypes = [i, i, i, i, vp, vp]
@@ -183,6 +186,11 @@ class GdnLayer:
         check(lib().omh_gdn_state_set(self.li, seq, _ptr(conv), _ptr(S)))
 
     # ---- host-pointer entry points ----
+    def copy_state(self, src_seq: int, dst_seq: int) -> None:
+        """Device-side copy of one sequence's whole state over another's
+        (snapshot before speculative tokens, rollback after a rejection)."""
+        state_copy([self.li], src_seq, dst_seq)
+
     def decode(self, x: np.ndarray) -> np.ndarray:
         x = _f32(x)
         B = x.shape[0]
@@ -280,3 +288,14 @@ class AttnLayer:
 
 def attn_forward_dev(li: int, seq: int, pos: int, T: int, x, out, stream=None) -> None:
     check(lib().omh_attn_forward_dev(li, seq, pos, T, _ptr(x), _ptr(out), _stream(stream)))
+
+
+def state_copy(lis, src_seq: int, dst_seq: int) -> None:
+    """Snapshot / rollback of one sequence's state across layers lis (one launch)."""
+    arr = (C.c_int * len(lis))(*lis)
+    check(lib().omh_gdn_state_copy(len(lis), arr, src_seq, dst_seq))
+
+
+def state_copy_dev(lis, src_seq: int, dst_seq: int, stream=None) -> None:
+    arr = (C.c_int * len(lis))(*lis)
+    check(lib().omh_gdn_state_copy_dev(len(lis), arr, src_seq, dst_seq, _stream(stream)))
