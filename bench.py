@@ -360,17 +360,19 @@ def bench_attn(hip, gdn, n, steps, warmup, nseq=8):
 def bench_snapshot(hip, gdn, synth, steps, warmup):
     """Speculative-decoding snapshot of one sequence's GDN state across the
     30 GDN layers of the 35B shape copied device to device into a spare
-    sequence slot, one omh_gdn_state_copy_dev call (one launch)."""
+    sequence slot, one omh_gdn_state_copy_dev call (one launch), rotating
+    over 4 groups of 30 layers so no step finds its state in the
+    last-level cache."""
     from overhang_amd.dims import Q35B
     d = Q35B
     w = synth.layer_weights(d, 0, projections=False)
-    lays = [gdn.GdnLayer(3500 + i, d, w, max_seqs=2) for i in range(N_LAYERS)]
+    R = 4                                  # layer groups rotated: 536 MB, beyond the last-level cache
+    lays = [gdn.GdnLayer(3500 + i, d, w, max_seqs=2) for i in range(R * N_LAYERS)]
     st = hip.Stream()
-
-    lis = [L.li for L in lays]
+    groups = [[L.li for L in lays[r * N_LAYERS:(r + 1) * N_LAYERS]] for r in range(R)]
 
     def one(k):
-        gdn.state_copy_dev(lis, 0, 1, stream=st)
+        gdn.state_copy_dev(groups[k % R], 0, 1, stream=st)
 
     el, _, _ = time_launches(hip, st, one, steps, warmup)
     for L in lays:

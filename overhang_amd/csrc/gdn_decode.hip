@@ -646,26 +646,21 @@ hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, 
     return hipErrorInvalidValue;
 }
 
-// State snapshot / rollback: blockIdx.y = layer, a grid-stride float4 copy
-// of the S block and the conv ring (HBM-bound, 2 x 2.2 MB per layer at the
+// State snapshot / rollback: blockIdx.y = layer, one float4 of the S block
+// and of the conv ring per thread (HBM-bound, 2 x 2.2 MB per layer at the
 // 35B shape), and the ring phase by the first thread.
 __global__ __launch_bounds__(256) void state_copy_kernel(const StateCopyArgs c) {
     const int l = blockIdx.y;
-    const size_t stride = (size_t)gridDim.x * 256, i0 = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const float4 *s = reinterpret_cast<const float4 *>(c.S_src[l]);
-    float4 *d = reinterpret_cast<float4 *>(c.S_dst[l]);
-    for (size_t i = i0; i < c.n4; i += stride) d[i] = s[i];
-    const float4 *rs = reinterpret_cast<const float4 *>(c.R_src[l]);
-    float4 *rd = reinterpret_cast<float4 *>(c.R_dst[l]);
-    for (size_t i = i0; i < c.r4; i += stride) rd[i] = rs[i];
-    if (i0 == 0) *c.P_dst[l] = *c.P_src[l];
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;   // one float4 of S and of the ring
+    if (i < c.n4) reinterpret_cast<float4 *>(c.S_dst[l])[i] = reinterpret_cast<const float4 *>(c.S_src[l])[i];
+    if (i < c.r4) reinterpret_cast<float4 *>(c.R_dst[l])[i] = reinterpret_cast<const float4 *>(c.R_src[l])[i];
+    if (i == 0) *c.P_dst[l] = *c.P_src[l];
 }
 
 hipError_t launch_state_copy(const StateCopyArgs &c, hipStream_t st) {
     if (c.nl < 1 || c.nl > kMaxDecodeLayers) return hipErrorInvalidValue;
-    // about 2 KiB of each layer's state per thread block
     const size_t per = c.n4 > c.r4 ? c.n4 : c.r4;
-    const unsigned gx = (unsigned)((per + 2047) / 2048 < 1 ? 1 : (per + 2047) / 2048);
+    const unsigned gx = (unsigned)((per + 255) / 256);
     hipLaunchKernelGGL(state_copy_kernel, dim3(gx, (unsigned)c.nl), dim3(256), 0, st, c);
     return hipGetLastError();
 }

@@ -157,3 +157,27 @@ def test_argument_checks():
         assert L.forward(0, 4, x).shape == (4, D)
     finally:
         L.free()
+
+
+def test_device_pointer_entry_matches_host_entry():
+    """omh_attn_forward_dev on a library-external stream: the same results as
+    the host entry point, bit for bit, over a prompt and decode steps."""
+    from overhang_amd import hip
+    D, H, KV, hd, rot = Q35B_ATTN
+    rng = np.random.default_rng(21)
+    w = _weights(rng, D, H, KV, hd)
+    A = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 128, w)
+    B = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 128, w)
+    st = hip.Stream()
+    try:
+        pos = 0
+        for T in (33, 1, 1):
+            x = rng.normal(0, 1, (T, D)).astype(np.float32)
+            xd, od = hip.Buffer.from_numpy(x), hip.Buffer(T * D * 4)
+            gdn.attn_forward_dev(A.li, 0, pos, T, xd, od, stream=st)
+            st.synchronize()
+            np.testing.assert_array_equal(od.numpy((T, D)), B.forward(0, pos, x))
+            pos += T
+    finally:
+        A.free()
+        B.free()

@@ -77,3 +77,27 @@ def test_copy_argument_checks():
         L.copy_state(1, 1)                                   # a no-op
     finally:
         L.free()
+
+
+def test_one_launch_over_many_layers_and_device_entry():
+    """The multi-layer copy (40 layers: two launches of up to 32) through the
+    device-pointer entry point on a stream: every layer's state moves."""
+    from overhang_amd import hip
+    d = CFG1
+    w = synth.layer_weights(d, 2, projections=False)
+    lays = [gdn.GdnLayer(new_li(), d, w, max_seqs=3) for _ in range(40)]
+    st = hip.Stream()
+    try:
+        for i, L in enumerate(lays):
+            conv, S = synth.states(d, 100 + i)
+            L.set_state(2, conv, S)
+        gdn.state_copy_dev([L.li for L in lays], 2, 0, stream=st)
+        st.synchronize()
+        for L in lays:
+            c0, S0 = L.get_state(0)
+            c2, S2 = L.get_state(2)
+            np.testing.assert_array_equal(c0, c2)
+            np.testing.assert_array_equal(S0, S2)
+    finally:
+        for L in lays:
+            L.free()
