@@ -38,7 +38,7 @@ struct AttnShape {
     static constexpr int KS = HD + 4;             // padded K row in LDS (floats)
     static constexpr int NG4 = HD / 4;            // float4 groups per row
     static constexpr int R4 = (NG4 + OMH_WAVE - 1) / OMH_WAVE;   // groups per lane in P.V
-    static constexpr int NW = 4;                  // waves
+    static constexpr int NW = 8;                  // waves (two per SIMD)
     static constexpr size_t LDS = (size_t)(kAttnMaxGroup * HD + KT * KS + KT * HD) * sizeof(float);
 };
 
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
 // whose head index runs past grp computes a copy of head grp-1 and does not
 // write it.
 template <int HD, int GPW>
-__global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all of each SIMD's registers
     using S = AttnShape<HD>;
     constexpr int R4 = S::R4, NG4 = S::NG4, KT = S::KT, NW = S::NW, NT = NW * OMH_WAVE;
