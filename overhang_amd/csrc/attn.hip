@@ -277,12 +277,14 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
 }
 #undef OMH_ATTN_LOAD_PIECE
 
-// One workgroup per (token, head, 64 columns): the four waves take every
-// fourth split, lane = column, then sum through LDS.
+// One workgroup per (token, head, 64 columns): the CW waves take every
+// CW-th split, lane = column, then sum through LDS.
+constexpr int kCombineWaves = 8;
 template <int HD>
-__global__ __launch_bounds__(4 * OMH_WAVE) void attn_combine_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kCombineWaves * OMH_WAVE) void attn_combine_kernel(const AttnArgs a) {
     constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;     // column blocks per head
-    __shared__ float so[4][OMH_WAVE], sl[4];
+    constexpr int CW = kCombineWaves;
+    __shared__ float so[CW][OMH_WAVE], sl[CW];
     const int th = blockIdx.x / NCB, cb = blockIdx.x % NCB;
     const int t = th / a.H, h = th % a.H, ns = a.ns;
     const int tid = threadIdx.x, lane = tid % OMH_WAVE;
@@ -295,7 +297,7 @@ __global__ __launch_bounds__(4 * OMH_WAVE) void attn_combine_kernel(const AttnAr
     float L = 0.f, o = 0.f;
     const int jc = j < HD ? j : HD - 1;
 #pragma unroll 8
-    for (int s = wave; s < ns; s += 4) {           // an empty split: m = -inf, weight 0, zero partial
+    for (int s = wave; s < ns; s += CW) {          // an empty split: m = -inf, weight 0, zero partial
         const float wgt = expf(a.pml[2 * (pb + s)] - M);
         L = fmaf(a.pml[2 * (pb + s) + 1], wgt, L);
         o = fmaf(a.po[(pb + s) * HD + jc], wgt, o);
@@ -304,8 +306,12 @@ __global__ __launch_bounds__(4 * OMH_WAVE) void attn_combine_kernel(const AttnAr
     if (lane == 0) sl[wave] = L;
     __syncthreads();
     if (wave == 0 && j < HD) {
-        const float ls = (sl[0] + sl[1]) + (sl[2] + sl[3]);   // split 0 always holds key 0: ls > 0
-        const float os = (so[0][lane] + so[1][lane]) + (so[2][lane] + so[3][lane]);
+        float ls = 0.f, os = 0.f;                  // split 0 always holds key 0: ls > 0
+#pragma unroll
+        for (int w = 0; w < CW; w++) {
+            ls += sl[w];
+            os += so[w][lane];
+        }
         const float g = a.qkv[(size_t)t * a.ld_qkv + (size_t)h * 2 * HD + HD + j];
         a.ctx[((size_t)t * a.H + h) * HD + j] = os / ls * omh_sigmoid(g);
     }
@@ -332,7 +338,7 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
     }
     constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;
-    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)(a.T * a.H * NCB)), dim3(4 * OMH_WAVE), 0, st, a);
+    hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)(a.T * a.H * NCB)), dim3(kCombineWaves * OMH_WAVE), 0, st, a);
     return hipGetLastError();
 }
 
