@@ -176,6 +176,18 @@ int omh_attn_layer_free(int li);
 int omh_attn_forward(int li, int seq, int pos, int T, const float *x, float *out);
 int omh_attn_forward_dev(int li, int seq, int pos, int T, const float *x, float *out, void *stream);
 
+/* Copy cache rows t0 .. t0+n-1 of every kv head of sequence seq out of /
+ * into the device, from host arrays in the engine's layout
+ * [n_kv][ld_t][head_dim] (m->K[li] / m->V[li] with ld_t = m->max_t,
+ * engines/qwen.c:257-258; rows written at qwen.c:399-402).  Either pointer
+ * may be NULL.  After the first successful omh_attn_forward the device
+ * cache is the authoritative copy: a caller that falls back to the CPU
+ * mid-sequence first fetches rows 0 .. pos with omh_attn_cache_get (the
+ * counterpart of omh_gdn_state_get); cache_set re-seeds a layer that moves
+ * to the GPU mid-sequence.  Synchronous. */
+int omh_attn_cache_get(int li, int seq, int t0, int n, float *K, float *V, int ld_t);
+int omh_attn_cache_set(int li, int seq, int t0, int n, const float *K, const float *V, int ld_t);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,8 @@ def ref_lib():
         L.ref_quantize_rows.argtypes = [_f32p, _i8p, _f32p, C.c_int, C.c_int]
         L.ref_matmul_q.argtypes = [_f32p, _f32p, _i8p, _f32p, C.c_int, C.c_int]
         L.ref_matvec.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int]
+        L.ref_attn_run.argtypes = ([C.c_int] * 5 + [C.c_float, C.c_float, C.c_int] + [_f32p] * 6
+                                   + [C.c_int, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, _f32p])
         _REF = L
     return _REF
 
@@ -197,3 +199,26 @@ def ref_matvec(x, W):
     y = np.empty(O, np.float32)
     ref_lib().ref_matvec(y, _c(x), _c(W), I, O)
     return y
+
+
+def ref_attn_run(w, H, KV, hd, rot, theta, eps, pos0, Kpre, Vpre, x, int8: bool = False):
+    """T tokens through the reference attn_step (qwen.c:367-425) at positions
+    pos0..pos0+T-1 over a cache prefilled with Kpre / Vpre [pos0][KV][hd];
+    returns (out [T][D], K rows written [T][KV][hd], V rows [T][KV][hd])."""
+    R = ref_lib()
+    if R is None:
+        raise RuntimeError("oracle/_ref not built (reference sources absent at build time)")
+    x = _c(x)
+    T, D = x.shape
+    out = np.empty((T, D), np.float32)
+    Kn = np.empty((T, KV, hd), np.float32)
+    Vn = np.empty((T, KV, hd), np.float32)
+    if pos0 == 0:
+        Kpre = np.zeros((1, KV, hd), np.float32)
+        Vpre = Kpre
+    rc = R.ref_attn_run(D, H, KV, hd, rot, theta, eps, int(int8), _c(w["W_q"]), _c(w["W_k"]),
+                        _c(w["W_v"]), _c(w["W_o"]), _c(w["q_norm"]), _c(w["k_norm"]), pos0,
+                        _c(Kpre), _c(Vpre), T, x, out, Kn, Vn)
+    if rc != 0:
+        raise ValueError(f"ref_attn_run: {rc}")
+    return out, Kn, Vn

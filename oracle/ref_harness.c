@@ -74,3 +74,63 @@ void ref_matmul_q(float *y, const float *x, const int8_t *q, const float *scale,
 void ref_matvec(float *y, const float *x, const float *W, int I, int O) {
     matvec(y, x, W, I, O);
 }
+
+/* T tokens through the reference attn_step (qwen.c:367-425) on a synthetic
+ * Model/Layer, at positions pos0 .. pos0+T-1 of one sequence.  The cache
+ * rows 0 .. pos0-1 are first filled from Kpre / Vpre ([pos0][KV][hd], keys
+ * as the cache holds them: normed and rotated), so the step attends over
+ * thousands of positions without running the prompt through the layer.
+ * stream != 0 quantises q/k/v/o with the reference's qw_make first
+ * (qwen.c:252-255), the int8 path of DM.  Knew / Vnew (may be NULL) receive
+ * the T cache rows the calls wrote, [T][KV][hd].  attn_step keeps its
+ * scores in a float[8192] (qwen.c:407), so pos0 + T <= 8192. */
+int ref_attn_run(int hidden, int H, int KV, int hd, int rot, float theta, float eps, int stream,
+                 const float *Wq, const float *Wk, const float *Wv, const float *Wo,
+                 const float *qn, const float *kn, int pos0, const float *Kpre, const float *Vpre,
+                 int T, const float *x, float *out, float *Knew, float *Vnew) {
+    if (pos0 < 0 || T < 1 || pos0 + T > 8192) return -2;
+    Model m; memset(&m, 0, sizeof(m));
+    Layer l; memset(&l, 0, sizeof(l));
+    m.c.hidden = hidden; m.c.n_heads = H; m.c.n_kv = KV; m.c.head_dim = hd; m.c.rot_dim = rot;
+    m.c.theta = theta; m.c.eps = eps;
+    m.stream = stream;
+    const int max_t = pos0 + T;
+    m.max_t = max_t;
+    float *cp[4]; const float *src[4] = {Wq, Wk, Wv, Wo};
+    const int64_t nel[4] = {(int64_t)2 * H * hd * hidden, (int64_t)KV * hd * hidden,
+                            (int64_t)KV * hd * hidden, (int64_t)hidden * H * hd};
+    for (int i = 0; i < 4; i++) {
+        cp[i] = falloc(nel[i]);
+        memcpy(cp[i], src[i], nel[i] * sizeof(float));
+    }
+    l.q = cp[0]; l.k = cp[1]; l.v = cp[2]; l.o = cp[3];
+    l.qn = (float *)qn; l.kn = (float *)kn;
+    if (stream) {
+        l.Qq = qw_make(&l.q, 2 * H * hd, hidden);
+        l.Qk = qw_make(&l.k, KV * hd, hidden);
+        l.Qv = qw_make(&l.v, KV * hd, hidden);
+        l.Qo = qw_make(&l.o, hidden, H * hd);
+    }
+    float *Kc = falloc((int64_t)KV * max_t * hd), *Vc = falloc((int64_t)KV * max_t * hd);
+    for (int t = 0; t < pos0; t++)
+        for (int h = 0; h < KV; h++) {
+            memcpy(Kc + ((int64_t)h * max_t + t) * hd, Kpre + ((int64_t)t * KV + h) * hd, hd * sizeof(float));
+            memcpy(Vc + ((int64_t)h * max_t + t) * hd, Vpre + ((int64_t)t * KV + h) * hd, hd * sizeof(float));
+        }
+    float *Ks[1] = {Kc}, *Vs[1] = {Vc};
+    m.K = Ks; m.V = Vs;
+    for (int t = 0; t < T; t++)
+        attn_step(&m, &l, 0, x + (int64_t)t * hidden, pos0 + t, out + (int64_t)t * hidden);
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < KV; h++) {
+            if (Knew) memcpy(Knew + ((int64_t)t * KV + h) * hd, Kc + ((int64_t)h * max_t + pos0 + t) * hd, hd * sizeof(float));
+            if (Vnew) memcpy(Vnew + ((int64_t)t * KV + h) * hd, Vc + ((int64_t)h * max_t + pos0 + t) * hd, hd * sizeof(float));
+        }
+    free(Kc); free(Vc);
+    free(l.q); free(l.k); free(l.v); free(l.o);
+    if (stream) {
+        free(l.Qq.q); free(l.Qq.s); free(l.Qk.q); free(l.Qk.s);
+        free(l.Qv.q); free(l.Qv.s); free(l.Qo.q); free(l.Qo.s);
+    }
+    return 0;
+}

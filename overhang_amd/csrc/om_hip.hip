@@ -785,6 +785,44 @@ int omh_attn_layer_free(int li) {
     return OMH_OK;
 }
 
+// Rows t0 .. t0+n-1 of every kv head of one sequence's K and V caches,
+// to or from host arrays in the engine's layout [n_kv][ld_t][head_dim]
+// (m->K[li], m->V[li] with ld_t = m->max_t, engines/qwen.c:257-258, 399-402).
+static int attn_cache_copy(int li, int seq, int t0, int n, float *K, float *V, int ld_t, bool to_host) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = check_attn(li)) return rc;
+    const AttnLayer &A = g_A[li];
+    const omh_attn_dims &d = A.d;
+    if (seq < 0 || seq >= A.max_seqs) return fail(OMH_ERR_ARG, "attn cache: seq %d outside [0, %d)", seq, A.max_seqs);
+    if (t0 < 0 || n < 0 || (long)t0 + n > d.max_t || (long)t0 + n > ld_t)
+        return fail(OMH_ERR_ARG, "attn cache: rows %d..%d outside the cache of %d (host rows %d)", t0, t0 + n - 1,
+                    d.max_t, ld_t);
+    if (n == 0) return OMH_OK;
+    const size_t hd = d.head_dim, row = hd * sizeof(float), w = (size_t)n * row;
+    for (int h = 0; h < d.n_kv; h++) {
+        const size_t dev_off = (((size_t)seq * d.n_kv + h) * d.max_t + t0) * hd;
+        const size_t host_off = ((size_t)h * ld_t + t0) * hd;
+        float *dk = A.Kc + dev_off, *dv = A.Vc + dev_off;
+        if (to_host) {
+            if (K) HIP_OK(hipMemcpyAsync(K + host_off, dk, w, hipMemcpyDeviceToHost, g_stream));
+            if (V) HIP_OK(hipMemcpyAsync(V + host_off, dv, w, hipMemcpyDeviceToHost, g_stream));
+        } else {
+            if (K) HIP_OK(hipMemcpyAsync(dk, K + host_off, w, hipMemcpyHostToDevice, g_stream));
+            if (V) HIP_OK(hipMemcpyAsync(dv, V + host_off, w, hipMemcpyHostToDevice, g_stream));
+        }
+    }
+    HIP_OK(hipStreamSynchronize(g_stream));
+    return OMH_OK;
+}
+
+int omh_attn_cache_get(int li, int seq, int t0, int n, float *K, float *V, int ld_t) {
+    return attn_cache_copy(li, seq, t0, n, K, V, ld_t, true);
+}
+
+int omh_attn_cache_set(int li, int seq, int t0, int n, const float *K, const float *V, int ld_t) {
+    return attn_cache_copy(li, seq, t0, n, const_cast<float *>(K), const_cast<float *>(V), ld_t, false);
+}
+
 int omh_attn_forward_dev(int li, int seq, int pos, int T, const float *x, float *out, void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;
     return attn_forward(li, seq, pos, T, x, out, static_cast<hipStream_t>(stream));

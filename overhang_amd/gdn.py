@@ -28,7 +28,7 @@ EXPORTS = (
     "omh_gdn_decode_core_dev", "omh_gdn_prefill_core_dev", "omh_gdn_decode_dev",
     "omh_gdn_prefill_dev", "omh_sync",
     "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
-    "omh_gdn_state_copy", "omh_gdn_state_copy_dev",
+    "omh_gdn_state_copy", "omh_gdn_state_copy_dev", "omh_attn_cache_get", "omh_attn_cache_set",
 )
 
 
@@ -97,6 +97,8 @@ def lib() -> C.CDLL:
         L.omh_attn_layer_free.argtypes = [i]
         L.omh_attn_forward.argtypes = [i, i, i, i, vp, vp]
         L.omh_attn_forward_dev.argtypes = [i, i, i, i, vp, vp, vp]
+        L.omh_attn_cache_get.argtypes = [i, i, i, i, vp, vp, i]
+        L.omh_attn_cache_set.argtypes = [i, i, i, i, vp, vp, i]
         _LIB = L
     return _LIB
 
@@ -266,6 +268,7 @@ class AttnLayer:
                  theta: float, eps: float, max_t: int, weights: dict, max_seqs: int = 1, int8: bool = False):
         require_gpu()
         self.li, self.hidden = li, hidden
+        self.n_kv, self.head_dim = n_kv, head_dim
         keep = {k: (v if k.startswith(("Q_", "S_")) else _f32(v)) for k, v in weights.items()}
         if int8:
             for nm in ("q", "k", "v", "o"):
@@ -277,6 +280,20 @@ class AttnLayer:
 
     def free(self) -> None:
         check(lib().omh_attn_layer_free(self.li))
+
+    def cache_get(self, seq: int, t0: int, n: int, ld_t: int | None = None):
+        """Cache rows t0..t0+n-1 as the engine holds them: K, V [KV][ld_t][hd]
+        (rows outside t0..t0+n-1 are zero)."""
+        ld_t = ld_t or t0 + n
+        K = np.zeros((self.n_kv, ld_t, self.head_dim), np.float32)
+        V = np.zeros_like(K)
+        check(lib().omh_attn_cache_get(self.li, seq, t0, n, _ptr(K), _ptr(V), ld_t))
+        return K, V
+
+    def cache_set(self, seq: int, t0: int, n: int, K: np.ndarray, V: np.ndarray) -> None:
+        """Rows t0..t0+n-1 of host K, V [KV][ld_t][hd] into the device cache."""
+        K, V = _f32(K), _f32(V)
+        check(lib().omh_attn_cache_set(self.li, seq, t0, n, _ptr(K), _ptr(V), K.shape[1]))
 
     def forward(self, seq: int, pos: int, x: np.ndarray) -> np.ndarray:
         """x [T][hidden] at positions pos .. pos+T-1 -> [T][hidden]."""

@@ -70,6 +70,7 @@ def uniform(seed: int, stream: int, shape, lo: float = 0.0, hi: float = 1.0) -> 
 # stream ids (stable: never renumber)
 S_WQKV, S_WZ, S_WB, S_WA, S_WOUT, S_CONV, S_ALOG, S_DT, S_GNORM = range(1, 10)
 S_X, S_QKV, S_Z, S_A, S_B, S_STATE, S_CONVST = range(20, 27)
+S_AQ, S_AK, S_AV, S_AO, S_AQN, S_AKN, S_AX, S_KPRE, S_VPRE = range(40, 49)
 
 
 def layer_weights(d, seed: int = 0, gnorm_std: float = 0.0, proj_std: float = 0.02,
@@ -118,3 +119,23 @@ def states(d, seed: int = 0, s_std: float = 0.05, conv_std: float = 1.0, B: int 
     S = normal(seed, S_STATE, lead + (d.vh, d.kd, d.vd), 0.0, s_std)
     conv = normal(seed, S_CONVST, lead + (conv_dim, d.K - 1), 0.0, conv_std)
     return conv, S
+
+
+def attn_weights(D: int, H: int, KV: int, hd: int, seed: int = 0, proj_std: float = 0.02,
+                 norm_std: float = 0.1) -> dict:
+    """Random gated-attention weights (the omh_attn_weights names): q_proj
+    [2*H*hd][D] (per head [hd q | hd gate]), k_proj / v_proj [KV*hd][D],
+    o_proj [D][H*hd], q_norm / k_norm [hd] (used as 1 + w)."""
+    return {"W_q": normal(seed, S_AQ, (2 * H * hd, D), 0.0, proj_std),
+            "W_k": normal(seed, S_AK, (KV * hd, D), 0.0, proj_std),
+            "W_v": normal(seed, S_AV, (KV * hd, D), 0.0, proj_std),
+            "W_o": normal(seed, S_AO, (D, H * hd), 0.0, proj_std),
+            "q_norm": normal(seed, S_AQN, (hd,), 0.0, norm_std),
+            "k_norm": normal(seed, S_AKN, (hd,), 0.0, norm_std)}
+
+
+def attn_inputs(D: int, KV: int, hd: int, pos0: int, T: int, seed: int = 0):
+    """x [T][D] ~ N(0,1) and a prefilled cache Kpre / Vpre [pos0][KV][hd]:
+    keys of unit RMS (as RMSNorm leaves them), values ~ N(0,1)."""
+    return (normal(seed, S_AX, (T, D)), normal(seed, S_KPRE, (pos0, KV, hd)),
+            normal(seed, S_VPRE, (pos0, KV, hd)))

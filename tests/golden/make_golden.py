@@ -14,7 +14,7 @@ exact and out[:vh*vd] is the reference core output.
 
 Also copies the reference's tiny end-to-end oracle (model, config, token ids).
 
-usage: python tests/golden/make_golden.py
+usage: python tests/golden/make_golden.py [attn]
 """
 from __future__ import annotations
 
@@ -108,6 +108,33 @@ def quant_fixture(name):
     print(f"{name}: scales {s}")
 
 
+# (name, hidden, H, KV, hd, rot, pos0, T, int8, seed): the reference tiny
+# model's attention shape (oracle/qwen_tiny/config.json: head_dim 32,
+# partial_rotary_factor 0.25) and the Qwen3.6-35B-A3B one (hidden 2048, 16
+# query / 2 kv heads of 256, rot 64), at positions below attn_step's
+# float[8192] score buffer (qwen.c:407).
+ATTN_FIXTURES = [
+    ("attn_tiny_f32", 64, 4, 2, 32, 8, 1000, 3, False, 11),
+    ("attn_tiny_int8", 64, 4, 2, 32, 8, 37, 4, True, 12),
+    ("attn_35b_f32", 2048, 16, 2, 256, 64, 5000, 2, False, 13),
+    ("attn_35b_int8", 2048, 16, 2, 256, 64, 8000, 3, True, 14),
+]
+ATTN_THETA, ATTN_EPS = 1e7, 1e-6
+
+
+def attn_fixture(name, D, H, KV, hd, rot, pos0, T, int8, seed):
+    w = synth.attn_weights(D, H, KV, hd, seed)
+    x, Kpre, Vpre = synth.attn_inputs(D, KV, hd, pos0, T, seed)
+    out, Kn, Vn = oracle.ref_attn_run(w, H, KV, hd, rot, ATTN_THETA, ATTN_EPS, pos0, Kpre, Vpre, x,
+                                      int8=int8)
+    meta = dict(kind="attn", dims=np.array([D, H, KV, hd, rot, pos0, T]), theta=np.float64(ATTN_THETA),
+                eps=np.float64(ATTN_EPS), int8=int(int8), seed=seed)
+    hashes = {"sha_" + k: sha(v) for k, v in w.items()}
+    hashes.update(sha_x=sha(x), sha_Kpre=sha(Kpre), sha_Vpre=sha(Vpre))
+    np.savez_compressed(os.path.join(OUT, name + ".npz"), out=out, K=Kn, V=Vn, **meta, **hashes)
+    print(f"{name}: out max|.| {np.abs(out).max():.4g}")
+
+
 def copy_tiny_model():
     dst = os.path.join(OUT, "qwen_tiny")
     os.makedirs(dst, exist_ok=True)
@@ -120,6 +147,10 @@ def copy_tiny_model():
 def main():
     if oracle.ref_lib() is None:
         sys.exit("oracle/_ref/libqwen_ref.so missing: run `make -C oracle` with the reference present")
+    if sys.argv[1:] == ["attn"]:                  # the attention fixtures alone
+        for f in ATTN_FIXTURES:
+            attn_fixture(*f)
+        return
     layer_fixture("cfg1_layer_f32", CFG1, seed=0, T=64, int8=False, zero_state=True, gnorm_std=0.0)
     layer_fixture("tiny_layer_int8", TINY, seed=1, T=65, int8=True, zero_state=False, gnorm_std=0.1)
     core_fixture("core_rep3_d16", GdnDims(2, 6, 16, 16, 4, 0), seed=2, T=33, gnorm_std=0.1)
@@ -128,6 +159,8 @@ def main():
     core_fixture("core_d32_decay", GdnDims(2, 4, 32, 32, 4, 0), seed=5, T=70, gnorm_std=0.1,
                  a_mean=2.0)
     quant_fixture("quant_rows")
+    for f in ATTN_FIXTURES:
+        attn_fixture(*f)
     copy_tiny_model()
 
 

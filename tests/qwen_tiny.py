@@ -20,6 +20,7 @@ ref_qwen.json, copied under tests/golden/qwen_tiny.
 """
 from __future__ import annotations
 
+import ctypes
 import json
 import os
 
@@ -122,6 +123,22 @@ class HipGdn:
 _ATTN_W = ("q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm")
 
 
+_LIBM = None
+
+
+def rope_inv_freq(theta, rot):
+    """powf(theta, -(float)(2j)/(float)rot) for j < rot/2 (qwen.c:391), through
+    the C library's own powf: numpy's float32 power can differ from it by an
+    ulp, which at positions in the thousands moves the rotation angle by
+    ~1e-4 rad."""
+    global _LIBM
+    if _LIBM is None:
+        _LIBM = ctypes.CDLL("libm.so.6")
+        _LIBM.powf.restype = ctypes.c_float
+        _LIBM.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    return np.array([_LIBM.powf(f32(theta), f32(-f32(2 * j) / f32(rot))) for j in range(rot // 2)], f32)
+
+
 def gated_attention(x, W, Kl, Vl, pos, H, KV, hd, rot, theta, eps):
     """The engine's attn_step (qwen.c:366-425) for T tokens x [T][D] at
     positions pos..pos+T-1, in float32: q/gate split per head (qwen.c:376-382),
@@ -138,8 +155,7 @@ def gated_attention(x, W, Kl, Vl, pos, H, KV, hd, rot, theta, eps):
     q = rmsnorm(q, W["q_norm"], eps)
     k = rmsnorm(k, W["k_norm"], eps)
     half = rot // 2
-    j = np.arange(half)
-    inv = np.power(f32(theta), -(2.0 * j).astype(f32) / f32(rot)).astype(f32)
+    inv = rope_inv_freq(theta, rot)
     ps = np.arange(pos, pos + T, dtype=f32)[:, None]
     ang = (ps * inv[None, :]).astype(f32)
     cs, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]

@@ -181,3 +181,29 @@ def test_device_pointer_entry_matches_host_entry():
     finally:
         A.free()
         B.free()
+
+
+@pytest.mark.parametrize("name", ["attn_tiny_f32", "attn_tiny_int8", "attn_35b_f32", "attn_35b_int8"])
+def test_attention_matches_reference_attn_golden(name):
+    """The GPU layer against the reference's own attn_step (qwen.c:367-425,
+    fixtures written by tests/golden/make_golden.py): the cache rows
+    0..pos0-1 are seeded through omh_attn_cache_set, then the fixture's
+    tokens run one call each at positions pos0.. (up to 8002, the 35B
+    shape), and the written cache rows come back through
+    omh_attn_cache_get."""
+    from tests.test_attn_ref import load_attn
+    s, w, x, Kpre, Vpre, exp = load_attn(name)
+    D, H, KV, hd, rot, pos0, T = (s[k] for k in ("D", "H", "KV", "hd", "rot", "pos0", "T"))
+    L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, s["theta"], s["eps"], pos0 + T, w, int8=s["int8"])
+    try:
+        L.cache_set(0, 0, pos0, np.ascontiguousarray(Kpre.transpose(1, 0, 2)),
+                    np.ascontiguousarray(Vpre.transpose(1, 0, 2)))
+        got = np.concatenate([L.forward(0, pos0 + t, x[t:t + 1]) for t in range(T)])
+        assert_close(got, exp["out"], what=f"{name} out")
+        K, V = L.cache_get(0, pos0, T, pos0 + T)
+        assert_close(K[:, pos0:].transpose(1, 0, 2), exp["K"], what=f"{name} K rows")
+        assert_close(V[:, pos0:].transpose(1, 0, 2), exp["V"], what=f"{name} V rows")
+        K0, _ = L.cache_get(0, 0, pos0, pos0 + T)
+        assert np.array_equal(K0[:, :pos0], Kpre.transpose(1, 0, 2)), "seeded rows come back unchanged"
+    finally:
+        L.free()

@@ -126,3 +126,59 @@ def test_projection_shape_limits_are_reported():
     with pytest.raises(gdn.OmhError) as e:
         gdn.GdnLayer(new_li(), d, w)
     assert e.value.code == gdn.OMH_ERR_SHAPE
+
+
+@pytest.mark.parametrize("B,int8", [(1, True), (3, True), (1, False)], ids=["B1-int8", "B3-int8", "B1-f32"])
+def test_35b_block_drop_in_small_batch(B, int8):
+    """The engine's own call at the real shape: omh_gdn_decode(li, B, x, out)
+    with the 35B-A3B GDN weights.  Up to 4 tokens the projections run on the
+    register GEMV, whose k split is 2 for in_proj (I = 2048: 12288 int8 rows
+    plus 64 fp32 b/a rows in one launch) and 4 for out_proj (I = 4096).
+    Three tokens per sequence, each sequence against its own oracle run."""
+    d = Q35B
+    seed = 7100 + B + 10 * int8
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed, B=B)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=int8)
+    for s in range(B):
+        L.set_state(s, conv0[s], S0[s])
+    T = 3
+    x = _x(d, seed, (T, B))
+    got = np.stack([L.decode(x[t]) for t in range(T)], axis=1)       # [B][T][D]
+    for s in range(B):
+        ref, cref, Sref = oracle.layer_seq(d, w, x[:, s], conv0[s], S0[s], int8=int8)
+        conv, S = L.get_state(s)
+        assert_close(got[s], ref, what=f"35B B={B} int8={int8} seq {s} out")
+        assert_close(S, Sref, what=f"35B B={B} int8={int8} seq {s} S")
+        assert np.array_equal(conv, cref), f"seq {s} conv history"
+    L.free()
+
+
+@pytest.mark.parametrize("T", [256, 1024])
+def test_35b_int8_prefill_block_matches_oracle(T):
+    """Row f2 at prefill size: the 35B-A3B int8 layer through
+    omh_gdn_prefill, whose projections run on the bf16 x 3 wave-tile kernel
+    (in_proj 2048 -> 12352, out_proj 4096 -> 2048), continuing from a nonzero
+    state.  Every token's output and the final state and conv history are
+    compared with the per-token oracle (engines/qwen.c:301-364 with
+    matmul_q, qwen.c:94-122)."""
+    d = Q35B
+    seed = 7300 + T
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed)
+    L = gdn.GdnLayer(new_li(), d, w, int8=True)
+    L.set_state(0, conv0, S0)
+    x = _x(d, seed, (T,))
+    out = L.prefill(0, x)
+    ref, cref, Sref = oracle.layer_seq(d, w, x, conv0, S0, int8=True)
+    conv, S = L.get_state(0)
+    assert_close(out, ref, what=f"35B int8 prefill T={T} out")
+    assert_close(S, Sref, what=f"35B int8 prefill T={T} S")
+    assert np.array_equal(conv, cref), "conv history"
+    # a decode step after the prefill continues the same recurrence
+    x1 = _x(d, seed + 1, (1,))
+    o1 = L.decode(x1)
+    ref1, _, Sref1 = oracle.layer_seq(d, w, x1, cref, Sref, int8=True)
+    assert_close(o1, ref1, what="decode after prefill out")
+    assert_close(L.get_state(0)[1], Sref1, what="decode after prefill S")
+    L.free()

@@ -310,3 +310,45 @@ def test_paired_kernel_rejects_rep_above_limit(monkeypatch):
                                 np.zeros((d.conv_dim, 3), np.float32), np.zeros((16, 16, 16), np.float32))
     assert_close(core, ref)
     L.free()
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_decode_core_dev_30_layers_35b_vs_oracle(B):
+    """Config 2's launch itself: the cores of 30 GDN layers of the 35B-A3B
+    shape in one omh_gdn_decode_core_dev call, two steps, every layer's
+    output, state and conv history against its own oracle run."""
+    from overhang_amd import hip
+    d = Q35B
+    nl, T = 30, 2
+    lays, ws, st0 = [], [], []
+    for l in range(nl):
+        w = synth.layer_weights(d, 500 + l, gnorm_std=0.1, projections=False)
+        conv0, S0 = synth.states(d, 500 + l, B=B)
+        L = gdn.GdnLayer(new_li(), d, w, max_seqs=B)
+        for s in range(B):
+            L.set_state(s, conv0[s], S0[s])
+        lays.append(L)
+        ws.append(w)
+        st0.append((conv0, S0))
+    inp = [synth.core_inputs(d, T, 600 + l, B=B) for l in range(nl)]     # per layer [B][T][...]
+    core = hip.Buffer(nl * B * d.val_dim * 4)
+    st = hip.Stream()
+    got = np.empty((T, nl, B, d.val_dim), np.float32)
+    for t in range(T):
+        host = {k: np.ascontiguousarray(np.stack([inp[l][k][:, t] for l in range(nl)]))
+                for k in ("qkv", "z", "a", "b")}
+        dev = {k: hip.Buffer.from_numpy(v) for k, v in host.items()}
+        gdn.decode_core_dev([L.li for L in lays], B, dev["qkv"], dev["z"], dev["a"], dev["b"], core,
+                            stream=st)
+        st.synchronize()
+        got[t] = core.numpy((nl, B, d.val_dim))
+    for l in range(nl):
+        for s in range(B):
+            ref, cref, Sref = oracle.core_seq(d, ws[l], inp[l]["qkv"][s], inp[l]["z"][s], inp[l]["a"][s],
+                                              inp[l]["b"][s], st0[l][0][s], st0[l][1][s])
+            conv, S = lays[l].get_state(s)
+            assert_close(got[:, l, s], ref, what=f"layer {l} seq {s} core")
+            assert_close(S, Sref, what=f"layer {l} seq {s} S")
+            assert np.array_equal(conv, cref), f"layer {l} seq {s} conv history"
+    for L in lays:
+        L.free()
