@@ -150,7 +150,8 @@ def test_35b_block_drop_in_small_batch(B, int8):
         conv, S = L.get_state(s)
         assert_close(got[s], ref, what=f"35B B={B} int8={int8} seq {s} out")
         assert_close(S, Sref, what=f"35B B={B} int8={int8} seq {s} S")
-        assert np.array_equal(conv, cref), f"seq {s} conv history"
+        # the history holds in_proj outputs: a floating-point result here
+        assert_close(conv, cref, what=f"35B B={B} int8={int8} seq {s} conv")
     L.free()
 
 
@@ -174,7 +175,7 @@ def test_35b_int8_prefill_block_matches_oracle(T):
     conv, S = L.get_state(0)
     assert_close(out, ref, what=f"35B int8 prefill T={T} out")
     assert_close(S, Sref, what=f"35B int8 prefill T={T} S")
-    assert np.array_equal(conv, cref), "conv history"
+    assert_close(conv, cref, what=f"35B int8 prefill T={T} conv")
     # a decode step after the prefill continues the same recurrence
     x1 = _x(d, seed + 1, (1,))
     o1 = L.decode(x1)
