@@ -134,6 +134,19 @@ int omh_gdn_prefill_core_dev(int li, int seq, int T, const float *qkv, const flo
 int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream);
 int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void *stream);
 
+/* omh_gdn_decode_dev without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory mid-run: code
+ * under HIP graph capture, fixed-footprint serving loops, harnesses that
+ * forbid hipMalloc.  Same computation and kernels as omh_gdn_decode_dev, but
+ * its scratch (in_proj rows, core rows, the int8 projections' bf16 planes,
+ * partial tiles and arrival counters) is one static 8 MiB device buffer per
+ * GPU, held until the process ends, instead of the library's grow-only
+ * scratch.  A call whose scratch would exceed 8 MiB returns OMH_ERR_SHAPE
+ * (35B-A3B GDN shape: up to B = 64 fits).  All calls on one GPU share that
+ * buffer, so calls that may overlap in time (different streams) race:
+ * issue them from one stream. */
+int omh_gdn_decode_noalloc_dev(int li, int B, const float *x, float *out, void *stream);
+
 /* Wait for all work this library enqueued on `stream`. */
 int omh_sync(void *stream);
 

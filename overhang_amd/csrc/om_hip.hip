@@ -72,7 +72,7 @@ struct Scratch {
     void *p = nullptr;
     size_t n = 0;
 };
-Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre, g_xb;
+Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre, g_xb, g_dec;
 
 int ensure(Scratch &s, size_t bytes) {
     if (bytes <= s.n) return OMH_OK;
@@ -190,24 +190,46 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
     return OMH_OK;
 }
 
-int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
+// Scratch of one whole-layer decode call of B sequences, as byte offsets in
+// one region: the in_proj rows [B][in_rows] and core rows [B][vdim] (fp32),
+// then, for int8 rows with B > 4, the projections' bf16 planes, block sums,
+// k-split partial tiles and arrival counters (proj_xb_bytes).
+struct DecodeScratch {
+    size_t in = 0, core = 0, xb = 0, xb_n = 0, total = 0;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+DecodeScratch decode_scratch(const DevLayer &L, int B) {
+    DecodeScratch s;
+    s.in = 0;
+    s.core = align256((size_t)B * L.in_rows * sizeof(float));
+    s.xb = s.core + align256((size_t)B * L.vdim * sizeof(float));
+    if (B > 4 && (L.in_nq > 0 || L.out_nq > 0))
+        s.xb_n = std::max(proj_xb_bytes(B, L.d.hidden, L.in_nq), proj_xb_bytes(B, L.vdim, L.out_nq));
+    s.total = s.xb + align256(s.xb_n);
+    return s;
+}
+
+int decode_full_args(int li, int B, const float *x, float *out) {
     if (int rc = check_layer(li)) return rc;
-    DevLayer &L = g_L[li];
+    const DevLayer &L = g_L[li];
     if (!L.has_proj) return fail(OMH_ERR_ARG, "layer %d was initialised without projections", li);
     if (B < 1 || B > L.max_seqs) return fail(OMH_ERR_ARG, "decode: B=%d outside [1, %d]", B, L.max_seqs);
     if (!x || !out || !aligned16(x) || !aligned16(out)) return fail(OMH_ERR_ARG, "decode: x/out must be 16-byte aligned");
+    return OMH_OK;
+}
+
+// The whole layer for B sequences with its scratch at `scr` (laid out as
+// decode_scratch(L, B) says); allocates nothing.
+int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, char *scr) {
+    DevLayer &L = g_L[li];
     const int D = L.d.hidden;
-    if (int rc = ensure(g_in, (size_t)B * L.in_rows * sizeof(float))) return rc;
-    if (int rc = ensure(g_core, (size_t)B * L.vdim * sizeof(float))) return rc;
-    uint16_t *xb = nullptr;
-    if (B > 4 && (L.in_nq > 0 || L.out_nq > 0)) {
-        const size_t xbn = std::max(proj_xb_bytes(B, D, L.in_nq), proj_xb_bytes(B, L.vdim, L.out_nq));
-        if (int rc = ensure(g_xb, xbn)) return rc;
-        xb = static_cast<uint16_t *>(g_xb.p);
-    }
-    float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
+    const DecodeScratch ds = decode_scratch(L, B);
+    float *in = reinterpret_cast<float *>(scr + ds.in), *core = reinterpret_cast<float *>(scr + ds.core);
+    uint16_t *xb = ds.xb_n ? reinterpret_cast<uint16_t *>(scr + ds.xb) : nullptr;
     ProjArgs p{};
-    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
+    p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = ds.xb_n;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
@@ -216,9 +238,39 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     uint16_t *planes = xb && L.out_nq > 0 && decode_planes_supported(L.d.vd, decode_variant()) ? xb : nullptr;
     if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes)) return rc;
     ProjArgs q{};
-    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0; q.x_split = planes != nullptr;
+    q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = ds.xb_n; q.x_split = planes != nullptr;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
+    return OMH_OK;
+}
+
+int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
+    if (int rc = decode_full_args(li, B, x, out)) return rc;
+    if (int rc = ensure(g_dec, decode_scratch(g_L[li], B).total)) return rc;
+    return decode_full_on(li, B, x, out, st, static_cast<char *>(g_dec.p));
+}
+
+// ---- the allocation-free decode entry point ----
+//
+// Its scratch is this file-scope array: one copy per GPU, held until the
+// process ends.  Host code never passes the array's name to a kernel or a
+// copy (on the host it is only a stand-in for the symbol): it uses the device
+// address hipGetSymbolAddress returns, fetched once per device.
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+char *g_scratch_dev[kMaxDevices];
+
+int noalloc_scratch(char **out) {
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(OMH_ERR_DEVICE, "device %d beyond the library's table", dev);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        g_scratch_dev[dev] = static_cast<char *>(p);
+    }
+    *out = g_scratch_dev[dev];
     return OMH_OK;
 }
 
@@ -379,6 +431,8 @@ int omh_init(void) {
         fail(OMH_ERR_DEVICE, "stream creation failed");
         return 0;
     }
+    char *scr = nullptr;
+    if (noalloc_scratch(&scr) != OMH_OK) return 0;        // the no-alloc scratch's device address
     g_ready = 1;
     return 1;
 }
@@ -622,6 +676,18 @@ int omh_gdn_decode_core(int li, int B, const float *qkv, const float *z, const f
 int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;
     return decode_full(li, B, x, out, static_cast<hipStream_t>(stream));
+}
+
+int omh_gdn_decode_noalloc_dev(int li, int B, const float *x, float *out, void *stream) {
+    if (!omh_init()) return OMH_ERR_DEVICE;
+    if (int rc = decode_full_args(li, B, x, out)) return rc;
+    const size_t need = decode_scratch(g_L[li], B).total;
+    if (need > kNoAllocScratchBytes)
+        return fail(OMH_ERR_SHAPE, "decode_noalloc: B=%d needs %zu bytes of scratch, above the %zu-byte static buffer",
+                    B, need, kNoAllocScratchBytes);
+    char *scr = nullptr;
+    if (int rc = noalloc_scratch(&scr)) return rc;
+    return decode_full_on(li, B, x, out, static_cast<hipStream_t>(stream), scr);
 }
 
 int omh_gdn_decode(int li, int B, const float *x, float *out) {

@@ -29,6 +29,7 @@ EXPORTS = (
     "omh_gdn_prefill_dev", "omh_sync",
     "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
     "omh_gdn_state_copy", "omh_gdn_state_copy_dev", "omh_attn_cache_get", "omh_attn_cache_set",
+    "omh_gdn_decode_noalloc_dev",
 )
 
 
@@ -90,6 +91,7 @@ def lib() -> C.CDLL:
         L.omh_gdn_prefill_core_dev.argtypes = [i, i, i, vp, vp, vp, vp, vp, vp]
         L.omh_gdn_decode_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_gdn_prefill_dev.argtypes = [i, i, i, vp, vp, vp]
+        L.omh_gdn_decode_noalloc_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_sync.argtypes = [vp]
         L.omh_gdn_state_copy.argtypes = [i, C.POINTER(C.c_int), i, i]
         L.omh_gdn_state_copy_dev.argtypes = [i, C.POINTER(C.c_int), i, i, vp]
@@ -244,6 +246,11 @@ def prefill_core_dev(li: int, seq: int, T: int, qkv, z, a, b, core, stream=None)
 
 def decode_dev(li: int, B: int, x, out, stream=None) -> None:
     check(lib().omh_gdn_decode_dev(li, B, _ptr(x), _ptr(out), _stream(stream)))
+
+
+def decode_noalloc_dev(li: int, B: int, x, out, stream=None) -> None:
+    """decode_dev with the library's static scratch: allocates nothing."""
+    check(lib().omh_gdn_decode_noalloc_dev(li, B, _ptr(x), _ptr(out), _stream(stream)))
 
 
 def prefill_dev(li: int, seq: int, T: int, x, out, stream=None) -> None:
