@@ -122,32 +122,47 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
         hip.device_synchronize()
         return fused, None, None, alg_bytes, R
 
-    # engine order: one launch per layer
+    # engine order: one launch per layer (the order an engine issues them)
     def step_layers(k):
         g = groups[k % R]
         for l in range(N_LAYERS):
             gdn.decode_core_dev([g[l]], 1, *(dev[nm].at(l * row[nm]) for nm in ("qkv", "z", "a", "b")),
                                 core.at(l * d.val_dim * 4), stream=st)
 
-    el2, durs2, _ = time_launches(hip, st, step_layers, max(steps // 2, 5), warmup)
     n2 = max(steps // 2, 5)
+    el2, durs2, _ = time_launches(hip, st, step_layers, n2, warmup)
     k2 = statistics.mean(durs2) / N_LAYERS
-    engine = {"tok_s": n2 / el2, "ms_per_step": 1e3 * el2 / n2, "kernel_us_per_layer_incl_gaps": 1e6 * k2,
-              "note": "30 dependent one-layer launches per token, as an engine issues them"}
-    log(f"decode engine order (30 launches/token): {engine['tok_s']:.0f} tok/s")
+    engine = {"tok_s": n2 / el2, "ms_per_step": 1e3 * el2 / n2, "us_per_layer_incl_gaps": 1e6 * k2,
+              "issue": "30 one-layer launches per token from Python (ctypes)"}
+    log(f"decode engine order (30 launches/token, ctypes): {engine['tok_s']:.0f} tok/s")
+    # the same 30 launches captured once in a HIP graph (two tokens per graph,
+    # so every layer's ring epoch alternates as in eager use) and replayed
+    graphs = [hip.Graph(st, lambda r=r: [step_layers(r), step_layers(r)]) for r in range(R)]
+    def step_graph(k):
+        graphs[k % R].launch()
+    n3 = max(steps // 2, 5)
+    el3, _, _ = time_launches(hip, st, step_graph, n3, warmup)
+    engine_graph = {"tok_s": 2 * n3 / el3, "ms_per_step": 1e3 * el3 / (2 * n3),
+                    "us_per_layer": 1e6 * el3 / (2 * n3 * N_LAYERS), "kernel_nodes_per_graph": graphs[0].nodes,
+                    "issue": "30 one-layer launches per token, captured in a HIP graph (2 tokens per graph)"}
+    log(f"decode engine order (graph): {engine_graph['tok_s']:.0f} tok/s, "
+        f"{engine_graph['us_per_layer']:.2f} us per layer")
+    for gr in graphs:
+        gr.close()
     for L in lays:
         L.free()
     hip.device_synchronize()
 
-    # batch sweep: one layer per launch, B sequences, rotating over >1 GiB
+    # batch sweep: one layer per launch, B sequences; every B rotates over
+    # more than 1 GiB of distinct states (layers of max_seqs = B)
     sweep = []
-    Bmax = 64
-    nrot = max(2, math.ceil(ROTATE_BYTES / (Bmax * per_layer)))
-    lays = make_layers(gdn, d, 1000, nrot, Bmax, w, conv0, S0)
-    inpB = synth.core_inputs(d, 1, 2, B=Bmax)
-    devB = {k: hip.Buffer.from_numpy(np.ascontiguousarray(v[:, 0])) for k, v in inpB.items()}
-    coreB = hip.Buffer(Bmax * d.val_dim * 4)
     for B in (1, 2, 4, 8, 16, 32, 64):
+        nrot = max(2, math.ceil(ROTATE_BYTES / (B * per_layer)))
+        lays = make_layers(gdn, d, 1000, nrot, B, w, conv0, S0)
+        inpB = synth.core_inputs(d, 1, 2, B=B)
+        devB = {k: hip.Buffer.from_numpy(np.ascontiguousarray(v[:, 0])) for k, v in inpB.items()}
+        coreB = hip.Buffer(B * d.val_dim * 4)
+
         def stepB(k, B=B):
             gdn.decode_core_dev([lays[k % nrot].li], B, devB["qkv"], devB["z"], devB["a"], devB["b"], coreB,
                                 stream=st)
@@ -156,12 +171,115 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
         kb = elB / nsteps
         gbs = B * 2 * d.state_bytes / kb / 1e9
         sweep.append({"B": B, "kernel_us": 1e6 * kb, "achieved_GBs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS,
-                      "tok_s_30_layers": B / (N_LAYERS * kb)})
-        log(f"decode sweep B={B}: kernel {1e6 * kb:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}%)")
+                      "tok_s_30_layers": B / (N_LAYERS * kb), "rotation_bytes": nrot * B * per_layer})
+        log(f"decode sweep B={B}: kernel {1e6 * kb:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}%), "
+            f"rotating over {nrot * B * per_layer / 2**30:.2f} GiB")
+        for L in lays:
+            L.free()
+        hip.device_synchronize()
+    return fused, {"ctypes": engine, "graph": engine_graph}, sweep, alg_bytes, R
+
+
+def quantized(w):
+    """w plus its int8 twins (Q_*, S_* for qkv, z, out), made once with the
+    engine's rule, so several layers can share one quantisation."""
+    from overhang_amd import gdn
+    w = dict(w)
+    for nm in ("qkv", "z", "out"):
+        w["Q_" + nm], w["S_" + nm] = gdn.quantize_rows(w["W_" + nm])
+    return w
+
+
+def bench_engine_block(hip, gdn, synth, steps, warmup):
+    """The drop-in as an engine uses it at B = 1: one token through the whole
+    GDN block (int8 in_proj -> core -> int8 out_proj) of each of 30 layers at
+    the 35B shape, layer after layer, each layer's output the next one's
+    input.  Every layer has its own weights and state (1.1 GB of weights in
+    all, beyond the last-level cache).  Issued as omh_gdn_decode_noalloc_dev
+    calls captured in a HIP graph (2 tokens per graph); also the latency of
+    the host-pointer call omh_gdn_decode(li, 1, x, out), the exact
+    deltanet_step replacement, with its copies."""
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = quantized(synth.layer_weights(d, 5))
+    lays = [gdn.GdnLayer(2100 + i, d, w, max_seqs=1) for i in range(N_LAYERS)]
+    bufs = [hip.Buffer.from_numpy(synth.normal(8, synth.S_X, (1, d.hidden), 0.0, 1.0))] + \
+           [hip.Buffer(d.hidden * 4) for _ in range(N_LAYERS)]
+    st = hip.Stream()
+
+    def token():
+        for l in range(N_LAYERS):
+            gdn.decode_noalloc_dev(lays[l].li, 1, bufs[l], bufs[l + 1], stream=st)
+
+    g = hip.Graph(st, lambda: [token(), token()])
+    n = max(steps // 2, 5)
+    el, _, _ = time_launches(hip, st, lambda k: g.launch(), n, warmup)
+    per_tok = el / (2 * n)
+    wbytes = block_bytes(d, 1) - 2 * (d.state_bytes + 4 * d.conv_dim * (d.K - 1)) - 2 * d.hidden * 4
+    alg = N_LAYERS * block_bytes(d, 1)
+    res = {"tok_s": 1 / per_tok, "us_per_token": 1e6 * per_tok, "us_per_layer": 1e6 * per_tok / N_LAYERS,
+           "alg_bytes_per_token": alg, "achieved_GBs": alg / per_tok / 1e9,
+           "frac_hbm": alg / per_tok / 1e9 / HBM_PEAK_GBS, "weight_bytes_per_layer": wbytes,
+           "kernel_nodes_per_graph": g.nodes,
+           "note": "30 GDN layers x whole block (int8 projections on the register GEMV, core), B=1, "
+                   "dependent chain, HIP graph replay"}
+    g.close()
+    log(f"engine block chain (graph): {res['us_per_layer']:.2f} us/layer, {res['tok_s']:.0f} tok/s "
+        f"({100 * res['frac_hbm']:.1f}% of HBM peak)")
+    # the host-pointer drop-in (synchronous, x and out in host memory)
+    x = synth.normal(9, synth.S_X, (1, d.hidden), 0.0, 1.0)
+    for _ in range(5):
+        lays[0].decode(x)
+    ts = []
+    for i in range(200):
+        t0 = time.perf_counter()
+        lays[i % N_LAYERS].decode(x)
+        ts.append(time.perf_counter() - t0)
+    res["host_call_us_median"] = 1e6 * statistics.median(ts)
+    res["host_call_note"] = ("omh_gdn_decode(li, 1, x, out) with host x/out: H2D copy, the 3 launches, D2H copy, "
+                             "stream sync; wall clock per call from Python, median of 200")
+    log(f"host-pointer omh_gdn_decode(li, 1, ...): {res['host_call_us_median']:.1f} us per call")
     for L in lays:
         L.free()
     hip.device_synchronize()
-    return fused, engine, sweep, alg_bytes, R
+    return res
+
+
+def bench_prefill_block(hip, gdn, synth, T, steps, warmup):
+    """Row f2 at prefill size: the whole GDN layer (int8 in_proj 2048 -> 12352
+    with fp32 b/a rows, core, int8 out_proj 4096 -> 2048) over T tokens of
+    one sequence, and the core alone on the same layer; the difference is
+    the two projections (with their x-split launches)."""
+    from overhang_amd.dims import Q35B
+    d = Q35B
+    w = quantized(synth.layer_weights(d, 6))
+    L = gdn.GdnLayer(2200, d, w, max_seqs=1)
+    x = hip.Buffer.from_numpy(synth.normal(10, synth.S_X, (T, d.hidden), 0.0, 1.0))
+    out = hip.Buffer(T * d.hidden * 4)
+    st = hip.Stream()
+    el, _, _ = time_launches(hip, st, lambda k: gdn.prefill_dev(L.li, 0, T, x, out, stream=st), steps, warmup)
+    t_layer = el / steps
+    inp = synth.core_inputs(d, T, 11)
+    dev = {k: hip.Buffer.from_numpy(v) for k, v in inp.items()}
+    core = hip.Buffer(T * d.val_dim * 4)
+    el2, _, _ = time_launches(hip, st, lambda k: gdn.prefill_core_dev(L.li, 0, T, dev["qkv"], dev["z"], dev["a"],
+                                                                       dev["b"], core, stream=st), steps, warmup)
+    t_core = el2 / steps
+    L.free()
+    t_proj = t_layer - t_core
+    macs = T * (d.hidden * (d.conv_dim + d.val_dim + 2 * d.vh) + d.val_dim * d.hidden)
+    tf = 2 * macs / t_proj / 1e12
+    res = {"T": T, "us_layer": 1e6 * t_layer, "us_core": 1e6 * t_core, "us_projections": 1e6 * t_proj,
+           "tok_s_layer": T / t_layer, "proj_flops": 2 * macs, "proj_TFLOPs": tf,
+           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
+                        "frac": tf / BF16_MFMA_TFLOPS,
+                        "basis": "algorithmic int8 x fp32 MACs of both projections x 2, against the dense bf16 "
+                                 "MFMA peak (the matrix cores the int8 rows run on)"},
+           "note": "35B GDN layer, int8 [qkv|z] in_proj + fp32 b/a rows, int8 out_proj; projections = "
+                   "whole-layer prefill minus core-only prefill on the same layer"}
+    log(f"prefill block T={T}: layer {1e6 * t_layer:.0f} us, core {1e6 * t_core:.0f} us, projections "
+        f"{1e6 * t_proj:.0f} us = {tf:.0f} TFLOP/s")
+    return res
 
 
 def copy_probe(hip, nbytes, steps, warmup):
@@ -448,13 +566,48 @@ def cpu_decode_baseline(synth, budget_s=10.0):
 
 
 def cpu_model() -> str:
+    """lscpu's model name, sockets x cores, and the threads this process may use."""
+    import subprocess
+    model, info = "unknown", {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info[k.strip()] = v.strip()
+        model = info.get("Model name", model)
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    return (f"{model}; {info.get('Socket(s)', '?')} socket(s) x {info.get('Core(s) per socket', '?')} cores, "
+            f"{info.get('CPU(s)', '?')} CPUs; nproc {len(os.sched_getaffinity(0))}")
+
+
+def cpu_reference_layer(synth, budget_s=10.0):
+    """The reference's own deltanet_step (engines/qwen.c:301-364, compiled
+    from the reference sources into oracle/_ref with the reference's flags)
+    on the whole GDN layer at the 35B shape with int8 projections, one token
+    per call as the engine runs it; tok/s for 30 such layers."""
+    import oracle
+    from overhang_amd.dims import Q35B
+    if oracle.ref_lib() is None:
+        return None
+    d = Q35B
+    R = oracle.RefLayer(d, synth.layer_weights(d, 5), int8=True)
+    x = synth.normal(9, synth.S_X, (1, d.hidden), 0.0, 1.0)
+    R.steps(x)
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < 5 or time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        R.steps(x)
+        ts.append(time.perf_counter() - t0)
+    R.close()
+    med = statistics.median(ts)
+    return {"value": 1.0 / (N_LAYERS * med), "unit": "tok/s", "cores": oracle.threads(), "kind": "reference",
+            "ms_per_layer": 1e3 * med,
+            "sample": f"{len(ts)} tokens through one whole GDN layer (int8 in/out projections, 35B shape) "
+                      f"with the reference deltanet_step; tok/s = 1 / (30 x median per-layer time)",
+            "cpu_model": cpu_model()}
 
 
 def committed_traffic(kernel: str):
@@ -475,10 +628,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn"), default="all",
+    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn", "engine", "proj"),
+                    default="all",
                     help="decode: the headline only (for profiling); prefill: the T=4096 and T=32768 "
                          "prefills only; block: the config 5 int8 block at B=64 only; attn: the gated "
-                         "attention layer's decode token at 32768 positions only")
+                         "attention layer's decode token at 32768 positions only; engine: the 30-layer "
+                         "whole-block B=1 chain in a HIP graph; proj: the T=4096 int8 layer prefill")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN layer needs no collectives and this build "
@@ -496,14 +651,23 @@ def main():
         print(json.dumps({"attn_decode_n32768": bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)}),
               flush=True)
         return
+    if a.part == "engine":
+        print(json.dumps({"engine_block_B1": bench_engine_block(hip, gdn, synth, a.steps, a.warmup)}), flush=True)
+        return
+    if a.part == "proj":
+        print(json.dumps({"prefill_block_int8_T4096": bench_prefill_block(hip, gdn, synth, 4096, max(a.steps // 5, 3),
+                                                                          a.warmup)}), flush=True)
+        return
     if a.part == "block":
         print(json.dumps({"block_int8_B64": bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)}),
               flush=True)
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = warm = block = attn = snap = None
+    pre = warm = block = attn = snap = eng = preb = None
     if a.part == "all":
+        eng = bench_engine_block(hip, gdn, synth, a.steps, a.warmup)
+        preb = bench_prefill_block(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
         attn = bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)
         snap = bench_snapshot(hip, gdn, synth, max(a.steps // 2, 10), a.warmup)
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
@@ -516,6 +680,11 @@ def main():
         log("cpu baseline (oracle, OpenMP) ...")
         cpu = cpu_decode_baseline(synth)
         log(f"cpu baseline: {cpu['value']:.1f} tok/s on {cpu['cores']} threads")
+        cpu_ref = cpu_reference_layer(synth)
+        if cpu_ref is not None:
+            log(f"cpu reference deltanet_step (whole layer, int8): {cpu_ref['ms_per_layer']:.1f} ms per layer")
+            if eng is not None:
+                eng["cpu_baseline"] = cpu_ref
         if pre is not None:
             pre["cpu_baseline"] = cpu_prefill_baseline(synth)
             log(f"cpu prefill baseline: {pre['cpu_baseline']['value']:.1f} tok/s")
@@ -553,6 +722,8 @@ def main():
         "attn_decode_n32768": attn,
         "gdn_state_snapshot_30layers": snap,
         "decode_engine_order": engine,
+        "engine_block_B1": eng,
+        "prefill_block_int8_T4096": preb,
         "decode_batch_sweep": sweep,
     }
     print(json.dumps(line), flush=True)

@@ -76,6 +76,9 @@ def ref_lib():
         L.ref_quantize_rows.argtypes = [_f32p, _i8p, _f32p, C.c_int, C.c_int]
         L.ref_matmul_q.argtypes = [_f32p, _f32p, _i8p, _f32p, C.c_int, C.c_int]
         L.ref_matvec.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int]
+        L.ref_layer_open.argtypes = [C.c_int] * 6 + [C.c_float, C.c_int] + [_f32p] * 9
+        L.ref_layer_steps.argtypes = [C.c_int, _f32p, C.c_void_p]
+        L.ref_layer_close.argtypes = []
         L.ref_attn_run.argtypes = ([C.c_int] * 5 + [C.c_float, C.c_float, C.c_int] + [_f32p] * 6
                                    + [C.c_int, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, _f32p])
         _REF = L
@@ -222,3 +225,26 @@ def ref_attn_run(w, H, KV, hd, rot, theta, eps, pos0, Kpre, Vpre, x, int8: bool 
     if rc != 0:
         raise ValueError(f"ref_attn_run: {rc}")
     return out, Kn, Vn
+
+
+class RefLayer:
+    """The reference's deltanet_step on one persistent synthetic layer (set up
+    once: weights copied, int8 twins made with qw_make when int8), for timing
+    it the way the engine calls it: one token per call, state carried."""
+
+    def __init__(self, d, w, int8: bool = False):
+        R = ref_lib()
+        if R is None:
+            raise RuntimeError("oracle/_ref not built (reference sources absent at build time)")
+        self._keep = {k: _c(v) for k, v in w.items()}
+        k = self._keep
+        R.ref_layer_open(d.kh, d.vh, d.kd, d.vd, d.K, d.hidden, d.eps, int(int8), k["W_qkv"], k["W_z"],
+                         k["W_b"], k["W_a"], k["W_out"], k["conv_w"], k["A_log"], k["dt_bias"], k["gnorm"])
+        self.R, self.d = R, d
+
+    def steps(self, x, out=None):
+        x = _c(x)
+        self.R.ref_layer_steps(x.shape[0], x, None if out is None else out.ctypes.data)
+
+    def close(self):
+        self.R.ref_layer_close()

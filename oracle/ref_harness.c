@@ -134,3 +134,72 @@ int ref_attn_run(int hidden, int H, int KV, int hd, int rot, float theta, float 
     }
     return 0;
 }
+
+/* One persistent GDN layer for timing the reference's deltanet_step as the
+ * engine runs it: ref_layer_open sets up a synthetic Model/Layer (and, for
+ * stream != 0, its int8 twins via qw_make, qwen.c:269-274) once,
+ * ref_layer_steps runs T tokens through deltanet_step (one call each,
+ * carrying the state), ref_layer_close frees it.  One layer at a time. */
+static Model g_rm;
+static Layer g_rl;
+static float *g_rconv, *g_rrec, *g_rtmp;
+static int g_ropen;
+
+void ref_layer_close(void) {
+    if (!g_ropen) return;
+    free(g_rl.qkv); free(g_rl.z); free(g_rl.b); free(g_rl.a); free(g_rl.outp);
+    if (g_rm.stream) {
+        free(g_rl.Qqkv.q); free(g_rl.Qqkv.s); free(g_rl.Qz.q); free(g_rl.Qz.s);
+        free(g_rl.Qout.q); free(g_rl.Qout.s);
+    }
+    free(g_rconv); free(g_rrec); free(g_rtmp);
+    free(g_rm.conv_st); free(g_rm.rec_st);
+    g_ropen = 0;
+}
+
+int ref_layer_open(int kh, int vh, int kd, int vd, int K, int hidden, float eps, int stream,
+                   const float *W_qkv, const float *W_z, const float *W_b, const float *W_a,
+                   const float *W_out, const float *conv_w, const float *A_log,
+                   const float *dt_bias, const float *gnorm) {
+    ref_layer_close();
+    memset(&g_rm, 0, sizeof(g_rm));
+    memset(&g_rl, 0, sizeof(g_rl));
+    g_rm.c.hidden = hidden; g_rm.c.lin_kh = kh; g_rm.c.lin_vh = vh; g_rm.c.lin_kd = kd; g_rm.c.lin_vd = vd;
+    g_rm.c.conv_k = K; g_rm.c.eps = eps;
+    g_rm.stream = stream;
+    const int key_dim = kh * kd, val_dim = vh * vd, conv_dim = 2 * key_dim + val_dim;
+    float **dst[5] = {&g_rl.qkv, &g_rl.z, &g_rl.b, &g_rl.a, &g_rl.outp};
+    const float *src[5] = {W_qkv, W_z, W_b, W_a, W_out};
+    const int64_t nel[5] = {(int64_t)conv_dim * hidden, (int64_t)val_dim * hidden,
+                            (int64_t)vh * hidden, (int64_t)vh * hidden, (int64_t)hidden * val_dim};
+    for (int i = 0; i < 5; i++) {
+        *dst[i] = falloc(nel[i]);
+        memcpy(*dst[i], src[i], nel[i] * sizeof(float));
+    }
+    g_rl.conv_w = (float *)conv_w; g_rl.A_log = (float *)A_log; g_rl.dt_bias = (float *)dt_bias;
+    g_rl.gnorm = (float *)gnorm;
+    if (stream) {
+        g_rl.Qqkv = qw_make(&g_rl.qkv, conv_dim, hidden);
+        g_rl.Qz = qw_make(&g_rl.z, val_dim, hidden);
+        g_rl.Qout = qw_make(&g_rl.outp, hidden, val_dim);
+    }
+    g_rconv = falloc((int64_t)conv_dim * (K - 1));
+    g_rrec = falloc((int64_t)vh * kd * vd);
+    g_rtmp = falloc(val_dim > hidden ? val_dim : hidden);
+    g_rm.conv_st = malloc(sizeof(float *));
+    g_rm.rec_st = malloc(sizeof(float *));
+    g_rm.conv_st[0] = g_rconv;
+    g_rm.rec_st[0] = g_rrec;
+    g_ropen = 1;
+    return 0;
+}
+
+int ref_layer_steps(int T, const float *x, float *out) {
+    if (!g_ropen) return -2;
+    const int D = g_rm.c.hidden;
+    for (int t = 0; t < T; t++) {
+        deltanet_step(&g_rm, &g_rl, 0, x + (int64_t)t * D, g_rtmp);
+        if (out) memcpy(out + (int64_t)t * D, g_rtmp, D * sizeof(float));
+    }
+    return 0;
+}

@@ -41,6 +41,13 @@ def rt() -> C.CDLL:
         H.hipEventDestroy.argtypes = [vp]
         H.hipGetErrorString.restype = C.c_char_p
         H.hipGetErrorString.argtypes = [C.c_int]
+        H.hipStreamBeginCapture.argtypes = [vp, C.c_int]
+        H.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+        H.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, C.c_char_p, sz]
+        H.hipGraphLaunch.argtypes = [vp, vp]
+        H.hipGraphExecDestroy.argtypes = [vp]
+        H.hipGraphDestroy.argtypes = [vp]
+        H.hipGraphGetNodes.argtypes = [vp, vp, C.POINTER(sz)]
         _H = H
     return _H
 
@@ -126,3 +133,37 @@ class Event:
         ms = C.c_float()
         ok(rt().hipEventElapsedTime(C.byref(ms), self.h, end.h))
         return ms.value
+
+
+class Graph:
+    """Work enqueued on one stream by a Python callable, captured once into
+    a HIP graph (hipStreamCaptureModeThreadLocal) and replayed with
+    launch().  The callable must only enqueue kernels on that stream: no
+    allocation, no synchronisation, no memset nodes."""
+
+    def __init__(self, stream: Stream, fn):
+        H = rt()
+        ok(H.hipStreamBeginCapture(stream.cuda_stream, 1))
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = H.hipStreamEndCapture(stream.cuda_stream, C.byref(g))
+        ok(rc)
+        self.graph = g.value
+        n = C.c_size_t(0)
+        ok(H.hipGraphGetNodes(self.graph, None, C.byref(n)))
+        self.nodes = n.value
+        e = C.c_void_p()
+        ok(H.hipGraphInstantiate(C.byref(e), self.graph, None, None, 0))
+        self.exec = e.value
+        self.stream = stream
+
+    def launch(self) -> None:
+        ok(rt().hipGraphLaunch(self.exec, self.stream.cuda_stream))
+
+    def close(self) -> None:
+        if self.exec:
+            rt().hipGraphExecDestroy(self.exec)
+            rt().hipGraphDestroy(self.graph)
+            self.exec = self.graph = None
