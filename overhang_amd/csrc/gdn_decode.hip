@@ -253,6 +253,7 @@ __device__ __forceinline__ void load_head(float4 (&s)[RPT], const float *Sp, int
 struct PlaneOut {
     uint16_t *xb;
     int T, I;
+    bool i8;
 };
 
 // Columns col .. col+3 (= 4 * c4 of a head starting at a multiple of 64) of
@@ -282,6 +283,33 @@ __device__ __forceinline__ void write_planes(const PlaneOut &po, int tok, int co
     if (c4 % 16 == 0) reinterpret_cast<float *>(po.xb + 3 * plane)[(size_t)tok * (po.I / 64) + col / 64] = sm;
 }
 
+// The same columns as int8 planes with the scale of their 128-wide block
+// (i8_off layout, omh_i8_split): a block is 32 lanes with consecutive c4,
+// all active here (vd a multiple of 128).
+__device__ __forceinline__ void write_planes_i8(const PlaneOut &po, int tok, int col, int c4, float4 y) {
+    float m = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, OMH_WAVE));
+    const int E = omh_i8_exponent(m);
+    char4 a, b, c;
+    int8_t t1, t2, t3;
+    omh_i8_split(y.x, E, t1, t2, t3); a.x = t1; b.x = t2; c.x = t3;
+    omh_i8_split(y.y, E, t1, t2, t3); a.y = t1; b.y = t2; c.y = t3;
+    omh_i8_split(y.z, E, t1, t2, t3); a.z = t1; b.z = t2; c.z = t3;
+    omh_i8_split(y.w, E, t1, t2, t3); a.w = t1; b.w = t2; c.w = t3;
+    int8_t *X = reinterpret_cast<int8_t *>(po.xb);
+    const size_t plane = i8_plane_bytes(po.T, po.I), o = i8_off(col, tok, po.T);
+    *reinterpret_cast<char4 *>(X + o) = a;
+    *reinterpret_cast<char4 *>(X + plane + o) = b;
+    *reinterpret_cast<char4 *>(X + 2 * plane + o) = c;
+    if (c4 % 32 == 0) reinterpret_cast<float *>(X + kI8Planes * plane)[(size_t)(col / kI8Blk) * po.T + tok] = ldexpf(1.f, E);
+}
+
+__device__ __forceinline__ void write_x(const PlaneOut &po, int tok, int col, int c4, float4 y) {
+    if (po.i8) write_planes_i8(po, tok, col, c4, y);
+    else write_planes(po, tok, col, c4, y);
+}
+
 // Delta rule + gated norm of one value head of the workgroup.
 template <int KD, int VD, int RPT, int C4>
 __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *core, const float *s_q,
@@ -301,7 +329,7 @@ __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *
         const float4 y = gated(o, rn, gn, zz);
         *reinterpret_cast<float4 *>(core + c4 * 4) = y;
         if constexpr (VD % 64 == 0)
-            if (po.xb) write_planes(po, tok, col0 + c4 * 4, c4, y);
+            if (po.xb) write_x(po, tok, col0 + c4 * 4, c4, y);
     }
 }
 
@@ -404,7 +432,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     // the two reduction buffers, so a wave that runs ahead into the next
     // head never overwrites sums another wave is still reading.
     float *core = args.core + tok * vdim + (size_t)h0 * VD;
-    const PlaneOut po{args.xb, args.xb_T, vdim};
+    const PlaneOut po{args.xb, args.xb_T, vdim, args.xb_i8};
     for (int j = 0; j < rep; j += 2) {
         hc.gam = s_gam[j];
         hc.beta = s_beta[j];
@@ -517,7 +545,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
             const float4 y = gated(o, rn, gn, zz);
             *reinterpret_cast<float4 *>(core + c4 * 4) = y;
             if constexpr (VD % 64 == 0)
-                if (args.xb) write_planes(PlaneOut{args.xb, args.xb_T, vdim}, args.xb_t0 + b, h * VD + c4 * 4, c4, y);
+                if (args.xb) write_x(PlaneOut{args.xb, args.xb_T, vdim, args.xb_i8}, args.xb_t0 + b, h * VD + c4 * 4, c4, y);
         }
     } else {
         // Cross-slice exchange with device-coherent (agent-scope) relaxed
@@ -628,14 +656,14 @@ int decode_seqs_per_launch(int kd, int vd, int kh, int vh, int nl, int B, int va
     return (B + chunks - 1) / chunks;
 }
 
-bool decode_planes_supported(int vd, int variant) {
-    return vd % 64 == 0 && (variant == 0 || variant == kDecodePaired || variant == 1);
+bool decode_planes_supported(int vd, int variant, bool i8) {
+    return vd % (i8 ? kI8Blk : 64) == 0 && (variant == 0 || variant == kDecodePaired || variant == 1);
 }
 
 hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, hipStream_t st) {
     if (!decode_core_supported(kd, vd, a.vh / a.kh, a.K)) return hipErrorInvalidValue;
     if (a.rep != a.vh / a.kh) return hipErrorInvalidValue;
-    if (a.xb && (a.nl != 1 || !decode_planes_supported(vd, variant))) return hipErrorInvalidValue;
+    if (a.xb && (a.nl != 1 || !decode_planes_supported(vd, variant, a.xb_i8))) return hipErrorInvalidValue;
     if (variant == 0) variant = choose_variant(a, kd, vd);
     if (variant == kDecodePaired && a.vh / a.kh > kMaxRep) return hipErrorInvalidValue;
     if (kd == 16 && vd == 16) return launch_kd_vd<16, 16>(a, variant, st);

@@ -28,6 +28,9 @@
 //     fp32 rows run as extra workgroups of the int8 launch where they can.
 #include "omh_device.h"
 #include "omh_internal.h"
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 namespace omh {
@@ -267,8 +270,11 @@ __device__ __forceinline__ void proj_mfma_wg(const ProjArgs &p, int bx, int by) 
 #pragma unroll
     for (int tt = 0; tt < 4; tt++) acc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
     if (r0 < p.O) {
+        // (fp32 fragments are 4x the registers of int8 ones: batches of 2
+        // blocks, except for a single 16 x 16 tile, whose 8 blocks fit)
+        constexpr int PF32 = (RT == 1 && TT == 1) ? PF : (PF > 2 ? 2 : PF);
         if (r0 < p.n_q) mfma_tiles<TT, true, PF>(p, r0, t0, kbeg, klen, lane, acc);
-        else mfma_tiles<TT, false, (PF > 2 ? 2 : PF)>(p, r0, t0, kbeg, klen, lane, acc);
+        else mfma_tiles<TT, false, PF32>(p, r0, t0, kbeg, klen, lane, acc);
     }
     if (KS > 1) {
         if (ks > 0)
@@ -820,6 +826,293 @@ void proj_q8_wave_kernel(const ProjArgs p, int nb, const F32Part f) {
     }
 }
 
+// ------------------------------------------- int8 rows, int8 matrix cores
+// x as three int8 planes with a power-of-two scale per (token, 128-wide k
+// block) (i8_off layout, omh_i8_split), so every product is int8 x int8 on
+// v_mfma_i32_16x16x64_i8 and exact in int32: per block and plane a wave
+// sums q * p over the block's 128 k exactly, then combines the three planes
+// and the block scale in fp32, y += 2^E (A1 + (128 A2 + A3) 2^-14), and the
+// row scale multiplies at the end (qwen.c:116-121).  The one approximation is
+// x's representation, |x - x^| <= 2^-20 max|x| per block.  The weights go
+// into the matrix cores as they are stored: no conversion.
+//
+// A wave owns a 64-row x 16 TT-token output tile; each weight fragment
+// (16 rows x 64 k, 16 bytes per lane) feeds TT x 3 products, each x fragment
+// 4.  The 4 waves of a workgroup take consecutive k-subslices of the tile
+// and are summed through LDS in wave order; with few rows G workgroups split
+// k further (partial tiles + arrival counter, summed in order by the last).
+// Operands go straight from L2 / HBM into registers, one block ahead.  Tiles
+// are numbered token tile fastest and dealt out so that one XCD runs the
+// token tiles of a row group back to back: workgroups go to the XCDs in turn
+// (workgroup i to XCD i mod 8), so tile (i mod 8) * per + i / 8 keeps a row
+// group's weights in one L2.
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// x -> int8 planes with one scale per token (the power of two of the row's
+// max|x|, written into every block's scale entry): one workgroup per token
+// row, a float4 per thread per 1024 columns, read once (up to I = 4096 the
+// row stays in registers between the max and the split).  Workgroup 0 also
+// clears the k-split arrival counters.
+__global__ __launch_bounds__(256)
+void proj_split_i8_kernel(const float *__restrict__ x, int64_t ldx, int8_t *__restrict__ xb, int T, int I, int *cnt,
+                          int ncnt) {
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < ncnt; i += 256) cnt[i] = 0;
+    const int t = blockIdx.x;
+    if (t >= T) return;
+    constexpr int kRegs = 4;                                // float4s per thread kept in registers (I <= 4096)
+    __shared__ float s_m[4];
+    const float *xr = x + (size_t)t * ldx;
+    float4 v[kRegs];
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRegs; j++) {
+        const int k = 4 * threadIdx.x + 1024 * j;
+        v[j] = k < I ? *reinterpret_cast<const float4 *>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+    for (int k = 4 * threadIdx.x + 1024 * kRegs; k < I; k += 1024) {
+        const float4 u = *reinterpret_cast<const float4 *>(xr + k);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+    }
+#pragma unroll
+    for (int off = 1; off < OMH_WAVE; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, OMH_WAVE));
+    if (threadIdx.x % OMH_WAVE == 0) s_m[threadIdx.x / OMH_WAVE] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    const int E = omh_i8_exponent(m);
+    const size_t plane = i8_plane_bytes(T, I);
+    auto put = [&](int k, float4 u) __attribute__((always_inline)) {
+        char4 a, b, c;
+        int8_t t1, t2, t3;
+        omh_i8_split(u.x, E, t1, t2, t3); a.x = t1; b.x = t2; c.x = t3;
+        omh_i8_split(u.y, E, t1, t2, t3); a.y = t1; b.y = t2; c.y = t3;
+        omh_i8_split(u.z, E, t1, t2, t3); a.z = t1; b.z = t2; c.z = t3;
+        omh_i8_split(u.w, E, t1, t2, t3); a.w = t1; b.w = t2; c.w = t3;
+        const size_t o = i8_off(k, t, T);
+        *reinterpret_cast<char4 *>(xb + o) = a;
+        *reinterpret_cast<char4 *>(xb + plane + o) = b;
+        *reinterpret_cast<char4 *>(xb + 2 * plane + o) = c;
+    };
+#pragma unroll
+    for (int j = 0; j < kRegs; j++) {
+        const int k = 4 * threadIdx.x + 1024 * j;
+        if (k < I) put(k, v[j]);
+    }
+    for (int k = 4 * threadIdx.x + 1024 * kRegs; k < I; k += 1024) put(k, *reinterpret_cast<const float4 *>(xr + k));
+    const float sc = ldexpf(1.f, E);
+    for (int kb = threadIdx.x; kb < I / kI8Blk; kb += 256) reinterpret_cast<float *>(xb + kI8Planes * plane)[(size_t)kb * T + t] = sc;
+}
+
+constexpr int kI8Rows = 64;                 // rows of a wave's tile
+
+// PT: x has one scale per token (the split kernel's planes): a wave then
+// sums each plane exactly in int32 over its whole k range (|sum| <= 2^13 k
+// for plane values within [-64, 64]) and combines once at the end.  Else
+// (planes written per 128-wide head block by the decode core) the planes
+// and the block scale are combined after every block.
+template <int G, int TT, bool F32, bool PT>
+__global__ __launch_bounds__(4 * OMH_WAVE, 1)
+void proj_i8_kernel(const ProjArgs p, int nb, const F32Part f, int nrg, int ntt, int per) {
+    constexpr int RW = kI8Rows / 16, NTOK = 16 * TT, NP = kI8Planes;
+    constexpr int kTileFloats = kI8Rows * NTOK;
+    const int L = blockIdx.x;
+    const int ntiles = nrg * ntt;
+    if constexpr (F32) {
+        if (L >= 8 * per) {
+            const int i = L - 8 * per;
+            if (i < f.nwg) proj_mfma_wg<1, 1, 8>(f.p, i % f.gx, i / f.gx);
+            return;
+        }
+    }
+    const int tile = (L % 8) * per + L / 8;
+    if (tile >= ntiles) return;
+    const int rg = tile / ntt, tt0 = tile % ntt;
+    __shared__ v4f s_red[4][RW][TT][OMH_WAVE];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, gq = lane / 16;
+    const int r0 = rg * kI8Rows, t0 = tt0 * NTOK;
+    const int g = blockIdx.y;
+    const int kb0 = (g * 4 + w) * nb;                      // the wave's first 128-wide block
+    const int8_t *X = reinterpret_cast<const int8_t *>(p.xb);
+    const size_t plane = i8_plane_bytes(p.T, p.I), bstride = (size_t)i8_tiles(p.T) * 2048;
+    const float *scl = reinterpret_cast<const float *>(X + NP * plane);
+
+    const int8_t *wp[RW];
+    const int8_t *xp[TT];
+    const float *sp[TT];
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++) wp[rw] = p.Q + (size_t)min(r0 + 16 * rw + l16, p.O - 1) * p.I + 16 * gq;
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int u = min(t0 / 16 + tt, i8_tiles(p.T) - 1);       // token tile
+        xp[tt] = X + (size_t)u * 2048 + 16 * lane;
+        sp[tt] = scl + min(t0 + 16 * tt + l16, p.T - 1);
+    }
+
+    // one block's operands: weights [RW][2 halves], x [TT][NP][2], scales [TT]
+    v4i wq[2][RW][2], xq[2][TT][NP][2];
+    float sq[2][TT];
+    auto load = [&](int kb, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+#pragma unroll
+        for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                wq[sl][rw][h] = *reinterpret_cast<const v4i *>(wp[rw] + (size_t)kb * kI8Blk + 64 * h);
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    xq[sl][tt][pl][h] = *reinterpret_cast<const v4i *>(xp[tt] + pl * plane + kb * bstride + 1024 * h);
+            sq[sl][tt] = sp[tt][(size_t)kb * p.T];
+        }
+    };
+    v4f acc[RW][TT];
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) acc[rw][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4i ia[PT ? NP : 1][RW][TT];
+#pragma unroll
+    for (int pl = 0; pl < (PT ? NP : 1); pl++)
+#pragma unroll
+        for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) ia[pl][rw][tt] = v4i{0, 0, 0, 0};
+    auto compute = [&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        const v4i zero = {0, 0, 0, 0};
+        if constexpr (PT) {
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+                for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+                    for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+                        for (int h = 0; h < 2; h++)
+                            ia[pl][rw][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wq[sl][rw][h], xq[sl][tt][pl][h],
+                                                                                   ia[pl][rw][tt], 0, 0, 0);
+            return;
+        }
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++) {
+                v4i a[NP];
+#pragma unroll
+                for (int pl = 0; pl < NP; pl++) {
+                    a[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wq[sl][rw][0], xq[sl][tt][pl][0], zero, 0, 0, 0);
+                    a[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wq[sl][rw][1], xq[sl][tt][pl][1], a[pl], 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float lo = (float)(a[1][r] * 128 + a[2][r]);      // |.| <= 2^27: exact in int32
+                    const float v = fmaf(lo, 0x1p-14f, (float)a[0][r]);
+                    acc[rw][tt][r] = fmaf(v, sq[sl][tt], acc[rw][tt][r]);
+                }
+            }
+    };
+    // Two blocks per iteration, one block ahead, every load unconditional
+    // (the prefetch past the last block re-loads it): the loop body is
+    // straight-line and both edges into the loop header leave the same
+    // loads (slot 0) in flight, so the compiler's load-counter waits before
+    // each compute cover only that slot's loads instead of draining all.
+    const int kl = kb0 + nb - 1;
+    load(kb0, std::integral_constant<int, 0>{});
+#pragma unroll 1
+    for (int b = 0; b < nb; b += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(kb0 + b + 1, kl), std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(kb0 + b + 2, kl), std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(std::integral_constant<int, 1>{});
+    }
+
+    if constexpr (PT) {
+        // the token's scale (the same in every block entry)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            const float st = sp[tt][0];
+#pragma unroll
+            for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float lo = fmaf((float)ia[2][rw][tt][r], 0x1p-7f, (float)ia[1][rw][tt][r]);
+                    acc[rw][tt][r] = fmaf(lo, 0x1p-7f, (float)ia[0][rw][tt][r]) * st;
+                }
+        }
+    }
+
+    // the workgroup's 4 k-subslices, in wave order; wave w then finishes
+    // row tile w
+#pragma unroll
+    for (int rw = 0; rw < RW; rw++)
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) s_red[w][rw][tt][lane] = acc[rw][tt];
+    __syncthreads();
+    v4f y[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+        y[tt] = ((s_red[0][w][tt][lane] + s_red[1][w][tt][lane]) + s_red[2][w][tt][lane]) + s_red[3][w][tt][lane];
+
+    if constexpr (G > 1) {
+        float *mine = p.part + ((size_t)tile * G + g) * kTileFloats;
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            float *d = mine + ((w * TT + tt) * OMH_WAVE + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) __hip_atomic_store(d + r, y[tt][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);           // this thread's stores are complete
+        __syncthreads();
+        if (tid == 0) s_last = __hip_atomic_fetch_add(p.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+        __syncthreads();
+        if (!s_last) return;
+        v4f pt[G][TT];
+#pragma unroll
+        for (int gg = 0; gg < G; gg++)
+#pragma unroll
+            for (int tt = 0; tt < TT; tt++) {
+                const float *q = p.part + ((size_t)tile * G + gg) * kTileFloats + ((w * TT + tt) * OMH_WAVE + lane) * 4;
+#pragma unroll
+                for (int r = 0; r < 4; r++) pt[gg][tt][r] = __hip_atomic_load(q + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            y[tt] = pt[0][tt];
+#pragma unroll
+            for (int gg = 1; gg < G; gg++) y[tt] += pt[gg][tt];
+        }
+        if (tid == 0) __hip_atomic_store(p.cnt + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // lane holds rows 4gq .. 4gq+3 of row tile w for token l16 of token tile tt
+    const int o = r0 + 16 * w + 4 * gq;
+    if (o >= p.O) return;
+    const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int t = t0 + 16 * tt + l16;
+        if (t >= p.T) continue;
+        float4 v;
+        v.x = y[tt][0] * sc.x;
+        v.y = y[tt][1] * sc.y;
+        v.z = y[tt][2] * sc.z;
+        v.w = y[tt][3] * sc.w;
+        *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = v;
+    }
+}
+
 // Launch shape of the fp32-MFMA projection: one row tile per workgroup (k
 // split over its 4 waves) unless that leaves k-slices narrower than a
 // 64-wide block or far more workgroups than the device holds at once; a
@@ -909,6 +1202,337 @@ void launch_q8_wave(const ProjArgs &p, WvPlan w, const ProjArgs *f32, bool *f32_
     else launch_q8_wave_tt<1>(p, w.G, nb, f, with, grid, st);
 }
 
+// ---------------------------------------- int8 rows, streaming (T <= 64)
+// For decode-sized batches the projection is a stream of the weights from
+// HBM (25 MB for the 35B in_proj at 4.6 us), which needs megabytes of loads
+// in flight.  A workgroup owns RT row tiles (16 rows each) for all T tokens
+// and splits k over its 4 waves (and G workgroups); every wave requests all
+// of its weights (RT x NB blocks x 2 halves of 16 bytes per lane) before
+// anything else, then walks its k range block by block with x one block
+// ahead from L2 (x is per-token scaled: exact int32 sums over the range,
+// one fp32 combine at the end).  The grid is about one workgroup per CU.
+// PT as for proj_i8_kernel: per-token scales (split kernel) sum in int32 over
+// the whole range; per-block scales (planes the decode core wrote per head)
+// combine after every block.  The k split G is gridDim.y; the fp32 rows of
+// the projection, if any, are the first f.nwg workgroups of row y = 0 (first,
+// so they start at once instead of queueing behind the int8 tiles).
+template <int RT, int NT, int NB, bool PT>
+__global__ __launch_bounds__(4 * OMH_WAVE, 1)
+void proj_i8_stream_kernel(const ProjArgs p, const F32Part f) {
+    constexpr int NP = kI8Planes;
+    constexpr int kTileFloats = RT * 16 * NT * 16;
+    const int G = gridDim.y;
+    if ((int)blockIdx.x < f.nwg) {
+        if (blockIdx.y == 0) proj_mfma_wg<1, 1, 8>(f.p, blockIdx.x % f.gx, blockIdx.x / f.gx);
+        return;
+    }
+    __shared__ v4f s_red[4][RT][NT][OMH_WAVE];
+    __shared__ int s_last;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, gq = lane / 16;
+    const int rg = blockIdx.x - f.nwg, g = blockIdx.y;
+    const int r0 = rg * RT * 16;
+    const int kb0 = (g * 4 + w) * NB;                       // the wave's first 128-wide block
+    const int8_t *X = reinterpret_cast<const int8_t *>(p.xb);
+    const size_t plane = i8_plane_bytes(p.T, p.I), bstride = (size_t)i8_tiles(p.T) * 2048;
+    const float *scl = reinterpret_cast<const float *>(X + NP * plane);
+
+    // Every workgroup walks the same x pieces; in the same order they would
+    // all hit the same L2 channels at once.  So the walk starts at a
+    // workgroup-dependent token tile (rn) and block (rb): register slot nt
+    // holds token tile (nt + rn) % NT and slot b block (b + rb) % NB.
+    const int rn = rg % NT, rb = (rg / NT) % NB;
+    v4i wq[NB][RT][2];
+    const int8_t *xp[NT];
+    const float *sp[NT];
+    int tok[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int u = min((nt + rn) % NT, i8_tiles(p.T) - 1);     // token tile
+        tok[nt] = 16 * ((nt + rn) % NT) + l16;
+        xp[nt] = X + (size_t)u * 2048 + 16 * lane;
+        sp[nt] = scl + min(tok[nt], p.T - 1);
+    }
+    auto kblock = [&](int b) __attribute__((always_inline)) { return kb0 + (b + rb) % NB; };
+    // x in pieces of (block b, token tile nt), q = b NT + nt, in a ring of
+    // XR register slots, XR - 1 pieces ahead of the products
+    constexpr int NQ = NB * NT, XR = 3;          // (a deeper ring measured no faster)
+    v4i xq[XR][NP][2];
+    float xs[XR];
+    auto x_load = [&](auto qc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value, b = q / NT, nt = q % NT, sl = q % XR;
+#pragma unroll
+        for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                xq[sl][pl][h] = *reinterpret_cast<const v4i *>(xp[nt] + pl * plane + (size_t)kblock(b) * bstride + 1024 * h);
+        if constexpr (!PT) xs[sl] = sp[nt][(size_t)kblock(b) * p.T];
+    };
+    v4i ia[NP][RT][NT];
+    v4f acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            acc[rt][nt] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) ia[pl][rt][nt] = v4i{0, 0, 0, 0};
+        }
+    // (planes, rt, nt) combined into acc with scale st
+    auto combine = [&](int rt, int nt, float st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float lo = fmaf((float)ia[2][rt][nt][r], 0x1p-7f, (float)ia[1][rt][nt][r]);
+            acc[rt][nt][r] = fmaf(fmaf(lo, 0x1p-7f, (float)ia[0][rt][nt][r]), st, acc[rt][nt][r]);
+        }
+    };
+    // issue order (pinned by scheduling barriers, or the scheduler sinks
+    // each load next to its use and the waits drain everything in flight):
+    // the first x pieces, then all of the wave's weights block by block,
+    // then x XR - 1 pieces ahead of the products.  Loads retire in issue
+    // order, so the products of block b wait only for the weights up to b.
+    static_for<XR - 1>([&](auto qc) __attribute__((always_inline)) {
+        if constexpr (decltype(qc)::value < NQ) x_load(qc);
+    });
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int8_t *src = p.Q + (size_t)min(r0 + 16 * rt + l16, p.O - 1) * p.I + (size_t)kblock(b) * kI8Blk + 16 * gq;
+#pragma unroll
+            for (int h = 0; h < 2; h++) wq[b][rt][h] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src + 64 * h));
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<NQ>([&](auto qc) __attribute__((always_inline)) {
+        constexpr int q = decltype(qc)::value, b = q / NT, nt = q % NT, sl = q % XR;
+        if constexpr (q + XR - 1 < NQ) x_load(std::integral_constant<int, q + XR - 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    ia[pl][rt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        wq[b][rt][h], xq[sl][pl][h], (PT || h == 1) ? ia[pl][rt][nt] : v4i{0, 0, 0, 0}, 0, 0, 0);
+            if constexpr (!PT) combine(rt, nt, xs[sl]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (PT)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) combine(rt, nt, sp[nt][0]);
+    // the 4 k-subslices in wave order; wave w then finishes tiles w, w+4, ...
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) s_red[w][rt][nt][lane] = acc[rt][nt];
+    __syncthreads();
+    constexpr int NTILE = RT * NT, PER = (NTILE + 3) / 4;
+    v4f y[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int q = w + 4 * j;
+        if (q < NTILE)
+            y[j] = ((s_red[0][q / NT][q % NT][lane] + s_red[1][q / NT][q % NT][lane]) + s_red[2][q / NT][q % NT][lane]) +
+                   s_red[3][q / NT][q % NT][lane];
+    }
+    if (G > 1) {
+        float *mine = p.part + ((size_t)rg * G + g) * kTileFloats;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int q = w + 4 * j;
+            if (q >= NTILE) continue;
+            float *d = mine + ((size_t)q * OMH_WAVE + lane) * 4;
+#pragma unroll
+            for (int r = 0; r < 4; r++) __hip_atomic_store(d + r, y[j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) s_last = __hip_atomic_fetch_add(p.cnt + rg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+        __syncthreads();
+        if (!s_last) return;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int q = w + 4 * j;
+            if (q >= NTILE) continue;
+            v4f tsum;
+            for (int gg = 0; gg < G; gg++) {
+                const float *src = p.part + ((size_t)rg * G + gg) * kTileFloats + ((size_t)q * OMH_WAVE + lane) * 4;
+                v4f v;
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[r] = __hip_atomic_load(src + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                tsum = gg == 0 ? v : tsum + v;
+            }
+            y[j] = tsum;
+        }
+        if (tid == 0) __hip_atomic_store(p.cnt + rg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int q = w + 4 * j;
+        if (q >= NTILE) continue;
+        const int rt = q / NT, nt = q % NT;
+        const int o = r0 + 16 * rt + 4 * gq, t = 16 * ((nt + rn) % NT) + l16;
+        if (o >= p.O || t >= p.T) continue;
+        const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+        float4 v;
+        v.x = y[j][0] * sc.x;
+        v.y = y[j][1] * sc.y;
+        v.z = y[j][2] * sc.z;
+        v.w = y[j][3] * sc.w;
+        *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = v;
+    }
+}
+
+// Plan of the streaming kernel: T <= 64 tokens, RT row tiles per workgroup,
+// a k split over G workgroups, NB = 1, 2 or 4 blocks per wave.  Measured at
+// the 35B shapes (B = 64, weights from HBM): the launch should fill the
+// device in one round of workgroups (one per CU, 256, the fp32-row ones
+// included), and a k split or more rows per workgroup only pay where they
+// are needed for that.  So: the most workgroups up to 256, then the
+// smallest G, then the smallest RT.  rt = 0: not taken.  OMH_I8_RT /
+// OMH_I8_G restrict the choice (tuning).
+struct StPlan {
+    int rt, nt, nb, G;
+};
+constexpr int kCUs = 256;
+StPlan i8_stream_plan(int O, int T, int I, int nf32) {
+    StPlan best{0, 0, 0, 1};
+    if (T > 64 || I % (4 * kI8Blk) != 0) return best;
+    if (const char *e = getenv("OMH_I8_STREAM"))
+        if (e[0] == '0') return best;
+    const int want_rt = getenv("OMH_I8_RT") ? atoi(getenv("OMH_I8_RT")) : 0;
+    const int want_g = getenv("OMH_I8_G") ? atoi(getenv("OMH_I8_G")) : 0;
+    const int tiles = (O + 15) / 16, nblk = I / kI8Blk, nt = T <= 16 ? 1 : 4;
+    long best_wgs = 0;
+    for (int G = 1; G <= 8; G *= 2)
+        for (int rt = 1; rt <= 4; rt++) {
+            const int nb = nblk / (4 * G);
+            if (nb * 4 * G != nblk || (nb != 1 && nb != 2 && nb != 4)) continue;
+            if ((want_rt && rt != want_rt) || (want_g && G != want_g)) continue;
+            const long wgs = (long)(tiles + rt - 1) / rt * G + nf32;
+            if (wgs > kCUs || wgs <= best_wgs) continue;
+            best = StPlan{rt, nt, nb, G};
+            best_wgs = wgs;
+        }
+    return best;
+}
+
+template <int RT, int NT, int NB>
+void launch_stream_rt(const ProjArgs &p, const F32Part &f, dim3 grid, hipStream_t st) {
+    const dim3 blk(4 * OMH_WAVE);
+    if (p.x_split) hipLaunchKernelGGL((proj_i8_stream_kernel<RT, NT, NB, false>), grid, blk, 0, st, p, f);
+    else hipLaunchKernelGGL((proj_i8_stream_kernel<RT, NT, NB, true>), grid, blk, 0, st, p, f);
+}
+
+template <int NT>
+void launch_stream_nt(const ProjArgs &p, const StPlan &sp, const F32Part &f, dim3 grid, hipStream_t st) {
+#define OMH_ST(RT)                                                             \
+    if (sp.nb == 1) launch_stream_rt<RT, NT, 1>(p, f, grid, st);               \
+    else if (sp.nb == 2) launch_stream_rt<RT, NT, 2>(p, f, grid, st);          \
+    else launch_stream_rt<RT, NT, 4>(p, f, grid, st);
+    if (sp.rt == 1) { OMH_ST(1) } else if (sp.rt == 2) { OMH_ST(2) } else if (sp.rt == 3) { OMH_ST(3) } else { OMH_ST(4) }
+#undef OMH_ST
+}
+
+// The fp32 rows' workgroups beside the int8 ones: their one-token-tile shape
+// (proj_mfma_wg<1, 1, 8>) when it applies, else 0.
+int f32_beside(const ProjArgs *f32, F32Part *f) {
+    if (!f32) return 0;
+    const F32Plan fp = f32_plan(*f32);
+    if (!(fp.rt == 1 && fp.tpw == 16 && f32->I / 4 / 64 % 8 == 0)) return 0;
+    f->p = *f32;
+    f->gx = fp.grid.x;
+    f->nwg = fp.grid.x * fp.grid.y;
+    return f->nwg;
+}
+
+void launch_i8_stream(const ProjArgs &p, const StPlan &sp, const F32Part &f, hipStream_t st) {
+    const int nrg = ((p.O + 15) / 16 + sp.rt - 1) / sp.rt;
+    const dim3 grid(f.nwg + nrg, sp.G);
+    if (sp.nt == 1) launch_stream_nt<1>(p, sp, f, grid, st);
+    else launch_stream_nt<4>(p, sp, f, grid, st);
+}
+
+// Plan of the int8-core kernel for O int8 rows, T tokens, I inputs: tokens
+// per wave 16 TT with the largest TT (up to what T needs) that still gives
+// kI8Waves waves, then a k split over G workgroups while there are fewer
+// than kI8Waves waves and every wave keeps at least two 128-wide blocks.
+// TT = 0: the kernel does not take the shape (I not a multiple of 1024).
+// OMH_I8_TT / OMH_I8_G override the choice (tuning).
+constexpr int kI8Waves = 1024;
+WvPlan i8_plan(int O, int T, int I) {
+    WvPlan w{0, 1};
+    if (I % (4 * kI8Blk) != 0) return w;
+    const long rg = (O + kI8Rows - 1) / kI8Rows;
+    auto waves = [&](int tt) { return rg * ((T + 16 * tt - 1) / (16 * tt)) * 4; };
+    int tt = T <= 16 ? 1 : 2;                     // (a 64-token tile needs more registers than a wave has)
+    while (tt > 1 && waves(tt) < kI8Waves) tt /= 2;
+    if (const char *e = getenv("OMH_I8_TT")) tt = atoi(e) == 2 ? 2 : 1;
+    // (a wave's k range is an even number of 128-wide blocks: I % (1024 G) == 0)
+    if (I % (8 * kI8Blk) != 0) return w;
+    while (w.G < 8 && waves(tt) * w.G < kI8Waves && I % (8 * kI8Blk * 2 * w.G) == 0) w.G *= 2;
+    if (const char *e = getenv("OMH_I8_G")) {
+        const int gg = atoi(e);
+        if ((gg == 1 || gg == 2 || gg == 4 || gg == 8) && I % (8 * kI8Blk * gg) == 0) w.G = gg;
+    }
+    w.TT = tt;
+    return w;
+}
+
+// The projection variant for int8 rows with T > 4: the int8-core kernel
+// where it takes the shape, else the bf16 x 3 kernels (OMH_PROJ_Q8=bf16x3
+// selects those everywhere, for comparison).
+bool use_i8(int T, int I, int n_q) {
+    if (n_q <= 0 || T <= 4 || i8_plan(n_q, T, I).TT == 0) return false;
+    const char *e = getenv("OMH_PROJ_Q8");
+    return !(e && strcmp(e, "bf16x3") == 0);
+}
+
+template <int TT, bool PT>
+void launch_i8_tt(const ProjArgs &p, int G, int nb, const F32Part &f, bool with, dim3 grid, int nrg, int ntt,
+                  int per, hipStream_t st) {
+    const dim3 blk(4 * OMH_WAVE);
+    if (G == 1 && with) hipLaunchKernelGGL((proj_i8_kernel<1, TT, true, PT>), grid, blk, 0, st, p, nb, f, nrg, ntt, per);
+    else if (G == 1) hipLaunchKernelGGL((proj_i8_kernel<1, TT, false, PT>), grid, blk, 0, st, p, nb, f, nrg, ntt, per);
+    else if (G == 2) hipLaunchKernelGGL((proj_i8_kernel<2, TT, false, PT>), grid, blk, 0, st, p, nb, f, nrg, ntt, per);
+    else if (G == 4) hipLaunchKernelGGL((proj_i8_kernel<4, TT, false, PT>), grid, blk, 0, st, p, nb, f, nrg, ntt, per);
+    else hipLaunchKernelGGL((proj_i8_kernel<8, TT, false, PT>), grid, blk, 0, st, p, nb, f, nrg, ntt, per);
+}
+
+// The int8 rows of q by plan w; with f32 (the fp32 rows, n_q = 0) also
+// those, in the same launch, when they take the one-token-tile fp32 shape.
+void launch_i8(const ProjArgs &p, WvPlan w, const ProjArgs *f32, bool *f32_done, hipStream_t st) {
+    const int nb = p.I / (4 * kI8Blk * w.G);
+    const int nrg = (p.O + kI8Rows - 1) / kI8Rows, ntt = (p.T + 16 * w.TT - 1) / (16 * w.TT);
+    const int per = (nrg * ntt + 7) / 8;
+    F32Part f{};
+    bool with = false;
+    if (f32 && w.G == 1) {
+        const F32Plan fp = f32_plan(*f32);
+        with = fp.rt == 1 && fp.tpw == 16 && fp.grid.y > 1 && f32->I / 4 / 64 % 8 == 0;
+        if (with) {
+            f.p = *f32;
+            f.gx = fp.grid.x;
+            f.nwg = fp.grid.x * fp.grid.y;
+        }
+    }
+    *f32_done = with;
+    const dim3 grid(8 * per + (with ? f.nwg : 0), w.G);
+    // per-token scales unless the decode core wrote the planes (per head);
+    // the int32 sums stay in range for a wave's k range up to 1024 (2^23)
+    const bool pt = !p.x_split && p.I / (4 * w.G) <= 1024;
+    if (w.TT == 2 && pt) launch_i8_tt<2, true>(p, w.G, nb, f, with, grid, nrg, ntt, per, st);
+    else if (w.TT == 2) launch_i8_tt<2, false>(p, w.G, nb, f, with, grid, nrg, ntt, per, st);
+    else if (pt) launch_i8_tt<1, true>(p, w.G, nb, f, with, grid, nrg, ntt, per, st);
+    else launch_i8_tt<1, false>(p, w.G, nb, f, with, grid, nrg, ntt, per, st);
+}
+
 inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 struct XbLayout {
@@ -918,16 +1542,32 @@ struct XbLayout {
 };
 XbLayout xb_layout(int T, int I, int n_q) {
     XbLayout l{};
-    const size_t planes = (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float);
-    l.w = n_q > 0 ? q8_wave_plan(n_q, T, I) : WvPlan{0, 1};
-    const int ntok = 16 * (l.w.TT > 0 ? l.w.TT : 1);
-    const size_t tiles = (size_t)((n_q + kWvRows - 1) / kWvRows) * ((T + ntok - 1) / ntok);
+    const bool i8 = use_i8(T, I, n_q);
+    const size_t planes = i8 ? i8_planes_bytes(T, I)
+                             : (size_t)3 * T * I * sizeof(uint16_t) + (size_t)T * (I / 64) * sizeof(float);
+    l.w = n_q > 0 ? (i8 ? i8_plan(n_q, T, I) : q8_wave_plan(n_q, T, I)) : WvPlan{0, 1};
     l.part = (planes + 255) / 256 * 256;
-    const bool split = l.w.TT > 0 && l.w.G > 1;
-    const size_t npart = split ? tiles * l.w.G * kWvRows * ntok * sizeof(float) : 0;
+    // k-split partial tiles and arrival counters: enough for whichever
+    // kernel the launch picks (the wave kernel's plan, or the streaming one)
+    size_t npart = 0, ncnt = 0;
+    if (l.w.TT > 0 && l.w.G > 1) {
+        const int ntok = 16 * l.w.TT;
+        const size_t tiles = (size_t)((n_q + kWvRows - 1) / kWvRows) * ((T + ntok - 1) / ntok);
+        npart = tiles * l.w.G * kWvRows * ntok * sizeof(float);
+        ncnt = tiles;
+    }
+    if (i8)
+        for (int nf32 : {0, 16}) {          // (the plan may differ with fp32-row workgroups beside)
+            const StPlan sp = i8_stream_plan(n_q, T, I, nf32);
+            if (sp.rt > 0 && sp.G > 1) {
+                const size_t tiles = (size_t)(((n_q + 15) / 16 + sp.rt - 1) / sp.rt);
+                npart = std::max(npart, tiles * sp.G * (size_t)(sp.rt * 16 * sp.nt * 16) * sizeof(float));
+                ncnt = std::max(ncnt, tiles);
+            }
+        }
     l.cnt = l.part + npart;
-    l.ncnt = split ? (int)tiles : 0;
-    l.total = l.cnt + (size_t)l.ncnt * sizeof(int);
+    l.ncnt = (int)ncnt;
+    l.total = l.cnt + ncnt * sizeof(int);
     return l;
 }
 
@@ -956,6 +1596,8 @@ void launch_q8(const ProjArgs &p, hipStream_t st) {
 bool proj_supported(int I, int n_q) { return I >= 64 && I % 64 == 0 && n_q % 16 == 0; }
 
 size_t proj_xb_bytes(int T, int I, int n_q) { return xb_layout(T, I, n_q).total; }
+
+bool proj_x_int8_planes(int T, int I, int n_q) { return use_i8(T, I, n_q); }
 
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
     if (p.O <= 0 || p.T <= 0) return hipSuccess;
@@ -986,8 +1628,15 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         q.O = p.n_q;
         q.part = reinterpret_cast<float *>(reinterpret_cast<char *>(p.xb) + lay.part);
         q.cnt = reinterpret_cast<int *>(reinterpret_cast<char *>(p.xb) + lay.cnt);
+        const bool i8 = use_i8(p.T, p.I, p.n_q);
         // (planes written by the decode core: no split, unless counters need clearing)
-        if (!p.x_split || lay.ncnt > 0) {
+        if (i8 && !p.x_split) {
+            hipLaunchKernelGGL(proj_split_i8_kernel, dim3((unsigned)p.T), dim3(256), 0, st, p.x, p.ldx,
+                               reinterpret_cast<int8_t *>(p.xb), p.T, p.I, q.cnt, lay.ncnt);
+        } else if (i8 && lay.ncnt > 0) {
+            hipLaunchKernelGGL(proj_split_i8_kernel, dim3(1), dim3(256), 0, st, p.x, p.ldx,
+                               reinterpret_cast<int8_t *>(p.xb), 0, p.I, q.cnt, lay.ncnt);
+        } else if (!i8 && (!p.x_split || lay.ncnt > 0)) {
             const size_t n8 = (size_t)p.T * (p.I / 8);
             hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb,
                                p.T, p.I, q.cnt, lay.ncnt);
@@ -1000,7 +1649,14 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         f.scale = nullptr;
         bool f32_done = false;
         const bool done = lay.w.TT > 0;
-        if (done) launch_q8_wave(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
+        F32Part fs{};
+        const int nf32 = i8 ? f32_beside(p.O > p.n_q ? &f : nullptr, &fs) : 0;
+        const StPlan sp = i8 ? i8_stream_plan(q.O, p.T, p.I, nf32) : StPlan{0, 0, 0, 1};
+        if (sp.rt > 0) {
+            launch_i8_stream(q, sp, fs, st);
+            f32_done = nf32 > 0;
+        } else if (done && i8) launch_i8(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
+        else if (done) launch_q8_wave(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
         if (!done) {
             // enough workgroups for the device (a k split where rows are few)
             const int tb = (p.T + kQ8Tok - 1) / kQ8Tok;

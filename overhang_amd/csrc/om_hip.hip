@@ -135,7 +135,7 @@ int decode_variant() {
 // out_proj scratch's bf16 planes and block sums (DecodeArgs::xb)
 int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv, const float *z,
                 int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
-                hipStream_t st, uint16_t *planes = nullptr, int b0 = 0) {
+                hipStream_t st, uint16_t *planes = nullptr, int b0 = 0, bool planes_i8 = false) {
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
     for (int i = 0; i < nl; i++) {
         if (int rc = check_layer(lis[i])) return rc;
@@ -179,6 +179,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
             A.ld_qkv = ld_qkv; A.ld_z = ld_z; A.ld_ab = ld_ab;
             A.B = len; A.nl = n; A.kh = d.kh; A.vh = d.vh; A.rep = d.vh / d.kh; A.K = d.conv_k; A.eps = d.eps;
             A.xb = nl == 1 ? planes : nullptr;
+            A.xb_i8 = planes_i8;
             A.xb_T = B;
             A.xb_t0 = c0;
             A.b0 = b0 + c0;
@@ -235,8 +236,10 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     // the core writes out_proj's bf16 planes itself, saving the split launch
-    uint16_t *planes = xb && L.out_nq > 0 && decode_planes_supported(L.d.vd, decode_variant()) ? xb : nullptr;
-    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes)) return rc;
+    const bool i8 = proj_x_int8_planes(B, L.vdim, L.out_nq);
+    uint16_t *planes = xb && L.out_nq > 0 && decode_planes_supported(L.d.vd, decode_variant(), i8) ? xb : nullptr;
+    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes, 0, i8))
+        return rc;
     ProjArgs q{};
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = ds.xb_n; q.x_split = planes != nullptr;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;

@@ -68,3 +68,24 @@ __device__ __forceinline__ float4 f4_fma(float4 a, float s, float4 c) {
     return make_float4(fmaf(a.x, s, c.x), fmaf(a.y, s, c.y), fmaf(a.z, s, c.z), fmaf(a.w, s, c.w));
 }
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// x split into three int8 planes at the power-of-two scale 2^E of its block
+// (omh_internal.h, i8_off): p1 = rint(x 2^-E), then the remainder twice at
+// 7 more bits each.  With |x| < 2^(E+6) every p lies in [-64, 64], and each
+// remainder is exact in fp32 (it is a multiple of ulp(x) no wider than 23
+// bits), so |x - 2^E (p1 + p2 2^-7 + p3 2^-14)| <= 2^(E-15).
+__device__ __forceinline__ int omh_i8_exponent(float maxabs) {
+    if (!(maxabs > 0.f)) return 0;                        // all-zero block: every plane value is 0
+    const int e = ilogbf(maxabs) - 5;
+    return e < -120 ? -120 : e;
+}
+__device__ __forceinline__ void omh_i8_split(float x, int E, int8_t &p1, int8_t &p2, int8_t &p3) {
+    const float a = rintf(ldexpf(x, -E));
+    const float r1 = x - ldexpf(a, E);
+    const float b = rintf(ldexpf(r1, 7 - E));
+    const float r2 = r1 - ldexpf(b, E - 7);
+    const float c = rintf(ldexpf(r2, 14 - E));
+    p1 = (int8_t)(int)a;
+    p2 = (int8_t)(int)b;
+    p3 = (int8_t)(int)c;
+}

@@ -67,8 +67,9 @@ struct DecodeArgs {
     float eps;
     int rep;            // vh / kh
     int b0;             // token row b is sequence (state slot) b0 + b
-    uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's bf16 planes and block sums (xpiece; I = vh*vd)
+    uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's x: bf16 planes and block sums (xpiece) or, with xb_i8, int8 planes and block scales (i8_off); I = vh*vd
     int xb_T, xb_t0;    // the planes' token count, and the planes' token of row 0 of this launch
+    bool xb_i8;
     LayerPtrs L[kMaxDecodeLayers];
 };
 
@@ -90,6 +91,32 @@ __host__ __device__ inline size_t xpiece(int m, int t, int T, int I) {
     return ((size_t)(4 * full + m % 2) * T + t) * 32 + 8 * ((m % 8) / 2);
 }
 
+// Layout of x as int8 planes (the scratch of the int8 projections on the
+// int8 matrix cores).  Per token t and 128-wide k block b, with the power of
+// two 2^E[b][t] (E = ilogb(m) - 5 for the max |x| m over the block, or over
+// the token's whole row when one scale serves the row, so every plane value
+// lies in [-64, 64]):
+//     x = 2^E (p1 + p2 2^-7 + p3 2^-14) + r,   |r| <= 2^(E-15) <= 2^-20 m
+// (each step of the split is exact in fp32: omh_i8_split).  Each plane is
+// stored in MFMA operand order: the 16-token x 64-k operand of one
+// v_mfma_i32_16x16x64_i8 (block b, token tile u = t / 16, half h of the
+// block) is one contiguous 1 KiB run in lane order, lane l16 + 16 g holding
+// token 16u + l16 at k = 128b + 64h + 16g .. +15 (a wave's load of it is one
+// contiguous 1 KiB request).  Token tiles are padded to 16 (padding never
+// read into a result that is kept).  Plane p starts at byte p * i8_plane_bytes;
+// after the planes, the scales 2^E as fp32 [I/128][T].
+constexpr int kI8Blk = 128;
+constexpr int kI8Planes = 3;
+__host__ __device__ inline int i8_tiles(int T) { return (T + 15) / 16; }
+__host__ __device__ inline size_t i8_plane_bytes(int T, int I) { return (size_t)i8_tiles(T) * 16 * I; }
+__host__ __device__ inline size_t i8_off(int k, int t, int T) {
+    return ((((size_t)(k / kI8Blk) * i8_tiles(T) + t / 16) * 2 + (k % kI8Blk) / 64) * 4 + (k % 64) / 16) * 256 +
+           (t % 16) * 16 + k % 16;
+}
+__host__ __device__ inline size_t i8_planes_bytes(int T, int I) {
+    return (size_t)kI8Planes * i8_plane_bytes(T, I) + (size_t)(I / kI8Blk) * T * sizeof(float);
+}
+
 // y[t][o] = sum_i x[t][i] * W[o][i] for t < T, o < O.  Rows o < n_q come
 // from the int8 matrix Q (times scale[o]); rows o >= n_q from the fp32
 // matrix W (row o - n_q).  Either part may be empty.
@@ -103,12 +130,15 @@ struct ProjArgs {
     int T, I, O, n_q;
     uint16_t *xb;          // scratch for int8 rows with T > 4 (proj_xb_bytes), or null: x as three bf16 planes [3][T][I], fp32 sums over 64-wide k blocks [T][I/64], k-split partial tiles and arrival counters
     size_t xb_n;           // bytes at xb (launch_proj refuses a shape whose scratch does not fit)
-    bool x_split;          // the planes and block sums of x are already in xb (written by the decode core)
+    bool x_split;          // x is already in xb, in the layout the kernel takes (written by the decode core)
     float *part;           // (set by launch_proj from xb)
     int *cnt;
 };
 // bytes of the scratch a projection of T tokens over I inputs into n_q int8 rows uses
 size_t proj_xb_bytes(int T, int I, int n_q);
+// whether that projection takes x as int8 planes (i8_off layout) rather than
+// bf16 planes (xpiece layout): what a kernel writing x ahead must produce
+bool proj_x_int8_planes(int T, int I, int n_q);
 // hidden size I and int8 row count n_q the projection kernels take
 bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
@@ -178,7 +208,7 @@ constexpr int kDecodePaired = -1;
 hipError_t launch_decode_core(const DecodeArgs &args, int kd, int vd, int variant, hipStream_t st);
 bool decode_core_supported(int kd, int vd, int rep, int K);
 // whether a launch with this variant request can also write the out_proj planes (DecodeArgs::xb)
-bool decode_planes_supported(int vd, int variant);
+bool decode_planes_supported(int vd, int variant, bool i8);
 // sequences per launch for one layer's B sequences: B, or chunks that each fit one round of resident workgroups
 int decode_seqs_per_launch(int kd, int vd, int kh, int vh, int nl, int B, int variant);
 
