@@ -1627,19 +1627,23 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         ProjArgs q = p;
         q.O = p.n_q;
         q.part = reinterpret_cast<float *>(reinterpret_cast<char *>(p.xb) + lay.part);
-        q.cnt = reinterpret_cast<int *>(reinterpret_cast<char *>(p.xb) + lay.cnt);
+        // the caller's always-zero counters where they suffice, else counters
+        // in the scratch, cleared by the split launch (or a launch of its own)
+        const bool own = p.counters && lay.ncnt <= p.ncounters;
+        q.cnt = own ? p.counters : reinterpret_cast<int *>(reinterpret_cast<char *>(p.xb) + lay.cnt);
+        const int nclear = own ? 0 : lay.ncnt;
         const bool i8 = use_i8(p.T, p.I, p.n_q);
         // (planes written by the decode core: no split, unless counters need clearing)
         if (i8 && !p.x_split) {
             hipLaunchKernelGGL(proj_split_i8_kernel, dim3((unsigned)p.T), dim3(256), 0, st, p.x, p.ldx,
-                               reinterpret_cast<int8_t *>(p.xb), p.T, p.I, q.cnt, lay.ncnt);
-        } else if (i8 && lay.ncnt > 0) {
+                               reinterpret_cast<int8_t *>(p.xb), p.T, p.I, q.cnt, nclear);
+        } else if (i8 && nclear > 0) {
             hipLaunchKernelGGL(proj_split_i8_kernel, dim3(1), dim3(256), 0, st, p.x, p.ldx,
-                               reinterpret_cast<int8_t *>(p.xb), 0, p.I, q.cnt, lay.ncnt);
-        } else if (!i8 && (!p.x_split || lay.ncnt > 0)) {
+                               reinterpret_cast<int8_t *>(p.xb), 0, p.I, q.cnt, nclear);
+        } else if (!i8 && (!p.x_split || nclear > 0)) {
             const size_t n8 = (size_t)p.T * (p.I / 8);
             hipLaunchKernelGGL(proj_split_x_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, p.x, p.ldx, p.xb,
-                               p.T, p.I, q.cnt, lay.ncnt);
+                               p.T, p.I, q.cnt, nclear);
         }
         ProjArgs f = p;
         f.y = p.y + p.n_q;

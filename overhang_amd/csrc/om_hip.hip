@@ -73,6 +73,11 @@ struct Scratch {
     size_t n = 0;
 };
 Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre, g_xb, g_dec;
+// k-split arrival counters of the projections: zeroed once at init and
+// zero between launches (each tile's last arriver resets its own), shared
+// by every call (calls that may overlap must come from one stream)
+constexpr int kCounters = 1 << 18;
+int *g_counters = nullptr;
 
 int ensure(Scratch &s, size_t bytes) {
     if (bytes <= s.n) return OMH_OK;
@@ -222,14 +227,16 @@ int decode_full_args(int li, int B, const float *x, float *out) {
 }
 
 // The whole layer for B sequences with its scratch at `scr` (laid out as
-// decode_scratch(L, B) says); allocates nothing.
-int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, char *scr) {
+// decode_scratch(L, B) says) and ncnt always-zero k-split counters at cnt;
+// allocates nothing.
+int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, char *scr, int *cnt, int ncnt) {
     DevLayer &L = g_L[li];
     const int D = L.d.hidden;
     const DecodeScratch ds = decode_scratch(L, B);
     float *in = reinterpret_cast<float *>(scr + ds.in), *core = reinterpret_cast<float *>(scr + ds.core);
     uint16_t *xb = ds.xb_n ? reinterpret_cast<uint16_t *>(scr + ds.xb) : nullptr;
     ProjArgs p{};
+    p.counters = cnt; p.ncounters = ncnt;
     p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = ds.xb_n;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
@@ -241,6 +248,7 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
     if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes, 0, i8))
         return rc;
     ProjArgs q{};
+    q.counters = cnt; q.ncounters = ncnt;
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = ds.xb_n; q.x_split = planes != nullptr;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
@@ -250,7 +258,7 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
 int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
     if (int rc = decode_full_args(li, B, x, out)) return rc;
     if (int rc = ensure(g_dec, decode_scratch(g_L[li], B).total)) return rc;
-    return decode_full_on(li, B, x, out, st, static_cast<char *>(g_dec.p));
+    return decode_full_on(li, B, x, out, st, static_cast<char *>(g_dec.p), g_counters, kCounters);
 }
 
 // ---- the allocation-free decode entry point ----
@@ -260,6 +268,9 @@ int decode_full(int li, int B, const float *x, float *out, hipStream_t st) {
 // copy (on the host it is only a stand-in for the symbol): it uses the device
 // address hipGetSymbolAddress returns, fetched once per device.
 constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+// its first 64 KiB: the projections' k-split counters (zero at load, and
+// zero again after every launch: each tile's last arriver resets its own)
+constexpr size_t kNoAllocCounterBytes = size_t(64) << 10;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 char *g_scratch_dev[kMaxDevices];
@@ -322,6 +333,7 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     }
     float *in = static_cast<float *>(g_in.p), *core = static_cast<float *>(g_core.p);
     ProjArgs p{};
+    p.counters = g_counters; p.ncounters = kCounters;
     p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
     p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
@@ -329,6 +341,7 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
     if (int rc = prefill_core(li, seq, T, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st)) return rc;
     ProjArgs q{};
+    q.counters = g_counters; q.ncounters = kCounters;
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
     q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
@@ -389,6 +402,7 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     }
     float *rowb = static_cast<float *>(g_arow.p), *ctx = static_cast<float *>(g_actx.p);
     ProjArgs p{};
+    p.counters = g_counters; p.ncounters = kCounters;
     p.x = x; p.ldx = D; p.y = rowb; p.ldy = A.rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
     p.Q = A.Qin; p.scale = A.Sin; p.W = A.Win; p.T = T; p.I = D; p.O = A.rows; p.n_q = A.nq;
     HIP_OK(launch_proj(p, st));
@@ -405,6 +419,7 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     a.scale = 1.f / sqrtf((float)hd);                // qwen.c:405
     HIP_OK(launch_attn(a, hd, st));
     ProjArgs q{};
+    q.counters = g_counters; q.ncounters = kCounters;
     q.x = ctx; q.ldx = A.qdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
     q.Q = A.Qout; q.scale = A.Sout; q.W = A.Wout; q.T = T; q.I = A.qdim; q.O = D; q.n_q = A.out_nq;
     HIP_OK(launch_proj(q, st));
@@ -436,6 +451,11 @@ int omh_init(void) {
     }
     char *scr = nullptr;
     if (noalloc_scratch(&scr) != OMH_OK) return 0;        // the no-alloc scratch's device address
+    if (hipMalloc(&g_counters, kCounters * sizeof(int)) != hipSuccess ||
+        hipMemset(g_counters, 0, kCounters * sizeof(int)) != hipSuccess) {
+        fail(OMH_ERR_DEVICE, "projection counters: allocation failed");
+        return 0;
+    }
     g_ready = 1;
     return 1;
 }
@@ -684,13 +704,14 @@ int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream) 
 int omh_gdn_decode_noalloc_dev(int li, int B, const float *x, float *out, void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;
     if (int rc = decode_full_args(li, B, x, out)) return rc;
-    const size_t need = decode_scratch(g_L[li], B).total;
+    const size_t need = kNoAllocCounterBytes + decode_scratch(g_L[li], B).total;
     if (need > kNoAllocScratchBytes)
         return fail(OMH_ERR_SHAPE, "decode_noalloc: B=%d needs %zu bytes of scratch, above the %zu-byte static buffer",
                     B, need, kNoAllocScratchBytes);
     char *scr = nullptr;
     if (int rc = noalloc_scratch(&scr)) return rc;
-    return decode_full_on(li, B, x, out, static_cast<hipStream_t>(stream), scr);
+    return decode_full_on(li, B, x, out, static_cast<hipStream_t>(stream), scr + kNoAllocCounterBytes,
+                          reinterpret_cast<int *>(scr), (int)(kNoAllocCounterBytes / sizeof(int)));
 }
 
 int omh_gdn_decode(int li, int B, const float *x, float *out) {

@@ -131,6 +131,8 @@ struct ProjArgs {
     uint16_t *xb;          // scratch for int8 rows with T > 4 (proj_xb_bytes), or null: x as three bf16 planes [3][T][I], fp32 sums over 64-wide k blocks [T][I/64], k-split partial tiles and arrival counters
     size_t xb_n;           // bytes at xb (launch_proj refuses a shape whose scratch does not fit)
     bool x_split;          // x is already in xb, in the layout the kernel takes (written by the decode core)
+    int *counters;         // or null: k-split arrival counters that are zero between launches (each tile's
+    int ncounters;         //   last arriver resets its own), so no launch has to clear them
     float *part;           // (set by launch_proj from xb)
     int *cnt;
 };
