@@ -904,6 +904,80 @@ void proj_split_i8_kernel(const float *__restrict__ x, int64_t ldx, int8_t *__re
     for (int kb = threadIdx.x; kb < I / kI8Blk; kb += 256) reinterpret_cast<float *>(xb + kI8Planes * plane)[(size_t)kb * T + t] = sc;
 }
 
+// The same split for many tokens: one workgroup per 16-token tile.  First
+// each token's max |x| (wave w reads tokens 4w .. 4w+3, a float4 per lane
+// per 1024 columns); then every 1 KiB fragment of the tile (one 64-wide k
+// half-block, in i8_off order) is written whole by one wave, lane
+// (l16, g) splitting token l16's x at k = 64 j + 16 g .. +15 (the row
+// again, now from L2) into three 16-byte stores, so every store instruction
+// writes one contiguous 1 KiB run per plane.
+__global__ __launch_bounds__(256)
+void proj_split_i8_tile_kernel(const float *__restrict__ x, int64_t ldx, int8_t *__restrict__ xb, int T, int I) {
+    __shared__ int s_e[16];
+    const int u = blockIdx.x, lane = threadIdx.x % OMH_WAVE, w = threadIdx.x / OMH_WAVE;
+    {
+        const float *xr[4];
+        float m[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xr[i] = x + (size_t)min(16 * u + 4 * w + i, T - 1) * ldx;   // (padding tokens repeat the last one)
+            m[i] = 0.f;
+        }
+#pragma unroll 4
+        for (int k = 4 * lane; k < I; k += 4 * OMH_WAVE) {
+            float4 v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = *reinterpret_cast<const float4 *>(xr[i] + k);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                m[i] = fmaxf(m[i], fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int off = 1; off < OMH_WAVE; off <<= 1) m[i] = fmaxf(m[i], __shfl_xor(m[i], off, OMH_WAVE));
+            if (lane == 0) s_e[4 * w + i] = omh_i8_exponent(m[i]);
+        }
+    }
+    __syncthreads();
+    const int l16 = lane % 16, g = lane / 16;
+    const int t = min(16 * u + l16, T - 1), E = s_e[l16];
+    const float *xr = x + (size_t)t * ldx + 16 * g;
+    const size_t plane = i8_plane_bytes(T, I);
+    int8_t *dst = xb + (size_t)u * 2048 + 16 * lane;
+#pragma unroll 2
+    for (int j = w; j < I / 64; j += 4) {
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = *reinterpret_cast<const float4 *>(xr + 64 * j + 4 * q);
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        v4i a, b, c;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int8_t a4[4], b4[4], c4[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) omh_i8_split(v[4 * q + e], E, a4[e], b4[e], c4[e]);
+            a[q] = (int)(uint8_t)a4[0] | (int)(uint8_t)a4[1] << 8 | (int)(uint8_t)a4[2] << 16 | (int)((uint32_t)(uint8_t)a4[3] << 24);
+            b[q] = (int)(uint8_t)b4[0] | (int)(uint8_t)b4[1] << 8 | (int)(uint8_t)b4[2] << 16 | (int)((uint32_t)(uint8_t)b4[3] << 24);
+            c[q] = (int)(uint8_t)c4[0] | (int)(uint8_t)c4[1] << 8 | (int)(uint8_t)c4[2] << 16 | (int)((uint32_t)(uint8_t)c4[3] << 24);
+        }
+        // fragment (block j / 2, tile u, half j % 2)
+        const size_t o = (size_t)(j >> 1) * i8_tiles(T) * 2048 + (j & 1) * 1024;
+        *reinterpret_cast<v4i *>(dst + o) = a;
+        *reinterpret_cast<v4i *>(dst + plane + o) = b;
+        *reinterpret_cast<v4i *>(dst + 2 * plane + o) = c;
+    }
+    // the token scales, in every block's entry
+    const float sc = ldexpf(1.f, s_e[threadIdx.x % 16]);
+    float *scl = reinterpret_cast<float *>(xb + kI8Planes * plane);
+    for (int i = threadIdx.x; i < 16 * (I / kI8Blk); i += 256) {
+        const int tt = 16 * u + i % 16;
+        if (tt < T) scl[(size_t)(i / 16) * T + tt] = sc;
+    }
+}
+
 constexpr int kI8Rows = 64;                 // rows of a wave's tile
 
 // PT: x has one scale per token (the split kernel's planes): a wave then
@@ -1111,6 +1185,198 @@ void proj_i8_kernel(const ProjArgs p, int nb, const F32Part f, int nrg, int ntt,
         v.w = y[tt][3] * sc.w;
         *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = v;
     }
+}
+
+// ------------------------------------ int8 rows, prefill-sized T: GEMM
+// For hundreds of tokens and more the projection is a dense contraction
+// (the 35B in_proj at T = 4096: 3 x 103 G int8 multiply-adds with x as
+// three planes), bound by the int8 matrix cores if operands are reused from
+// LDS and registers rather than re-read from L2 by every wave.  A workgroup
+// of 8 waves owns a 256-row x 64-token output tile over the whole k range;
+// wave (wr, wt) = (w % 4, w / 4) the rows 64 wr .. +63 for the 32 tokens
+// 32 wt .. +31 and the three planes: 4 x 2 x 3 accumulators of
+// v_mfma_i32_16x16x64_i8, 96 int32 per lane, kept in VGPRs (two waves per
+// SIMD).  Per 64-wide k step the workgroup stages its 16 weight fragments
+// (16 rows x 64 k each, 16 KiB) and 12 x fragments (4 token tiles x 3
+// planes, 12 KiB, 1 KiB contiguous runs of the i8_off layout) from L2 / HBM
+// into one of three LDS stages, every fragment loaded once by one wave
+// (through registers, two steps ahead of its store), and each wave reads
+// its 4 weight and 6 x fragments (lane-contiguous 16 bytes: no bank
+// conflicts) one step ahead, while the current step's 24 products run, so
+// neither HBM nor LDS latency sits between two steps' products; one
+// barrier per step.  Every sum is exact in int32 (|sum| <= 64 x 127 x k <
+// 2^31 for k <= 2^25 / 127); the planes, the token's scale and the row
+// scale combine once at the end, as in proj_i8_kernel's per-token form.
+// Tiles go to the XCDs by token tile (XCD x takes token tiles x, x + 8, ..),
+// each XCD walking patches of 4 row blocks x its token tiles, so the
+// workgroups one XCD runs together share their weights and x in its L2.
+constexpr int kGmRows = 256, kGmTok = 64;
+constexpr int kGmWFrags = kGmRows / 16, kGmXFrags = kI8Planes * kGmTok / 16;   // fragments of one k step
+constexpr int kGmStage = (kGmWFrags + kGmXFrags) * 1024;                       // bytes of one LDS stage
+
+__global__ __launch_bounds__(8 * OMH_WAVE, 1)
+void proj_i8_gemm_kernel(const ProjArgs p, int nrb, int ntt) {
+    const int i = blockIdx.x, xcd = i % 8, j = i / 8;
+    const int nx = (ntt - xcd + 7) / 8;                      // token tiles of this XCD
+    if (j >= nx * nrb) return;
+    const int grp = j / (4 * nx), rem = j % (4 * nx);
+    const int gr = min(4, nrb - 4 * grp);                    // row blocks in this patch
+    const int rb = 4 * grp + rem % gr, tb = xcd + 8 * (rem / gr);
+
+    __shared__ __attribute__((aligned(16))) int8_t s_op[3 * kGmStage];   // [stage][W fragments | x fragments]
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int wr = w % 4, wt = w / 4;
+    const int l16 = lane % 16, gq = lane / 16;
+    const int R0 = rb * kGmRows, t0 = tb * kGmTok;
+    const int S = p.I / 64;                                  // k steps (even)
+    const int8_t *X = reinterpret_cast<const int8_t *>(p.xb);
+    const size_t plane = i8_plane_bytes(p.T, p.I), bstride = (size_t)i8_tiles(p.T) * 2048;
+    const float *scl = reinterpret_cast<const float *>(X + kI8Planes * plane);
+
+    // The loads of one step: wave w copies weight fragments 2w, 2w + 1 (rows
+    // R0 + 16 f + l16 at k = 64 s + 16 gq .. +15, buffer loads with the step in
+    // the scalar offset) and x fragments w and w + 8 (< 12) of the step
+    // (fragment f = 4 plane + token tile).
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.Q), 0, (int)((size_t)p.O * p.I), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(X), 0, (int)(kI8Planes * plane), 0x00020000);
+    int wv[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++) wv[f] = min(R0 + 16 * (2 * w + f) + l16, p.O - 1) * p.I + 16 * gq;
+    const bool x2 = w + 8 < kGmXFrags;
+    int xv[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++) {
+        const int fr = min(w + 8 * f, kGmXFrags - 1), pl = fr / 4, tt = fr % 4;
+        xv[f] = (int)(pl * plane) + min(t0 / 16 + tt, i8_tiles(p.T) - 1) * 2048 + 16 * lane;
+    }
+    int8_t *const lbase = s_op + 16 * lane;
+
+    v4i ld[2][4];                   // [slot][W 0, W 1, x 0, x 1]: one step's loads on their way into LDS
+    auto load = [&](int s, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        s = min(s, S - 1);
+        const int so = 64 * s, xo = (int)((s >> 1) * bstride) + (s & 1) * 1024;
+#pragma unroll
+        for (int f = 0; f < 2; f++) ld[sl][f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[f], so, 0));
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+            ld[sl][2 + f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[f], xo, 0));
+    };
+    auto put = [&](int stage, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        int8_t *st = lbase + stage * kGmStage;
+#pragma unroll
+        for (int f = 0; f < 2; f++) *reinterpret_cast<v4i *>(st + (2 * w + f) * 1024) = ld[sl][f];
+        *reinterpret_cast<v4i *>(st + (kGmWFrags + w) * 1024) = ld[sl][2];
+        if (x2) *reinterpret_cast<v4i *>(st + (kGmWFrags + w + 8) * 1024) = ld[sl][3];
+    };
+    v4i fr[2][4 + 2 * kI8Planes];   // [slot][W rows 0..3, x (token tile, plane)]: one step's operands
+    auto get = [&](int stage, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        const int8_t *st = lbase + stage * kGmStage;
+#pragma unroll
+        for (int rw = 0; rw < 4; rw++) fr[sl][rw] = *reinterpret_cast<const v4i *>(st + (4 * wr + rw) * 1024);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int pl = 0; pl < kI8Planes; pl++)
+                fr[sl][4 + kI8Planes * tt + pl] = *reinterpret_cast<const v4i *>(st + (kGmWFrags + 4 * pl + 2 * wt + tt) * 1024);
+    };
+
+    v4i acc[kI8Planes][4][2];       // [plane][row fragment][token tile]
+#pragma unroll
+    for (int pl = 0; pl < kI8Planes; pl++)
+#pragma unroll
+        for (int rw = 0; rw < 4; rw++)
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) acc[pl][rw][tt] = v4i{0, 0, 0, 0};
+    auto compute = [&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int rw = 0; rw < 4; rw++)
+#pragma unroll
+                for (int pl = 0; pl < kI8Planes; pl++)
+                    acc[pl][rw][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fr[sl][rw], fr[sl][4 + kI8Planes * tt + pl],
+                                                                            acc[pl][rw][tt], 0, 0, 0);
+    };
+    // Step s (register slot m = s % 2; LDS stage of step t: t % 3): the
+    // loads of step s + 3 go out, step s + 1's operands are read from its
+    // stage (published by the barrier that ended step s - 1), step s's
+    // products run from registers, then step s + 2's loads (requested in step
+    // s - 1) go into stage (s + 2) % 3, whose previous contents (step s - 1)
+    // were read during step s - 2, and a barrier publishes them.  Loads past
+    // the last step re-load it (unused), so every step's counts are the same.
+    int sc = 0, sn = 1, sw = 2;                              // stages of steps s, s + 1, s + 2
+    auto step = [&](int s, auto m_c) __attribute__((always_inline)) {
+        constexpr int m = decltype(m_c)::value;
+        load(s + 3, std::integral_constant<int, 1 - m>{});
+        get(sn, std::integral_constant<int, 1 - m>{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(std::integral_constant<int, m>{});
+        __builtin_amdgcn_sched_barrier(0);
+        put(sw, std::integral_constant<int, m>{});
+        __syncthreads();
+        const int t = sc;
+        sc = sn;
+        sn = sw;
+        sw = t;
+    };
+    load(0, std::integral_constant<int, 0>{});
+    load(1, std::integral_constant<int, 1>{});
+    put(0, std::integral_constant<int, 0>{});
+    put(1, std::integral_constant<int, 1>{});
+    load(2, std::integral_constant<int, 0>{});
+    __syncthreads();
+    get(0, std::integral_constant<int, 0>{});
+#pragma unroll 1
+    for (int s = 0; s < S; s += 2) {
+        step(s, std::integral_constant<int, 0>{});
+        step(s + 1, std::integral_constant<int, 1>{});
+    }
+
+    // lane holds rows 4gq .. 4gq+3 of row fragment rw for token l16 of token tile tt
+#pragma unroll
+    for (int tt = 0; tt < 2; tt++) {
+        const int t = t0 + 32 * wt + 16 * tt + l16;
+        const float st = scl[min(t, p.T - 1)];             // the token's scale (block 0's entry)
+#pragma unroll
+        for (int rw = 0; rw < 4; rw++) {
+            const int o = R0 + 64 * wr + 16 * rw + 4 * gq;
+            if (t >= p.T || o >= p.O) continue;
+            const float4 sc4 = *reinterpret_cast<const float4 *>(p.scale + o);
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float lo = fmaf((float)acc[2][rw][tt][r], 0x1p-7f, (float)acc[1][rw][tt][r]);
+                v[r] = fmaf(lo, 0x1p-7f, (float)acc[0][rw][tt][r]) * st;
+            }
+            *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) =
+                make_float4(v[0] * sc4.x, v[1] * sc4.y, v[2] * sc4.z, v[3] * sc4.w);
+        }
+    }
+}
+
+// The GEMM takes int8 rows with x split per token (not the decode core's
+// per-head planes), from kGmMinT tokens (OMH_I8_GEMM=0 / 1 overrides, for
+// tuning), with k a multiple of the loop body's two 64-wide steps.
+constexpr int kGmMinT = 256;
+bool use_i8_gemm(const ProjArgs &p) {
+    if (p.x_split || p.I % 128 != 0 || p.I > (1 << 25) / 127) return false;
+    // (buffer offsets are 32-bit)
+    if ((size_t)p.O * p.I >= (1u << 31) || kI8Planes * i8_plane_bytes(p.T, p.I) >= (1u << 31)) return false;
+    if (const char *e = getenv("OMH_I8_GEMM")) return e[0] == '1';
+    return p.T >= kGmMinT;
+}
+
+void launch_i8_gemm(const ProjArgs &p, hipStream_t st) {
+    const int nrb = (p.O + kGmRows - 1) / kGmRows, ntt = (p.T + kGmTok - 1) / kGmTok;
+    const int per = (ntt + 7) / 8 * nrb;                     // tiles of the XCD with the most
+    hipLaunchKernelGGL(proj_i8_gemm_kernel, dim3(8 * per), dim3(8 * OMH_WAVE), 0, st, p, nrb, ntt);
 }
 
 // Launch shape of the fp32-MFMA projection: one row tile per workgroup (k
@@ -1634,7 +1900,13 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         const int nclear = own ? 0 : lay.ncnt;
         const bool i8 = use_i8(p.T, p.I, p.n_q);
         // (planes written by the decode core: no split, unless counters need clearing)
-        if (i8 && !p.x_split) {
+        if (i8 && !p.x_split && p.T > 64) {
+            hipLaunchKernelGGL(proj_split_i8_tile_kernel, dim3((unsigned)i8_tiles(p.T)), dim3(256), 0, st, p.x, p.ldx,
+                               reinterpret_cast<int8_t *>(p.xb), p.T, p.I);
+            if (nclear > 0)
+                hipLaunchKernelGGL(proj_split_i8_kernel, dim3(1), dim3(256), 0, st, p.x, p.ldx,
+                                   reinterpret_cast<int8_t *>(p.xb), 0, p.I, q.cnt, nclear);
+        } else if (i8 && !p.x_split) {
             hipLaunchKernelGGL(proj_split_i8_kernel, dim3((unsigned)p.T), dim3(256), 0, st, p.x, p.ldx,
                                reinterpret_cast<int8_t *>(p.xb), p.T, p.I, q.cnt, nclear);
         } else if (i8 && nclear > 0) {
@@ -1659,7 +1931,8 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         if (sp.rt > 0) {
             launch_i8_stream(q, sp, fs, st);
             f32_done = nf32 > 0;
-        } else if (done && i8) launch_i8(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
+        } else if (i8 && use_i8_gemm(q)) launch_i8_gemm(q, st);
+        else if (done && i8) launch_i8(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
         else if (done) launch_q8_wave(q, lay.w, p.O > p.n_q ? &f : nullptr, &f32_done, st);
         if (!done) {
             // enough workgroups for the device (a k split where rows are few)

@@ -51,7 +51,7 @@ def test_batched_decode_block_matches_oracle(dims, int8, B):
     L.free()
 
 
-@pytest.mark.parametrize("T", [5, 64, 65, 200])
+@pytest.mark.parametrize("T", [5, 64, 65, 200, 300])
 def test_prefill_block_matches_oracle(T):
     d = CFG1
     seed = 9500 + T
@@ -155,14 +155,15 @@ def test_35b_block_drop_in_small_batch(B, int8):
     L.free()
 
 
-@pytest.mark.parametrize("T", [256, 1024])
+@pytest.mark.parametrize("T", [256, 333, 1024])
 def test_35b_int8_prefill_block_matches_oracle(T):
     """Row f2 at prefill size: the 35B-A3B int8 layer through
-    omh_gdn_prefill, whose projections run on the bf16 x 3 wave-tile kernel
-    (in_proj 2048 -> 12352, out_proj 4096 -> 2048), continuing from a nonzero
-    state.  Every token's output and the final state and conv history are
-    compared with the per-token oracle (engines/qwen.c:301-364 with
-    matmul_q, qwen.c:94-122)."""
+    omh_gdn_prefill, whose int8 projections (in_proj 2048 -> 12352 with the
+    fp32 b/a rows beside, out_proj 4096 -> 2048) run on the int8 matrix-core
+    GEMM from 256 tokens (T = 333: partial token tiles), continuing from a
+    nonzero state.  Every token's output and the final state and conv
+    history are compared with the per-token oracle (engines/qwen.c:301-364
+    with matmul_q, qwen.c:94-122)."""
     d = Q35B
     seed = 7300 + T
     w = synth.layer_weights(d, seed, gnorm_std=0.1)
@@ -183,3 +184,29 @@ def test_35b_int8_prefill_block_matches_oracle(T):
     assert_close(o1, ref1, what="decode after prefill out")
     assert_close(L.get_state(0)[1], Sref1, what="decode after prefill S")
     L.free()
+
+
+@pytest.mark.parametrize("shape,T", [((16, 32, 128, 128, 2048), 300), ((3, 6, 64, 64, 1024), 270)],
+                         ids=["35b-T300", "kh3-T270"])
+def test_int8_gemm_matches_wave_kernel(shape, T, monkeypatch):
+    """The prefill-sized int8 GEMM against the int8 wave-tile kernel it
+    replaces from 256 tokens (OMH_I8_GEMM forces either): both sum every
+    plane product exactly in int32, so the two layers agree to fp32
+    rounding of the plane combine (kh3: 1152 in_proj int8 rows, not a
+    multiple of the GEMM's 256-row tile; both: partial token tiles)."""
+    from overhang_amd.dims import GdnDims
+    kh, vh, kd, vd, hidden = shape
+    d = GdnDims(kh=kh, vh=vh, kd=kd, vd=vd, K=4, hidden=hidden)
+    seed = 7600 + T
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed)
+    x = _x(d, seed, (T,))
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("OMH_I8_GEMM", mode)
+        L = gdn.GdnLayer(new_li(), d, w, int8=True)
+        L.set_state(0, conv0, S0)
+        outs[mode] = (L.prefill(0, x), L.get_state(0)[1])
+        L.free()
+    assert_close(outs["1"][0], outs["0"][0], atol=2e-5, rtol=2e-5, what=f"{T} gemm vs wave out")
+    assert_close(outs["1"][1], outs["0"][1], atol=2e-5, rtol=2e-5, what=f"{T} gemm vs wave S")
