@@ -498,6 +498,49 @@ def bench_attn(hip, gdn, n, steps, warmup, nseq=8):
     return res
 
 
+def attn_prefill_flops(T, pos=0):
+    """Algorithmic flops of the causal attention core for T new tokens at
+    positions pos .. pos+T-1 (35B-A3B attention shape): per query head and
+    token t, 2 hd flops per visible key for q.k and 2 hd for p.v."""
+    D, H, KV, hd, rot = ATTN_SHAPE
+    keys = T * pos + T * (T + 1) / 2
+    return 4.0 * H * hd * keys
+
+
+def bench_attn_prefill(hip, gdn, T, steps, warmup):
+    """One prompt step of the gated full-attention layer at the 35B-A3B
+    attention shape: T tokens of one sequence at positions 0 .. T-1 through
+    omh_attn_forward_dev (int8 q/k/v/o projections, norm + RoPE + cache
+    write, causal attention, gate)."""
+    D, H, KV, hd, rot = ATTN_SHAPE
+    rng = np.random.default_rng(19)
+    w = {"W_q": rng.normal(0, 0.02, (2 * H * hd, D)).astype(np.float32),
+         "W_k": rng.normal(0, 0.02, (KV * hd, D)).astype(np.float32),
+         "W_v": rng.normal(0, 0.02, (KV * hd, D)).astype(np.float32),
+         "W_o": rng.normal(0, 0.02, (D, H * hd)).astype(np.float32),
+         "q_norm": rng.normal(0, 0.1, hd).astype(np.float32),
+         "k_norm": rng.normal(0, 0.1, hd).astype(np.float32)}
+    L = gdn.AttnLayer(4010, D, H, KV, hd, rot, 1e7, 1e-6, T, w, max_seqs=1, int8=True)
+    x = hip.Buffer.from_numpy(rng.normal(0, 1, (T, D)).astype(np.float32))
+    out = hip.Buffer(T * D * 4)
+    st = hip.Stream()
+
+    def one(k):
+        gdn.attn_forward_dev(L.li, 0, 0, T, x, out, stream=st)
+
+    el, _, _ = time_launches(hip, st, one, steps, warmup)
+    L.free()
+    t = el / steps
+    fl = attn_prefill_flops(T)
+    res = {"T": T, "us_per_call": 1e6 * t, "tok_s": T / t, "attn_flops": fl, "attn_TFLOPs_layer_time": fl / t / 1e12,
+           "note": "gated full-attention layer prompt step, T tokens from position 0, hidden 2048, 16 query / 2 kv "
+                   "heads of 256 (rot 64), int8 q/k/v/o projections; TFLOP/s = causal attention flops over the "
+                   "whole layer's time"}
+    log(f"attn prefill T={T}: {1e6 * t:.0f} us/call, {T / t:.3g} tok/s, attention {fl / t / 1e12:.1f} TFLOP/s "
+        f"over the layer time")
+    return res
+
+
 def bench_snapshot(hip, gdn, synth, steps, warmup):
     """Speculative-decoding snapshot of one sequence's GDN state across the
     30 GDN layers of the 35B shape copied device to device into a spare
@@ -651,12 +694,13 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn", "engine", "proj"),
+    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn", "attnp", "engine", "proj"),
                     default="all",
                     help="decode: the headline only (for profiling); prefill: the T=4096 and T=32768 "
                          "prefills only; block: the config 5 int8 block at B=64 only; attn: the gated "
                          "attention layer's decode token at 32768 positions only; engine: the 30-layer "
-                         "whole-block B=1 chain in a HIP graph; proj: the T=4096 int8 layer prefill")
+                         "whole-block B=1 chain in a HIP graph; proj: the T=4096 int8 layer prefill; attnp: the "
+                         "attention layer's T=4096 prompt step")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GDN layer needs no collectives and this build "
@@ -673,6 +717,10 @@ def main():
         return
     if a.part == "attn":
         print(json.dumps({"attn_decode_n32768": bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)}),
+              flush=True)
+        return
+    if a.part == "attnp":
+        print(json.dumps({"attn_prefill_T4096": bench_attn_prefill(hip, gdn, 4096, max(a.steps // 10, 3), 1)}),
               flush=True)
         return
     if a.part == "engine":

@@ -277,6 +277,163 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
 }
 #undef OMH_ATTN_LOAD_PIECE
 
+// ---------------------------------------------------------------- prompt steps
+// Flash attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32) for
+// prompt steps of at least kFlashMinT tokens: the same fp32 scores, online
+// softmax and P.V as the split kernel, as dense products.  A wave owns one
+// unit, 16 consecutive tokens of one query head; a workgroup of 8 waves
+// takes 8 units of one kv group (the group's heads of a token block, then
+// the next block), so the K and V tiles it stages in LDS (32 keys, double
+// buffered, HBM -> registers -> LDS one tile ahead) serve 8 waves.  Per
+// wave, S^T = K Q^T (A = a K row from LDS, B = the wave's q, held in
+// registers for the whole sweep), so each lane's scores belong to its own
+// query row (lane % 16): the row max and sum need two exchanges and the
+// rescale of the output is lane-local; O^T = V^T P^T (A = V from LDS, B =
+// the probabilities as the score product left them: key 16 n + 4 g + s of
+// lane group g is register s).  The head dims of q.k are taken in the order
+// 16 c + 4 g + s on both operands (one 16-byte K read per 4 products).  The
+// workgroups holding the most keys (the prompt's end) start first.  Keys
+// past a token's position are masked; rows of the last tile past the
+// visible keys repeat the tile's first row, so every LDS value is finite.
+template <int HD>
+struct FlashShape {
+    static constexpr int KT = 32;                  // keys per tile
+    static constexpr int LD = HD + 4;              // padded row in LDS (floats)
+    static constexpr int STAGE = 2 * KT * LD;      // one stage: K rows, then V rows
+    static constexpr size_t LDS = 2 * (size_t)STAGE * sizeof(float);
+    static constexpr int NC = HD / 16;             // 16-dim groups (q registers; output tiles)
+    static constexpr int PER = KT * HD / 4 / (8 * OMH_WAVE);   // float4 pieces of K (and of V) per thread
+};
+constexpr int kFlashMinT = 64;
+
+template <int HD>
+__global__ __launch_bounds__(8 * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_flash_kernel(const AttnArgs a) {
+    using F = FlashShape<HD>;
+    constexpr int KT = F::KT, LD = F::LD, NC = F::NC, PER = F::PER, NT = 8 * OMH_WAVE;
+    extern __shared__ float smem[];
+    const int H = a.H, KV = a.KV, grp = H / KV;
+    const int nunit = (a.T + 15) / 16 * grp, wpg = (nunit + 7) / 8;
+    const int g = blockIdx.x % KV, wi = wpg - 1 - (int)blockIdx.x / KV;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, gq = lane / 16;
+    const bool own = 8 * wi + w < nunit;
+    const int u = min(8 * wi + w, nunit - 1);
+    const int tb = u / grp, h = g * grp + u % grp;
+    const int tq = 16 * tb + l16;                  // this lane's query token (may be past T: not written)
+    const int tlast = min(16 * (min(8 * wi + 7, nunit - 1) / grp) + 15, a.T - 1);
+    const int nkeys = a.pos + tlast + 1;           // keys the workgroup's last token sees
+    const int kmax = a.pos + tq;                   // the last key this lane's token sees
+
+    omh_v4f q[NC];                                 // dims 16 c + 4 gq .. +3 of token tq
+    {
+        const float *qr = a.qb + ((size_t)min(tq, a.T - 1) * H + h) * HD + 4 * gq;
+#pragma unroll
+        for (int c = 0; c < NC; c++) q[c] = *reinterpret_cast<const omh_v4f *>(qr + 16 * c);
+    }
+    const size_t cache0 = ((size_t)a.seq * KV + g) * a.max_t;
+    const float *Kg = a.Kc + cache0 * HD, *Vg = a.Vc + cache0 * HD;
+    omh_v4f kr[PER], vr[PER];
+    auto load = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            const size_t off = (size_t)(kt + kk < nkeys ? kt + kk : kt) * HD + 4 * c;
+            kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + off);
+            vr[i] = *reinterpret_cast<const omh_v4f *>(Vg + off);
+        }
+    };
+    auto put = [&](int stage) __attribute__((always_inline)) {
+        float *Ks = smem + stage * F::STAGE, *Vs = Ks + KT * LD;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            *reinterpret_cast<omh_v4f *>(Ks + kk * LD + 4 * c) = kr[i];
+            *reinterpret_cast<omh_v4f *>(Vs + kk * LD + 4 * c) = vr[i];
+        }
+    };
+
+    omh_v4f o[NC];                                     // O^T: o[j][i] = O[token tq][dim 16 j + 4 gq + i]
+#pragma unroll
+    for (int j = 0; j < NC; j++) o[j] = omh_v4f{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    load(0);
+    put(0);
+    __syncthreads();
+    for (int kt = 0, st = 0; kt < nkeys; kt += KT, st ^= 1) {
+        if (kt + KT < nkeys) load(kt + KT);
+        const float *Ks = smem + st * F::STAGE, *Vs = Ks + KT * LD;
+        // S^T for keys kt + 16 n + 4 gq + i (register i of sc[n]), query row tq
+        omh_v4f sc[KT / 16];
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++) {
+            sc[n] = omh_v4f{0.f, 0.f, 0.f, 0.f};
+            const float *kp = Ks + (16 * n + l16) * LD + 4 * gq;
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const omh_v4f kf = *reinterpret_cast<const omh_v4f *>(kp + 16 * c);
+#pragma unroll
+                for (int s = 0; s < 4; s++) sc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], q[c][s], sc[n], 0, 0, 0);
+            }
+        }
+        // scores * hd^-1/2, causal mask, online softmax (qwen.c:410-414)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = kt + 16 * n + 4 * gq + i;
+                sc[n][i] = key <= kmax ? sc[n][i] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sc[n][i]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        const float mn = fmaxf(m, mx);             // finite: key 0 is in every token's first tile
+        const float corr = expf(m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sc[n][i] = expf(sc[n][i] - mn);
+                ps += sc[n][i];
+            }
+        ps += __shfl_xor(ps, 16, OMH_WAVE);
+        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        l = fmaf(l, corr, ps);
+        m = mn;
+        // O^T = corr O^T + V^T P^T (qwen.c:415-419)
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            o[j] = o[j] * corr;
+#pragma unroll
+            for (int n = 0; n < KT / 16; n++) {
+                const float *vp = Vs + (16 * n + 4 * gq) * LD + 16 * j + l16;
+#pragma unroll
+                for (int s = 0; s < 4; s++) o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vp[s * LD], sc[n][s], o[j], 0, 0, 0);
+            }
+        }
+        if (kt + KT < nkeys) put(st ^ 1);
+        __syncthreads();
+    }
+    // normalise and gate (qwen.c:420-421)
+    if (!own || tq >= a.T) return;
+    const float il = 1.f / l;
+    const float *gate = a.qkv + (size_t)tq * a.ld_qkv + (size_t)h * 2 * HD + HD + 4 * gq;
+    float *dst = a.ctx + ((size_t)tq * H + h) * HD + 4 * gq;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        const float4 gv = *reinterpret_cast<const float4 *>(gate + 16 * j);
+        float4 r;
+        r.x = o[j][0] * il * omh_sigmoid(gv.x);
+        r.y = o[j][1] * il * omh_sigmoid(gv.y);
+        r.z = o[j][2] * il * omh_sigmoid(gv.z);
+        r.w = o[j][3] * il * omh_sigmoid(gv.w);
+        *reinterpret_cast<float4 *>(dst + 16 * j) = r;
+    }
+}
+
 // One workgroup per (token, head, 64 columns): the CW waves take every
 // CW-th split, lane = column, then sum through LDS.
 constexpr int kCombineWaves = 8;
@@ -329,6 +486,18 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     if (!lds_ok) return hipErrorInvalidValue;
     static_assert(kAttnMaxGroup <= 4 * AttnShape<HD>::NW, "heads per wave");
     hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
+    if constexpr (HD >= 128) {
+        if (attn_uses_flash(a.T, HD)) {
+            static const bool flash_ok = hipFuncSetAttribute((const void *)attn_flash_kernel<HD>,
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                             (int)FlashShape<HD>::LDS) == hipSuccess;
+            if (!flash_ok) return hipErrorInvalidValue;
+            const int wpg = ((a.T + 15) / 16 * (a.H / a.KV) + 7) / 8;
+            hipLaunchKernelGGL((attn_flash_kernel<HD>), dim3((unsigned)(a.KV * wpg)), dim3(8 * OMH_WAVE),
+                               FlashShape<HD>::LDS, st, a);
+            return hipGetLastError();
+        }
+    }
     const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(AttnShape<HD>::NW * OMH_WAVE);
     const size_t lds = AttnShape<HD>::LDS;
     switch ((a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW) {
@@ -343,6 +512,12 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
 }
 
 }  // namespace
+
+bool attn_uses_flash(int T, int hd) {
+    if (const char *e = getenv("OMH_ATTN_FLASH"))
+        if (e[0] == '0') return false;
+    return T >= kFlashMinT && (hd == 128 || hd == 256);
+}
 
 bool attn_supported(int hd, int H, int KV, int rot) {
     return (hd == 32 || hd == 64 || hd == 128 || hd == 256) && KV >= 1 && H >= KV && H % KV == 0 &&

@@ -394,8 +394,10 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     if (int rc = ensure(g_arow, (size_t)T * A.rows * sizeof(float))) return rc;
     if (int rc = ensure(g_aqb, nth * hd * sizeof(float))) return rc;
     if (int rc = ensure(g_actx, nth * hd * sizeof(float))) return rc;
-    if (int rc = ensure(g_apo, nth * ns * hd * sizeof(float))) return rc;
-    if (int rc = ensure(g_apml, nth * ns * 2 * sizeof(float))) return rc;
+    if (!attn_uses_flash(T, hd)) {                    // (the flash kernel keeps no split partials)
+        if (int rc = ensure(g_apo, nth * ns * hd * sizeof(float))) return rc;
+        if (int rc = ensure(g_apml, nth * ns * 2 * sizeof(float))) return rc;
+    }
     uint16_t *xb = nullptr;
     if (T > 4 && (A.nq > 0 || A.out_nq > 0)) {
         const size_t xbn = std::max(proj_xb_bytes(T, D, A.nq), proj_xb_bytes(T, A.qdim, A.out_nq));

@@ -199,6 +199,8 @@ struct AttnArgs {
     float eps, scale;                  // RMSNorm eps, hd^-1/2
 };
 bool attn_supported(int hd, int H, int KV, int rot);
+// whether a prompt step of T tokens runs on the flash kernel (no split partials)
+bool attn_uses_flash(int T, int hd);
 // splits for pos + T visible keys: ns * KV * T >= 256 workgroups where the keys allow
 void attn_plan(int pos, int T, int KV, int &ns, int &kps);
 hipError_t launch_attn(const AttnArgs &a, int hd, hipStream_t st);

@@ -98,8 +98,12 @@ def test_tiny_teacher_forced_with_gpu_attention_prompt_step():
     assert got == exp, f"teacher-forced {sum(int(a == b) for a, b in zip(got, exp))}/28"
 
 
-@pytest.mark.parametrize("steps", [[1, 1, 1], [37, 1, 1], [200, 1, 64, 1]], ids=["decode", "prompt37", "prompt200"])
+@pytest.mark.parametrize("steps", [[1, 1, 1], [37, 1, 1], [200, 1, 64, 1], [37, 100, 1, 71]],
+                         ids=["decode", "prompt37", "prompt200", "prompt-after-prompt"])
 def test_35b_shape_prompt_then_decode(steps):
+    """Prompt steps of 64 tokens and more run on the flash kernel (fp32
+    matrix cores), shorter ones and decode steps on the split kernel; a
+    prompt step may start after earlier tokens (pos > 0)."""
     _run(Q35B_ATTN, steps)
 
 
