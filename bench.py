@@ -736,11 +736,12 @@ def main():
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = pre16 = warm = block = attn = snap = eng = preb = None
+    pre = pre16 = warm = block = attn = attnp = snap = eng = preb = None
     if a.part == "all":
         eng = bench_engine_block(hip, gdn, synth, a.steps, a.warmup)
         preb = bench_prefill_block(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
         attn = bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)
+        attnp = bench_attn_prefill(hip, gdn, 4096, 5, 1)
         snap = bench_snapshot(hip, gdn, synth, max(a.steps // 2, 10), a.warmup)
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
         pre16 = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup, math="bf16")
@@ -794,6 +795,7 @@ def main():
         "prefill_T32768_warm": warm,
         "block_int8_B64": block,
         "attn_decode_n32768": attn,
+        "attn_prefill_T4096": attnp,
         "gdn_state_snapshot_30layers": snap,
         "decode_engine_order": engine,
         "engine_block_B1": eng,

@@ -1196,179 +1196,243 @@ void proj_i8_kernel(const ProjArgs p, int nb, const F32Part f, int nrg, int ntt,
 // wave (wr, wt) = (w % 4, w / 4) the rows 64 wr .. +63 for the 32 tokens
 // 32 wt .. +31 and the three planes: 4 x 2 x 3 accumulators of
 // v_mfma_i32_16x16x64_i8, 96 int32 per lane, kept in VGPRs (two waves per
-// SIMD).  Per 64-wide k step the workgroup stages its 16 weight fragments
-// (16 rows x 64 k each, 16 KiB) and 12 x fragments (4 token tiles x 3
-// planes, 12 KiB, 1 KiB contiguous runs of the i8_off layout) from L2 / HBM
-// into one of three LDS stages, every fragment loaded once by one wave
-// (through registers, two steps ahead of its store), and each wave reads
-// its 4 weight and 6 x fragments (lane-contiguous 16 bytes: no bank
-// conflicts) one step ahead, while the current step's 24 products run, so
-// neither HBM nor LDS latency sits between two steps' products; one
-// barrier per step.  Every sum is exact in int32 (|sum| <= 64 x 127 x k <
-// 2^31 for k <= 2^25 / 127); the planes, the token's scale and the row
-// scale combine once at the end, as in proj_i8_kernel's per-token form.
+// SIMD).  Per 64-wide k step the workgroup's 16 weight fragments (16 rows x
+// 64 k, 16 KiB) and 12 x fragments (4 token tiles x 3 planes, 12 KiB, 1 KiB
+// contiguous runs of the i8_off layout) go from L2 / HBM straight into one
+// of four LDS stages (buffer loads to LDS, three steps ahead, each fragment
+// loaded once, by one wave), and each wave reads its 4 weight and 6 x
+// fragments (lane-contiguous 16 bytes: no bank conflicts) one step ahead,
+// while the current step's 24 products run.  One barrier per step: before
+// it each wave waits for its own copies into the stage the next step reads
+// ahead, so a stage is read only once every wave's copies into it have
+// landed, and it is refilled only after every wave has passed the barrier
+// that follows its last read.  Every sum is exact in int32 (|sum| <= 64 x
+// 127 x k < 2^31 for k <= 2^25 / 127); the planes, the token's scale and the
+// row scale combine once at the end, as in proj_i8_kernel's per-token form.
 // Tiles go to the XCDs by token tile (XCD x takes token tiles x, x + 8, ..),
 // each XCD walking patches of 4 row blocks x its token tiles, so the
 // workgroups one XCD runs together share their weights and x in its L2.
 constexpr int kGmRows = 256, kGmTok = 64;
 constexpr int kGmWFrags = kGmRows / 16, kGmXFrags = kI8Planes * kGmTok / 16;   // fragments of one k step
 constexpr int kGmStage = (kGmWFrags + kGmXFrags) * 1024;                       // bytes of one LDS stage
+constexpr int kGmWgs = 256;                                                    // resident workgroups (one per CU)
+#define OMH_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+
+// Persistent: workgroup b takes the tiles of blocks b, b + gridDim.x, ...
+// (block i: XCD i % 8, the XCD's i / 8-th tile, below), and its copy stream
+// runs on across tiles, so the next tile's first steps load while the
+// current one finishes and stores its outputs.
+__device__ __forceinline__ bool gemm_tile(int i, int nrb, int ntt, int &R0, int &t0) {
+    const int xcd = i % 8, j = i / 8;
+    const int nx = (ntt - xcd + 7) / 8;                      // token tiles of this XCD
+    if (j >= nx * nrb) return false;
+    const int grp = j / (4 * nx), rem = j % (4 * nx);
+    const int gr = min(4, nrb - 4 * grp);                    // row blocks in this patch
+    R0 = (4 * grp + rem % gr) * kGmRows;
+    t0 = (xcd + 8 * (rem / gr)) * kGmTok;
+    return true;
+}
 
 __global__ __launch_bounds__(8 * OMH_WAVE, 1)
 void proj_i8_gemm_kernel(const ProjArgs p, int nrb, int ntt) {
-    const int i = blockIdx.x, xcd = i % 8, j = i / 8;
-    const int nx = (ntt - xcd + 7) / 8;                      // token tiles of this XCD
-    if (j >= nx * nrb) return;
-    const int grp = j / (4 * nx), rem = j % (4 * nx);
-    const int gr = min(4, nrb - 4 * grp);                    // row blocks in this patch
-    const int rb = 4 * grp + rem % gr, tb = xcd + 8 * (rem / gr);
-
-    __shared__ __attribute__((aligned(16))) int8_t s_op[3 * kGmStage];   // [stage][W fragments | x fragments]
+    // four stages, separate arrays, so each stage's copies and reads are
+    // told apart by the compiler (its waits for this wave's copies into a
+    // stage then cover only that stage)
+    __shared__ __attribute__((aligned(16))) int8_t s_st0[kGmStage], s_st1[kGmStage], s_st2[kGmStage], s_st3[kGmStage];
     const int tid = threadIdx.x, lane = tid % OMH_WAVE;
     const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
     const int wr = w % 4, wt = w / 4;
     const int l16 = lane % 16, gq = lane / 16;
-    const int R0 = rb * kGmRows, t0 = tb * kGmTok;
-    const int S = p.I / 64;                                  // k steps (even)
+    const int S = p.I / 64;                                  // k steps per tile (a multiple of 4)
     const int8_t *X = reinterpret_cast<const int8_t *>(p.xb);
     const size_t plane = i8_plane_bytes(p.T, p.I), bstride = (size_t)i8_tiles(p.T) * 2048;
     const float *scl = reinterpret_cast<const float *>(X + kI8Planes * plane);
+    const int G = gridDim.x, b0 = blockIdx.x;
+    int NTL = 0;                                             // this workgroup's tiles
+    {
+        int r, t;
+        while (gemm_tile(b0 + G * NTL, nrb, ntt, r, t)) NTL++;
+    }
+    if (NTL == 0) return;
+    const int NG = NTL * S;                                  // k steps over all of its tiles
 
-    // The loads of one step: wave w copies weight fragments 2w, 2w + 1 (rows
-    // R0 + 16 f + l16 at k = 64 s + 16 gq .. +15, buffer loads with the step in
-    // the scalar offset) and x fragments w and w + 8 (< 12) of the step
-    // (fragment f = 4 plane + token tile).
+    // The copies of one step, 4 per wave: weight fragments 2w, 2w + 1 of the
+    // tile (rows R0 + 16 f .. +15 at k = 64 s .. +63: one contiguous 1 KiB
+    // run of the tiled copy; the step in the scalar offset) and x fragments
+    // w and w + 8 (fragment f = 4 plane + token tile; waves 4..7, with no
+    // second one, copy their first again).
+    const int nrf = (p.O + 15) / 16;                         // 16-row fragments of the tiled weights
     const __amdgpu_buffer_rsrc_t wrs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.Q), 0, (int)((size_t)p.O * p.I), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.Qt), 0, (int)(tile_q8_bytes(p.O, p.I)), 0x00020000);
     const __amdgpu_buffer_rsrc_t xrs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(X), 0, (int)(kI8Planes * plane), 0x00020000);
-    int wv[2];
-#pragma unroll
-    for (int f = 0; f < 2; f++) wv[f] = min(R0 + 16 * (2 * w + f) + l16, p.O - 1) * p.I + 16 * gq;
-    const bool x2 = w + 8 < kGmXFrags;
-    int xv[2];
+    int xf[2], xpl[2], xtt[2];
 #pragma unroll
     for (int f = 0; f < 2; f++) {
-        const int fr = min(w + 8 * f, kGmXFrags - 1), pl = fr / 4, tt = fr % 4;
-        xv[f] = (int)(pl * plane) + min(t0 / 16 + tt, i8_tiles(p.T) - 1) * 2048 + 16 * lane;
+        const int fr = w + 8 * f < kGmXFrags ? w + 8 * f : w;
+        xf[f] = kGmWFrags + fr;
+        xpl[f] = fr / 4;
+        xtt[f] = fr % 4;
     }
-    int8_t *const lbase = s_op + 16 * lane;
-
-    v4i ld[2][4];                   // [slot][W 0, W 1, x 0, x 1]: one step's loads on their way into LDS
-    auto load = [&](int s, auto slot_c) __attribute__((always_inline)) {
-        constexpr int sl = decltype(slot_c)::value;
-        s = min(s, S - 1);
-        const int so = 64 * s, xo = (int)((s >> 1) * bstride) + (s & 1) * 1024;
-#pragma unroll
-        for (int f = 0; f < 2; f++) ld[sl][f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[f], so, 0));
-#pragma unroll
-        for (int f = 0; f < 2; f++)
-            ld[sl][2 + f] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xrs, xv[f], xo, 0));
+    auto stage_of = [&](auto st_c) __attribute__((always_inline)) -> int8_t * {
+        constexpr int st = decltype(st_c)::value;
+        if constexpr (st == 0) return s_st0;
+        else if constexpr (st == 1) return s_st1;
+        else if constexpr (st == 2) return s_st2;
+        else return s_st3;
     };
-    auto put = [&](int stage, auto slot_c) __attribute__((always_inline)) {
-        constexpr int sl = decltype(slot_c)::value;
-        int8_t *st = lbase + stage * kGmStage;
+    // the next step of the workgroup's copy stream: tile ck, k step cs (past
+    // the end: the last step again, unused); the stream runs in order, so the
+    // tile's rows and tokens are worked out once per tile
+    int ck = 0, cs = 0, cR0 = 0, ct0 = 0;
+    gemm_tile(b0, nrb, ntt, cR0, ct0);
+    auto copy = [&](auto st_c) __attribute__((always_inline)) {
+        int8_t *dst = stage_of(st_c);
+        const int R0 = cR0, t0 = ct0, s = cs;
+        if (++cs == S) {
+            if (ck + 1 < NTL) {
+                cs = 0;
+                gemm_tile(b0 + G * ++ck, nrb, ntt, cR0, ct0);
+            } else {
+                cs = S - 1;
+            }
+        }
+        const int xo = (int)((s >> 1) * bstride) + (s & 1) * 1024;
 #pragma unroll
-        for (int f = 0; f < 2; f++) *reinterpret_cast<v4i *>(st + (2 * w + f) * 1024) = ld[sl][f];
-        *reinterpret_cast<v4i *>(st + (kGmWFrags + w) * 1024) = ld[sl][2];
-        if (x2) *reinterpret_cast<v4i *>(st + (kGmWFrags + w + 8) * 1024) = ld[sl][3];
+        for (int f = 0; f < 2; f++) {
+            const int wv = min(R0 / 16 + 2 * w + f, nrf - 1) * S * 1024 + 16 * lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, OMH_LDS(dst + (2 * w + f) * 1024), 16, wv, 1024 * s, 0, 0);
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            const int xv = (int)(xpl[f] * plane) + min(t0 / 16 + xtt[f], i8_tiles(p.T) - 1) * 2048 + 16 * lane;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, OMH_LDS(dst + xf[f] * 1024), 16, xv, xo, 0, 0);
+        }
     };
     v4i fr[2][4 + 2 * kI8Planes];   // [slot][W rows 0..3, x (token tile, plane)]: one step's operands
-    auto get = [&](int stage, auto slot_c) __attribute__((always_inline)) {
-        constexpr int sl = decltype(slot_c)::value;
-        const int8_t *st = lbase + stage * kGmStage;
+    // part 0: the weights and token tile 0's x; part 1: token tile 1's x
+    auto get = [&](auto st_c, auto slot_c, auto part_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value, part = decltype(part_c)::value;
+        const int8_t *st = stage_of(st_c) + 16 * lane;
+        if constexpr (part == 0)
 #pragma unroll
-        for (int rw = 0; rw < 4; rw++) fr[sl][rw] = *reinterpret_cast<const v4i *>(st + (4 * wr + rw) * 1024);
+            for (int rw = 0; rw < 4; rw++) fr[sl][rw] = *reinterpret_cast<const v4i *>(st + (4 * wr + rw) * 1024);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-            for (int pl = 0; pl < kI8Planes; pl++)
-                fr[sl][4 + kI8Planes * tt + pl] = *reinterpret_cast<const v4i *>(st + (kGmWFrags + 4 * pl + 2 * wt + tt) * 1024);
+        for (int pl = 0; pl < kI8Planes; pl++)
+            fr[sl][4 + kI8Planes * part + pl] = *reinterpret_cast<const v4i *>(st + (kGmWFrags + 4 * pl + 2 * wt + part) * 1024);
     };
 
     v4i acc[kI8Planes][4][2];       // [plane][row fragment][token tile]
+    auto zero = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int pl = 0; pl < kI8Planes; pl++)
-#pragma unroll
-        for (int rw = 0; rw < 4; rw++)
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++) acc[pl][rw][tt] = v4i{0, 0, 0, 0};
-    auto compute = [&](auto slot_c) __attribute__((always_inline)) {
-        constexpr int sl = decltype(slot_c)::value;
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int pl = 0; pl < kI8Planes; pl++)
 #pragma unroll
             for (int rw = 0; rw < 4; rw++)
 #pragma unroll
-                for (int pl = 0; pl < kI8Planes; pl++)
-                    acc[pl][rw][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fr[sl][rw], fr[sl][4 + kI8Planes * tt + pl],
-                                                                            acc[pl][rw][tt], 0, 0, 0);
+                for (int tt = 0; tt < 2; tt++) acc[pl][rw][tt] = v4i{0, 0, 0, 0};
     };
-    // Step s (register slot m = s % 2; LDS stage of step t: t % 3): the
-    // loads of step s + 3 go out, step s + 1's operands are read from its
-    // stage (published by the barrier that ended step s - 1), step s's
-    // products run from registers, then step s + 2's loads (requested in step
-    // s - 1) go into stage (s + 2) % 3, whose previous contents (step s - 1)
-    // were read during step s - 2, and a barrier publishes them.  Loads past
-    // the last step re-load it (unused), so every step's counts are the same.
-    int sc = 0, sn = 1, sw = 2;                              // stages of steps s, s + 1, s + 2
-    auto step = [&](int s, auto m_c) __attribute__((always_inline)) {
-        constexpr int m = decltype(m_c)::value;
-        load(s + 3, std::integral_constant<int, 1 - m>{});
-        get(sn, std::integral_constant<int, 1 - m>{});
-        __builtin_amdgcn_sched_barrier(0);
-        compute(std::integral_constant<int, m>{});
-        __builtin_amdgcn_sched_barrier(0);
-        put(sw, std::integral_constant<int, m>{});
-        __syncthreads();
-        const int t = sc;
-        sc = sn;
-        sn = sw;
-        sw = t;
+    auto compute = [&](auto slot_c, auto tt_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value, tt = decltype(tt_c)::value;
+#pragma unroll
+        for (int rw = 0; rw < 4; rw++)
+#pragma unroll
+            for (int pl = 0; pl < kI8Planes; pl++)
+                acc[pl][rw][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fr[sl][rw], fr[sl][4 + kI8Planes * tt + pl],
+                                                                        acc[pl][rw][tt], 0, 0, 0);
     };
-    load(0, std::integral_constant<int, 0>{});
-    load(1, std::integral_constant<int, 1>{});
-    put(0, std::integral_constant<int, 0>{});
-    put(1, std::integral_constant<int, 1>{});
-    load(2, std::integral_constant<int, 0>{});
-    __syncthreads();
-    get(0, std::integral_constant<int, 0>{});
-#pragma unroll 1
-    for (int s = 0; s < S; s += 2) {
-        step(s, std::integral_constant<int, 0>{});
-        step(s + 1, std::integral_constant<int, 1>{});
-    }
-
     // lane holds rows 4gq .. 4gq+3 of row fragment rw for token l16 of token tile tt
+    auto store = [&](int k) __attribute__((always_inline)) {
+        int R0, t0;
+        gemm_tile(b0 + G * k, nrb, ntt, R0, t0);
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++) {
-        const int t = t0 + 32 * wt + 16 * tt + l16;
-        const float st = scl[min(t, p.T - 1)];             // the token's scale (block 0's entry)
+        for (int tt = 0; tt < 2; tt++) {
+            const int t = t0 + 32 * wt + 16 * tt + l16;
+            const float st = scl[min(t, p.T - 1)];         // the token's scale (block 0's entry)
 #pragma unroll
-        for (int rw = 0; rw < 4; rw++) {
-            const int o = R0 + 64 * wr + 16 * rw + 4 * gq;
-            if (t >= p.T || o >= p.O) continue;
-            const float4 sc4 = *reinterpret_cast<const float4 *>(p.scale + o);
-            float v[4];
+            for (int rw = 0; rw < 4; rw++) {
+                const int o = R0 + 64 * wr + 16 * rw + 4 * gq;
+                if (t >= p.T || o >= p.O) continue;
+                const float4 sc4 = *reinterpret_cast<const float4 *>(p.scale + o);
+                float v[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float lo = fmaf((float)acc[2][rw][tt][r], 0x1p-7f, (float)acc[1][rw][tt][r]);
-                v[r] = fmaf(lo, 0x1p-7f, (float)acc[0][rw][tt][r]) * st;
+                for (int r = 0; r < 4; r++) {
+                    const float lo = fmaf((float)acc[2][rw][tt][r], 0x1p-7f, (float)acc[1][rw][tt][r]);
+                    v[r] = fmaf(lo, 0x1p-7f, (float)acc[0][rw][tt][r]) * st;
+                }
+                *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) =
+                    make_float4(v[0] * sc4.x, v[1] * sc4.y, v[2] * sc4.z, v[3] * sc4.w);
             }
-            *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) =
-                make_float4(v[0] * sc4.x, v[1] * sc4.y, v[2] * sc4.z, v[3] * sc4.w);
+        }
+    };
+    // the wave's copies of all but the last step issued are complete, then
+    // every wave's (vmcnt(4): 4 copies per step; other memory operations in
+    // flight, the output stores of a finished tile, are older and complete
+    // first)
+    auto step_barrier = [&]() __attribute__((always_inline)) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0x0F74);                  // vmcnt(4), expcnt / lgkmcnt not waited
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // Step g (stage g % 4, register slot g % 2): the copies of step g + 3 go
+    // into stage (g + 3) % 4 (last read during step g - 2, before the barrier
+    // that ended step g - 1); step g + 1's operands are read from its stage,
+    // whose copies (issued in step g - 2) every wave waited for before that
+    // barrier; step g's products run from registers.
+    // (The reads of step g + 1 go out in two parts, each before the half of
+    // step g's products that follows it, so that no more LDS reads are in
+    // flight than the wait counter expresses and the products' waits cover
+    // only the previous step's reads.)
+    auto step = [&](int g, auto m_c) __attribute__((always_inline)) {
+        constexpr int m = decltype(m_c)::value;
+        using SN = std::integral_constant<int, (m + 1) % 4>;
+        using RN = std::integral_constant<int, (m + 1) % 2>;
+        using RC = std::integral_constant<int, m % 2>;
+        copy(std::integral_constant<int, (m + 3) % 4>{});        // step g + 3
+        get(SN{}, RN{}, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(RC{}, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        get(SN{}, RN{}, std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        compute(RC{}, std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        step_barrier();
+    };
+    zero();
+    copy(std::integral_constant<int, 0>{});
+    copy(std::integral_constant<int, 1>{});
+    copy(std::integral_constant<int, 2>{});
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F74);                      // steps 0 and 1 copied (this wave)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    get(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    get(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+#pragma unroll 1
+    for (int g = 0; g < NG; g += 4) {
+        step(g, std::integral_constant<int, 0>{});
+        step(g + 1, std::integral_constant<int, 1>{});
+        step(g + 2, std::integral_constant<int, 2>{});
+        step(g + 3, std::integral_constant<int, 3>{});
+        if ((g + 4) % S == 0) {                              // a tile's last step: its outputs
+            store(g / S);
+            zero();
         }
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);                      // (the last, unused copies land before the workgroup ends)
 }
+#undef OMH_LDS
 
 // The GEMM takes int8 rows with x split per token (not the decode core's
-// per-head planes), from kGmMinT tokens (OMH_I8_GEMM=0 / 1 overrides, for
-// tuning), with k a multiple of the loop body's two 64-wide steps.
+// per-head planes) and the tiled copy of the weights, from kGmMinT tokens
+// (OMH_I8_GEMM=0 / 1 overrides, for tuning), with k a multiple of the loop
+// body's four 64-wide steps.
 constexpr int kGmMinT = 256;
 bool use_i8_gemm(const ProjArgs &p) {
-    if (p.x_split || p.I % 128 != 0 || p.I > (1 << 25) / 127) return false;
+    if (p.x_split || !p.Qt || p.I % 256 != 0 || p.I > (1 << 25) / 127) return false;
     // (buffer offsets are 32-bit)
-    if ((size_t)p.O * p.I >= (1u << 31) || kI8Planes * i8_plane_bytes(p.T, p.I) >= (1u << 31)) return false;
+    if (tile_q8_bytes(p.O, p.I) >= (1u << 31) || kI8Planes * i8_plane_bytes(p.T, p.I) >= (1u << 31)) return false;
     if (const char *e = getenv("OMH_I8_GEMM")) return e[0] == '1';
     return p.T >= kGmMinT;
 }
@@ -1376,7 +1440,8 @@ bool use_i8_gemm(const ProjArgs &p) {
 void launch_i8_gemm(const ProjArgs &p, hipStream_t st) {
     const int nrb = (p.O + kGmRows - 1) / kGmRows, ntt = (p.T + kGmTok - 1) / kGmTok;
     const int per = (ntt + 7) / 8 * nrb;                     // tiles of the XCD with the most
-    hipLaunchKernelGGL(proj_i8_gemm_kernel, dim3(8 * per), dim3(8 * OMH_WAVE), 0, st, p, nrb, ntt);
+    // one resident workgroup per CU (LDS), each taking every 256th block
+    hipLaunchKernelGGL(proj_i8_gemm_kernel, dim3(std::min(8 * per, kGmWgs)), dim3(8 * OMH_WAVE), 0, st, p, nrb, ntt);
 }
 
 // Launch shape of the fp32-MFMA projection: one row tile per workgroup (k
@@ -1857,7 +1922,30 @@ void launch_q8(const ProjArgs &p, hipStream_t st) {
     }
 }
 
+// Row-major int8 weights [O][I] -> the tiled copy (tile_q8_bytes): one
+// thread per 16-byte piece of the copy.
+__global__ __launch_bounds__(256)
+void tile_q8_kernel(const int8_t *__restrict__ Q, int O, int I, int8_t *__restrict__ Qt) {
+    const size_t P = (size_t)blockIdx.x * 256 + threadIdx.x;           // piece of the copy
+    const int nks = I / 64;
+    if (P >= (size_t)(O + 15) / 16 * nks * OMH_WAVE) return;
+    const size_t frag = P / OMH_WAVE;
+    const int L = (int)(P % OMH_WAVE), rb = (int)(frag / nks), ks = (int)(frag % nks);
+    const int o = 16 * rb + L % 16, k = 64 * ks + 16 * (L / 16);
+    v4i v = {0, 0, 0, 0};
+    if (o < O) v = *reinterpret_cast<const v4i *>(Q + (size_t)o * I + k);
+    *reinterpret_cast<v4i *>(Qt + 16 * P) = v;
+}
+
 }  // namespace
+
+bool tile_q8_wanted(int O, int I) { return O > 0 && I % 256 == 0 && tile_q8_bytes(O, I) < (1u << 31); }
+hipError_t tile_q8(const int8_t *Q, int O, int I, int8_t *Qt, hipStream_t st) {
+    if (!tile_q8_wanted(O, I)) return hipErrorInvalidValue;
+    const size_t pieces = (size_t)(O + 15) / 16 * (I / 64) * OMH_WAVE;
+    hipLaunchKernelGGL(tile_q8_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, Q, O, I, Qt);
+    return hipGetLastError();
+}
 
 bool proj_supported(int I, int n_q) { return I >= 64 && I % 64 == 0 && n_q % 16 == 0; }
 

@@ -62,6 +62,7 @@ struct DevLayer {
     int out_nq = 0;
     int8_t *Qout = nullptr;
     float *Sout = nullptr, *Wout = nullptr;
+    int8_t *Qtin = nullptr, *Qtout = nullptr;   // tiled copies of the int8 rows (tile_q8), or null
 };
 
 DevLayer g_L[kMaxLayers];
@@ -99,9 +100,20 @@ int upload(T **dst, size_t count, const T *src) {
     return OMH_OK;
 }
 
+// The tiled copy of O x I int8 weights the prefill-sized GEMM reads
+// (tile_q8), where the shape takes one; *Qt stays null otherwise.
+int upload_tiled(int8_t **Qt, const int8_t *Q, int O, int I) {
+    if (!tile_q8_wanted(O, I)) return OMH_OK;
+    if (hipMalloc(reinterpret_cast<void **>(Qt), tile_q8_bytes(O, I)) != hipSuccess)
+        return fail(OMH_ERR_ALLOC, "alloc of %zu bytes failed", tile_q8_bytes(O, I));
+    HIP_OK(tile_q8(Q, O, I, *Qt, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    return OMH_OK;
+}
+
 void free_layer(DevLayer &L) {
     void *ps[] = {L.conv_w, L.A_log, L.dt_bias, L.gnorm, L.conv_st, L.S, L.phase, L.o_raw, L.ssq,
-                  L.cnt, L.Qin, L.Sin, L.Win, L.Qout, L.Sout, L.Wout};
+                  L.cnt, L.Qin, L.Sin, L.Win, L.Qout, L.Sout, L.Wout, L.Qtin, L.Qtout};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     L = DevLayer{};
@@ -239,7 +251,7 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
     ProjArgs p{};
     p.counters = cnt; p.ncounters = ncnt;
     p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = ds.xb_n;
-    p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
+    p.Q = L.Qin; p.Qt = L.Qtin; p.scale = L.Sin; p.W = L.Win; p.T = B; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
@@ -251,7 +263,7 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
     ProjArgs q{};
     q.counters = cnt; q.ncounters = ncnt;
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = ds.xb_n; q.x_split = planes != nullptr;
-    q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
+    q.Q = L.Qout; q.Qt = L.Qtout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
 }
@@ -337,7 +349,7 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     ProjArgs p{};
     p.counters = g_counters; p.ncounters = kCounters;
     p.x = x; p.ldx = D; p.y = in; p.ldy = L.in_rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
-    p.Q = L.Qin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
+    p.Q = L.Qin; p.Qt = L.Qtin; p.scale = L.Sin; p.W = L.Win; p.T = T; p.I = D; p.O = L.in_rows; p.n_q = L.in_nq;
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
@@ -345,7 +357,7 @@ int prefill_full(int li, int seq, int T, const float *x, float *out, hipStream_t
     ProjArgs q{};
     q.counters = g_counters; q.ncounters = kCounters;
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
-    q.Q = L.Qout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
+    q.Q = L.Qout; q.Qt = L.Qtout; q.scale = L.Sout; q.W = L.Wout; q.T = T; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
 }
@@ -360,6 +372,7 @@ struct AttnLayer {
     int out_nq = 0;
     int8_t *Qout = nullptr;
     float *Sout = nullptr, *Wout = nullptr;
+    int8_t *Qtin = nullptr, *Qtout = nullptr;   // tiled copies of the int8 rows (tile_q8), or null
     float *qn = nullptr, *kn = nullptr, *inv = nullptr;
     float *Kc = nullptr, *Vc = nullptr;
 };
@@ -367,7 +380,7 @@ AttnLayer g_A[kMaxLayers];
 Scratch g_arow, g_aqb, g_actx, g_apo, g_apml;
 
 void free_attn(AttnLayer &A) {
-    void *ps[] = {A.Qin, A.Sin, A.Win, A.Qout, A.Sout, A.Wout, A.qn, A.kn, A.inv, A.Kc, A.Vc};
+    void *ps[] = {A.Qin, A.Sin, A.Win, A.Qout, A.Sout, A.Wout, A.Qtin, A.Qtout, A.qn, A.kn, A.inv, A.Kc, A.Vc};
     for (void *p : ps)
         if (p) (void)hipFree(p);
     A = AttnLayer{};
@@ -408,7 +421,7 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     ProjArgs p{};
     p.counters = g_counters; p.ncounters = kCounters;
     p.x = x; p.ldx = D; p.y = rowb; p.ldy = A.rows; p.xb = xb; p.xb_n = xb ? g_xb.n : 0;
-    p.Q = A.Qin; p.scale = A.Sin; p.W = A.Win; p.T = T; p.I = D; p.O = A.rows; p.n_q = A.nq;
+    p.Q = A.Qin; p.Qt = A.Qtin; p.scale = A.Sin; p.W = A.Win; p.T = T; p.I = D; p.O = A.rows; p.n_q = A.nq;
     HIP_OK(launch_proj(p, st));
     AttnArgs a{};
     a.qkv = rowb; a.ld_qkv = A.rows;
@@ -425,7 +438,7 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     ProjArgs q{};
     q.counters = g_counters; q.ncounters = kCounters;
     q.x = ctx; q.ldx = A.qdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = xb ? g_xb.n : 0;
-    q.Q = A.Qout; q.scale = A.Sout; q.W = A.Wout; q.T = T; q.I = A.qdim; q.O = D; q.n_q = A.out_nq;
+    q.Q = A.Qout; q.Qt = A.Qtout; q.scale = A.Sout; q.W = A.Wout; q.T = T; q.I = A.qdim; q.O = D; q.n_q = A.out_nq;
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
 }
@@ -534,6 +547,7 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
             memcpy(s.data() + L.conv_dim, w->S_z, L.vdim * sizeof(float));
             UP(L.Qin, q.size(), q.data());
             UP(L.Sin, s.size(), s.data());
+            if ((rc = upload_tiled(&L.Qtin, L.Qin, L.in_nq, D)) != OMH_OK) { free_layer(L); return rc; }
         }
         const int nf = L.in_rows - L.in_nq;
         std::vector<float> f((size_t)nf * Dz);
@@ -549,6 +563,7 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
             L.out_nq = D;
             UP(L.Qout, (size_t)D * L.vdim, w->Q_out);
             UP(L.Sout, D, w->S_out);
+            if ((rc = upload_tiled(&L.Qtout, L.Qout, D, L.vdim)) != OMH_OK) { free_layer(L); return rc; }
         } else {
             UP(L.Wout, (size_t)D * L.vdim, w->W_out);
         }
@@ -845,6 +860,7 @@ int omh_attn_layer_init(int li, const omh_attn_dims *d, const omh_attn_weights *
         memcpy(s.data() + nqr + nkr, w->S_v, nkr * sizeof(float));
         UPA(A.Qin, q.size(), q.data());
         UPA(A.Sin, s.size(), s.data());
+        if ((rc = upload_tiled(&A.Qtin, A.Qin, A.rows, D)) != OMH_OK) { free_attn(A); return rc; }
     } else {
         std::vector<float> f((size_t)A.rows * Dz);
         memcpy(f.data(), w->W_q, nqr * Dz * sizeof(float));
@@ -855,6 +871,7 @@ int omh_attn_layer_init(int li, const omh_attn_dims *d, const omh_attn_weights *
     if (w->Q_o) {
         UPA(A.Qout, (size_t)D * A.qdim, w->Q_o);
         UPA(A.Sout, D, w->S_o);
+        if ((rc = upload_tiled(&A.Qtout, A.Qout, D, A.qdim)) != OMH_OK) { free_attn(A); return rc; }
     } else {
         UPA(A.Wout, (size_t)D * A.qdim, w->W_o);
     }

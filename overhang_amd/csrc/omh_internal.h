@@ -124,6 +124,7 @@ struct ProjArgs {
     const float *x;        // [T][ldx]
     float *y;              // [T][ldy]
     const int8_t *Q;       // [n_q][I]
+    const int8_t *Qt;      // the same int8 rows tiled (tile_q8), or null: the prefill-sized GEMM reads these
     const float *scale;    // [n_q]
     const float *W;        // [O - n_q][I]
     int64_t ldx, ldy;
@@ -144,6 +145,14 @@ bool proj_x_int8_planes(int T, int I, int n_q);
 // hidden size I and int8 row count n_q the projection kernels take
 bool proj_supported(int I, int n_q);
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st);
+// Tiled copy of int8 weights [O][I] for the prefill-sized GEMM: 16-row x
+// 64-k fragments, each a contiguous 1 KiB run in v_mfma_i32_16x16x64_i8
+// A-operand order (byte 16 L + j of fragment (o / 16, k / 64) holds row
+// 16 (o / 16) + L % 16 at k = 64 (k / 64) + 16 (L / 16) + j), fragments
+// k-fastest, rows padded to 16 with zeros.  Wanted for I a multiple of 256.
+bool tile_q8_wanted(int O, int I);
+__host__ __device__ inline size_t tile_q8_bytes(int O, int I) { return (size_t)(O + 15) / 16 * 16 * I; }
+hipError_t tile_q8(const int8_t *Q, int O, int I, int8_t *Qt, hipStream_t st);
 
 // Chunked prefill of T tokens of one sequence (kd == vd == D).
 constexpr int kChunk = 64;
