@@ -278,8 +278,10 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
 #undef OMH_ATTN_LOAD_PIECE
 
 // ---------------------------------------------------------------- prompt steps
-// Flash attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32) for
-// prompt steps of at least kFlashMinT tokens: the same fp32 scores, online
+// Flash attention on the matrix cores for prompt steps of at least
+// kFlashMinT tokens (attn_flash3_kernel below: bf16 x 3 products, the
+// default; this one with fp32 products, v_mfma_f32_16x16x4f32, kept for
+// comparison, OMH_ATTN_FLASH=fp32): the same fp32 scores, online
 // softmax and P.V as the split kernel, as dense products.  A wave owns one
 // unit, 16 consecutive tokens of one query head; a workgroup of 8 waves
 // takes 8 units of one kv group (the group's heads of a token block, then
@@ -305,6 +307,11 @@ struct FlashShape {
     static constexpr int PER = KT * HD / 4 / (8 * OMH_WAVE);   // float4 pieces of K (and of V) per thread
 };
 constexpr int kFlashMinT = 64;
+// the fp32-product flash kernel instead of the bf16 x 3 one (OMH_ATTN_FLASH=fp32, for comparison)
+bool flash_fp32() {
+    const char *e = getenv("OMH_ATTN_FLASH");
+    return e && e[0] == 'f';
+}
 
 template <int HD>
 __global__ __launch_bounds__(8 * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -434,6 +441,206 @@ void attn_flash_kernel(const AttnArgs a) {
     }
 }
 
+// The same flash attention with every product as three bf16 products on
+// the bf16 matrix cores (v_mfma_f32_16x16x32_bf16, fp32 accumulation): each
+// fp32 operand x splits as hi = bf16(x), lo = bf16(x - hi), so
+// x = hi + lo to 2^-16 relative, and a.b = hi.hi + hi.lo + lo.hi with the
+// dropped lo.lo term below 2^-16 |a||b|; per 32 keys a wave issues 96 such
+// products against 256 fp32 ones.  K is staged into LDS as hi / lo planes
+// row-major (32 head dims per 16-byte read), V transposed (V^T[dim][key],
+// 8 keys per 16-byte read) with its keys in the order the probabilities
+// already sit in the score product's registers: position 8 g + j of a
+// V^T row holds key 16 (j / 4) + 4 g + j % 4, which lane group g of the
+// B operand P^T holds as register j % 4 of its score sub-tile j / 4.  Rows
+// are padded so that every 16-lane group's reads fall in distinct banks.
+template <int HD>
+struct Flash3Shape {
+    static constexpr int KT = 32;                  // keys per tile
+    static constexpr int KLD = 2 * HD + 16;        // bytes of one bf16 K row
+    static constexpr int VLD = 2 * KT + 16;        // bytes of one bf16 V^T row
+    static constexpr int KPL = KT * KLD, VPL = HD * VLD;
+    static constexpr int STAGE = 2 * KPL + 2 * VPL;   // K hi, K lo, V^T hi, V^T lo
+    static constexpr size_t LDS = 2 * (size_t)STAGE;
+    static constexpr int NS = HD / 32;             // 32-dim steps of q.k
+    static constexpr int NJ = HD / 16;             // 16-dim output tiles
+    static constexpr int PK = KT * HD / 4 / (8 * OMH_WAVE);         // K float4 pieces per thread
+    static constexpr int PV = KT / 2 * HD / 4 / (8 * OMH_WAVE);     // V (key pair, 4 dims) units per thread
+};
+typedef __bf16 omh_v8bf __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)a) | (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)b) << 16;
+}
+__device__ __forceinline__ float bf16_rest(float x) { return x - (float)(__bf16)x; }
+
+template <int HD>
+__global__ __launch_bounds__(8 * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_flash3_kernel(const AttnArgs a) {
+    using F = Flash3Shape<HD>;
+    constexpr int KT = F::KT, KLD = F::KLD, VLD = F::VLD, NS = F::NS, NJ = F::NJ, NT = 8 * OMH_WAVE;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem3[];
+    const int H = a.H, KV = a.KV, grp = H / KV;
+    const int nunit = (a.T + 15) / 16 * grp, wpg = (nunit + 7) / 8;
+    const int g = blockIdx.x % KV, wi = wpg - 1 - (int)blockIdx.x / KV;
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, gq = lane / 16;
+    const bool own = 8 * wi + w < nunit;
+    const int u = min(8 * wi + w, nunit - 1);
+    const int tb = u / grp, h = g * grp + u % grp;
+    const int tq = 16 * tb + l16;                  // this lane's query token (may be past T: not written)
+    const int tlast = min(16 * (min(8 * wi + 7, nunit - 1) / grp) + 15, a.T - 1);
+    const int nkeys = a.pos + tlast + 1;
+    const int kmax = a.pos + tq;
+
+    // q as the B operand of S^T: dims 32 s + 8 gq .. +7 of token tq, hi and lo
+    omh_v8bf qh[NS], ql[NS];
+    {
+        const float *qr = a.qb + ((size_t)min(tq, a.T - 1) * H + h) * HD + 8 * gq;
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(qr + 32 * s);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qr + 32 * s + 4);
+            const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                qh[s][j] = (__bf16)v[j];
+                ql[s][j] = (__bf16)bf16_rest(v[j]);
+            }
+        }
+    }
+    const size_t cache0 = ((size_t)a.seq * KV + g) * a.max_t;
+    const float *Kg = a.Kc + cache0 * HD, *Vg = a.Vc + cache0 * HD;
+    omh_v4f kr[F::PK], vr[F::PV][2];
+    auto key_of = [&](int kt, int kk) { return (size_t)(kt + kk < nkeys ? kt + kk : kt); };
+    auto load = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < F::PK; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + key_of(kt, kk) * HD + 4 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < F::PV; i++) {
+            const int e = tid + NT * i, kp = e / (HD / 4), c = e % (HD / 4);
+            vr[i][0] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, 2 * kp) * HD + 4 * c);
+            vr[i][1] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, 2 * kp + 1) * HD + 4 * c);
+        }
+    };
+    auto put = [&](int stage) __attribute__((always_inline)) {
+        unsigned char *st = smem3 + stage * F::STAGE;
+        unsigned char *Kh = st, *Kl = st + F::KPL, *Vh = st + 2 * F::KPL, *Vl = Vh + F::VPL;
+#pragma unroll
+        for (int i = 0; i < F::PK; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            const omh_v4f x = kr[i];
+            uint2 hi, lo;
+            hi.x = bf16_pair(x[0], x[1]);
+            hi.y = bf16_pair(x[2], x[3]);
+            lo.x = bf16_pair(bf16_rest(x[0]), bf16_rest(x[1]));
+            lo.y = bf16_pair(bf16_rest(x[2]), bf16_rest(x[3]));
+            *reinterpret_cast<uint2 *>(Kh + kk * KLD + 8 * c) = hi;
+            *reinterpret_cast<uint2 *>(Kl + kk * KLD + 8 * c) = lo;
+        }
+#pragma unroll
+        for (int i = 0; i < F::PV; i++) {
+            const int e = tid + NT * i, kp = e / (HD / 4), c = e % (HD / 4);
+            const int k0 = 2 * kp;                 // key = 16 a + 4 g + b, b even: position 8 g + 4 a + b
+            const int pos = 8 * ((k0 % 16) / 4) + 4 * (k0 / 16) + k0 % 4;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const float x0 = vr[i][0][d], x1 = vr[i][1][d];
+                *reinterpret_cast<uint32_t *>(Vh + (4 * c + d) * VLD + 2 * pos) = bf16_pair(x0, x1);
+                *reinterpret_cast<uint32_t *>(Vl + (4 * c + d) * VLD + 2 * pos) = bf16_pair(bf16_rest(x0), bf16_rest(x1));
+            }
+        }
+    };
+
+    omh_v4f o[NJ];                                 // O^T: o[j][i] = O[token tq][dim 16 j + 4 gq + i]
+#pragma unroll
+    for (int j = 0; j < NJ; j++) o[j] = omh_v4f{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    load(0);
+    put(0);
+    __syncthreads();
+    for (int kt = 0, st = 0; kt < nkeys; kt += KT, st ^= 1) {
+        if (kt + KT < nkeys) load(kt + KT);
+        const unsigned char *sb = smem3 + st * F::STAGE;
+        const unsigned char *Kh = sb, *Kl = sb + F::KPL, *Vh = sb + 2 * F::KPL, *Vl = Vh + F::VPL;
+        // S^T for keys kt + 16 n + 4 gq + i (register i of sc[n]), query row tq
+        omh_v4f sc[KT / 16];
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++) {
+            sc[n] = omh_v4f{0.f, 0.f, 0.f, 0.f};
+            const size_t ro = (size_t)(16 * n + l16) * KLD + 16 * gq;
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                const omh_v8bf kh = *reinterpret_cast<const omh_v8bf *>(Kh + ro + 64 * s);
+                const omh_v8bf kl = *reinterpret_cast<const omh_v8bf *>(Kl + ro + 64 * s);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[s], sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[s], sc[n], 0, 0, 0);
+                sc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[s], sc[n], 0, 0, 0);
+            }
+        }
+        // scores * hd^-1/2, causal mask, online softmax (qwen.c:410-414)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = kt + 16 * n + 4 * gq + i;
+                sc[n][i] = key <= kmax ? sc[n][i] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sc[n][i]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        const float mn = fmaxf(m, mx);             // finite: key 0 is in every token's first tile
+        const float corr = expf(m - mn);
+        float ps = 0.f;
+        omh_v8bf ph, pl;                           // P^T as the B operand: j = 4 n + i
+#pragma unroll
+        for (int n = 0; n < KT / 16; n++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float pv = expf(sc[n][i] - mn);
+                ps += pv;
+                ph[4 * n + i] = (__bf16)pv;
+                pl[4 * n + i] = (__bf16)bf16_rest(pv);
+            }
+        ps += __shfl_xor(ps, 16, OMH_WAVE);
+        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        l = fmaf(l, corr, ps);
+        m = mn;
+        // O^T = corr O^T + V^T P^T (qwen.c:415-419)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            o[j] = o[j] * corr;
+            const size_t ro = (size_t)(16 * j + l16) * VLD + 16 * gq;
+            const omh_v8bf vh = *reinterpret_cast<const omh_v8bf *>(Vh + ro);
+            const omh_v8bf vl = *reinterpret_cast<const omh_v8bf *>(Vl + ro);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[j], 0, 0, 0);
+        }
+        if (kt + KT < nkeys) put(st ^ 1);
+        __syncthreads();
+    }
+    // normalise and gate (qwen.c:420-421)
+    if (!own || tq >= a.T) return;
+    const float il = 1.f / l;
+    const float *gate = a.qkv + (size_t)tq * a.ld_qkv + (size_t)h * 2 * HD + HD + 4 * gq;
+    float *dst = a.ctx + ((size_t)tq * H + h) * HD + 4 * gq;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float4 gv = *reinterpret_cast<const float4 *>(gate + 16 * j);
+        float4 r;
+        r.x = o[j][0] * il * omh_sigmoid(gv.x);
+        r.y = o[j][1] * il * omh_sigmoid(gv.y);
+        r.z = o[j][2] * il * omh_sigmoid(gv.z);
+        r.w = o[j][3] * il * omh_sigmoid(gv.w);
+        *reinterpret_cast<float4 *>(dst + 16 * j) = r;
+    }
+}
+
 // One workgroup per (token, head, 64 columns): the CW waves take every
 // CW-th split, lane = column, then sum through LDS.
 constexpr int kCombineWaves = 8;
@@ -488,13 +695,21 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
     if constexpr (HD >= 128) {
         if (attn_uses_flash(a.T, HD)) {
-            static const bool flash_ok = hipFuncSetAttribute((const void *)attn_flash_kernel<HD>,
-                                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                             (int)FlashShape<HD>::LDS) == hipSuccess;
-            if (!flash_ok) return hipErrorInvalidValue;
             const int wpg = ((a.T + 15) / 16 * (a.H / a.KV) + 7) / 8;
-            hipLaunchKernelGGL((attn_flash_kernel<HD>), dim3((unsigned)(a.KV * wpg)), dim3(8 * OMH_WAVE),
-                               FlashShape<HD>::LDS, st, a);
+            const dim3 grid((unsigned)(a.KV * wpg)), blk(8 * OMH_WAVE);
+            if (flash_fp32()) {
+                static const bool ok = hipFuncSetAttribute((const void *)attn_flash_kernel<HD>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)FlashShape<HD>::LDS) == hipSuccess;
+                if (!ok) return hipErrorInvalidValue;
+                hipLaunchKernelGGL((attn_flash_kernel<HD>), grid, blk, FlashShape<HD>::LDS, st, a);
+            } else {
+                static const bool ok = hipFuncSetAttribute((const void *)attn_flash3_kernel<HD>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)Flash3Shape<HD>::LDS) == hipSuccess;
+                if (!ok) return hipErrorInvalidValue;
+                hipLaunchKernelGGL((attn_flash3_kernel<HD>), grid, blk, Flash3Shape<HD>::LDS, st, a);
+            }
             return hipGetLastError();
         }
     }

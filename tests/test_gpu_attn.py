@@ -211,3 +211,23 @@ def test_attention_matches_reference_attn_golden(name):
         assert np.array_equal(K0[:, :pos0], Kpre.transpose(1, 0, 2)), "seeded rows come back unchanged"
     finally:
         L.free()
+
+
+def test_flash_bf16x3_matches_fp32_products(monkeypatch):
+    """The bf16 x 3 flash kernel (the default for prompt steps) against the
+    fp32-product flash kernel on the same 35B-shape prompt (OMH_ATTN_FLASH
+    selects): three bf16 products per fp32 one leave a relative error near
+    2^-16 per product, far inside the layer's tolerance."""
+    D, H, KV, hd, rot = Q35B_ATTN
+    rng = np.random.default_rng(23)
+    w = _weights(rng, D, H, KV, hd)
+    x = rng.normal(0, 1, (300, D)).astype(np.float32)
+    outs = {}
+    for mode in ("fp32", "bf16x3"):
+        monkeypatch.setenv("OMH_ATTN_FLASH", mode)
+        L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 300, w)
+        try:
+            outs[mode] = L.forward(0, 0, x)
+        finally:
+            L.free()
+    assert_close(outs["bf16x3"], outs["fp32"], atol=2e-5, rtol=2e-4, what="flash bf16x3 vs fp32")
