@@ -513,6 +513,11 @@ void attn_flash3_kernel(const AttnArgs a) {
     const float *Kg = a.Kc + cache0 * HD, *Vg = a.Vc + cache0 * HD;
     omh_v4f kr[F::PK], vr[F::PV][2];
     auto key_of = [&](int kt, int kk) { return (size_t)(kt + kk < nkeys ? kt + kk : kt); };
+    // V unit e: the key pair at V^T positions 2 pp, 2 pp + 1 (pp = e % 16) for
+    // head dims 4 c .. 4 c + 3 (c = e / 16), so the 16 lanes of a position
+    // pair sweep write one 64-byte run of a V^T row: no bank conflicts.
+    // Position 8 g + j holds key 16 (j / 4) + 4 g + j % 4.
+    auto vkey = [](int pp) { const int pos = 2 * pp, g8 = pos / 8, j = pos % 8; return 16 * (j / 4) + 4 * g8 + j % 4; };
     auto load = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < F::PK; i++) {
@@ -521,9 +526,9 @@ void attn_flash3_kernel(const AttnArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < F::PV; i++) {
-            const int e = tid + NT * i, kp = e / (HD / 4), c = e % (HD / 4);
-            vr[i][0] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, 2 * kp) * HD + 4 * c);
-            vr[i][1] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, 2 * kp + 1) * HD + 4 * c);
+            const int e = tid + NT * i, k0 = vkey(e % 16), c = e / 16;
+            vr[i][0] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, k0) * HD + 4 * c);
+            vr[i][1] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, k0 + 1) * HD + 4 * c);
         }
     };
     auto put = [&](int stage) __attribute__((always_inline)) {
@@ -543,9 +548,7 @@ void attn_flash3_kernel(const AttnArgs a) {
         }
 #pragma unroll
         for (int i = 0; i < F::PV; i++) {
-            const int e = tid + NT * i, kp = e / (HD / 4), c = e % (HD / 4);
-            const int k0 = 2 * kp;                 // key = 16 a + 4 g + b, b even: position 8 g + 4 a + b
-            const int pos = 8 * ((k0 % 16) / 4) + 4 * (k0 / 16) + k0 % 4;
+            const int e = tid + NT * i, pos = 2 * (e % 16), c = e / 16;
 #pragma unroll
             for (int d = 0; d < 4; d++) {
                 const float x0 = vr[i][0][d], x1 = vr[i][1][d];
@@ -594,14 +597,16 @@ void attn_flash3_kernel(const AttnArgs a) {
         mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
         mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
         const float mn = fmaxf(m, mx);             // finite: key 0 is in every token's first tile
-        const float corr = expf(m - mn);
+        // e^(s - mn) as 2^((s - mn) log2 e) on the hardware exp2 (a masked
+        // score, -inf, gives 0; the first tile's corr, 2^-inf, 0)
+        const float corr = __builtin_amdgcn_exp2f((m - mn) * 1.4426950408889634f);
         float ps = 0.f;
         omh_v8bf ph, pl;                           // P^T as the B operand: j = 4 n + i
 #pragma unroll
         for (int n = 0; n < KT / 16; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float pv = expf(sc[n][i] - mn);
+                const float pv = __builtin_amdgcn_exp2f((sc[n][i] - mn) * 1.4426950408889634f);
                 ps += pv;
                 ph[4 * n + i] = (__bf16)pv;
                 pl[4 * n + i] = (__bf16)bf16_rest(pv);
@@ -610,10 +615,13 @@ void attn_flash3_kernel(const AttnArgs a) {
         ps += __shfl_xor(ps, 32, OMH_WAVE);
         l = fmaf(l, corr, ps);
         m = mn;
-        // O^T = corr O^T + V^T P^T (qwen.c:415-419)
+        // O^T = corr O^T + V^T P^T (qwen.c:415-419); the rescale only when a
+        // row's max moved (corr = 1 otherwise)
+        if (__builtin_amdgcn_ballot_w64(corr != 1.f))
+#pragma unroll
+            for (int j = 0; j < NJ; j++) o[j] = o[j] * corr;
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            o[j] = o[j] * corr;
             const size_t ro = (size_t)(16 * j + l16) * VLD + 16 * gq;
             const omh_v8bf vh = *reinterpret_cast<const omh_v8bf *>(Vh + ro);
             const omh_v8bf vl = *reinterpret_cast<const omh_v8bf *>(Vl + ro);
