@@ -1720,6 +1720,150 @@ void proj_i8_stream_kernel(const ProjArgs p, const F32Part f) {
     }
 }
 
+// ------------------------------- int8 rows, decode batches, split queues
+// The streaming kernel's waves issue their x pieces after all of their
+// weights, and a wave's loads complete in issue order, so its products wait
+// for its whole share of the weight stream and then for x one L2 round trip
+// per ring slot.  Here the two streams are on different waves: a workgroup
+// of 8 waves owns RT 16-row tiles x all (up to 64) tokens over the whole k
+// range; waves 4..7 only copy the weights (from the tiled copy, straight into
+// an LDS ring of kDqAhead + 1 128-wide blocks, kDqAhead blocks ahead), waves
+// 0..3 only load x (token tile w, three int8 planes, from L2 into a register
+// ring kDqX blocks ahead) and run the products.  One barrier per block: a
+// loader reaches it once its copies of the block have landed, a compute wave
+// when it is about to read the block (so it has finished the previous one,
+// whose slot the loaders refill next).  Plane sums are exact in int32 over
+// the whole k range (per-token scales), combined once at the end.
+constexpr int kDqAhead = 8, kDqX = 4;
+
+template <int RT>
+__global__ __launch_bounds__(8 * OMH_WAVE, 1)
+void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
+    constexpr int NP = kI8Planes, SL = kDqAhead + 1;
+    constexpr int WB = RT * 2 * 1024;                        // bytes of one block of the workgroup's weights
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    if ((int)blockIdx.x < f.nwg) {
+        if (w < 4) proj_mfma_wg<1, 1, 8>(f.p, blockIdx.x % f.gx, blockIdx.x / f.gx);
+        else __syncthreads();                                // (the fp32 workgroup's one barrier)
+        return;
+    }
+    __shared__ __attribute__((aligned(16))) int8_t s_w[SL * WB];
+    const int rg = blockIdx.x - f.nwg, r0 = rg * RT * 16;
+    const int NB = p.I / kI8Blk;                             // 128-wide blocks
+    const int l16 = lane % 16, gq = lane / 16;
+
+    if (w >= 4) {
+        // loader: fragment j = 2 rt + h of a block is (row tile rt, k half h);
+        // this wave copies fragments (w - 4) and (w - 4) + 4 (where RT > 2)
+        constexpr int FPL = RT * 2 / 4 > 0 ? RT * 2 / 4 : 1;      // fragments per loader wave per block
+        const int nrf = (p.O + 15) / 16;
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.Qt), 0, (int)tile_q8_bytes(p.O, p.I), 0x00020000);
+        auto copy = [&](int b) __attribute__((always_inline)) {
+            const int bb = min(b, NB - 1);                   // (past the end: the last block again, unused)
+            int8_t *dst = s_w + (b % SL) * WB;
+#pragma unroll
+            for (int q = 0; q < FPL; q++) {
+                const int j = min((w - 4) + 4 * q, RT * 2 - 1), rt = j / 2, h = j % 2;
+                const int vo = min(r0 / 16 + rt, nrf - 1) * (p.I / 64) * 1024 + 16 * lane;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *)(dst + j * 1024),
+                                                         16, vo, (2 * bb + h) * 1024, 0, 0);
+            }
+        };
+        for (int b = 0; b < kDqAhead; b++) copy(b);
+        for (int b = 0; b < NB; b++) {
+            asm volatile("" ::: "memory");
+            // this wave's copies of block b have landed: kDqAhead - 1 later blocks in flight
+            if constexpr (FPL == 1) __builtin_amdgcn_s_waitcnt(0x0F77);          // vmcnt(7)
+            else __builtin_amdgcn_s_waitcnt(0x0F7E);                             // vmcnt(14)
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            copy(b + kDqAhead);                              // into the slot of block b - 1 (read before this barrier)
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);                  // (the last, unused copies land before the wave ends)
+        return;
+    }
+
+    // compute wave: token tile w
+    const int8_t *X = reinterpret_cast<const int8_t *>(p.xb);
+    const size_t plane = i8_plane_bytes(p.T, p.I), bstride = (size_t)i8_tiles(p.T) * 2048;
+    const float *scl = reinterpret_cast<const float *>(X + NP * plane);
+    const int u = min(w, i8_tiles(p.T) - 1);
+    const int8_t *xp = X + (size_t)u * 2048 + 16 * lane;
+    v4i xq[kDqX][NP][2];
+    auto x_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        const size_t o = (size_t)min(b, NB - 1) * bstride;
+#pragma unroll
+        for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) xq[sl][pl][h] = *reinterpret_cast<const v4i *>(xp + pl * plane + o + 1024 * h);
+    };
+    v4i ia[NP][RT];
+#pragma unroll
+    for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) ia[pl][rt] = v4i{0, 0, 0, 0};
+    auto block = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();                        // block b's weights are in LDS
+        asm volatile("" ::: "memory");
+        const int8_t *src = s_w + (b % SL) * WB + 16 * lane;
+        v4i wf[RT][2];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) wf[rt][h] = *reinterpret_cast<const v4i *>(src + (2 * rt + h) * 1024);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++)
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+                    ia[pl][rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[rt][h], xq[sl][pl][h], ia[pl][rt], 0, 0, 0);
+        x_load(b + kDqX, slot_c);                            // the ring slot just used, kDqX blocks ahead
+    };
+    static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { x_load(decltype(sc)::value, sc); });
+#pragma unroll 1
+    for (int b = 0; b < NB; b += kDqX)
+        static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { block(b + decltype(sc)::value, sc); });
+
+    // lane holds rows 4gq .. 4gq+3 of row tile rt for token l16 of token tile w
+    const int t = 16 * w + l16;
+    if (t >= p.T) return;
+    const float st = scl[t];                                 // the token's scale (block 0's entry)
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int o = r0 + 16 * rt + 4 * gq;
+        if (o >= p.O) continue;
+        const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float lo = fmaf((float)ia[2][rt][r], 0x1p-7f, (float)ia[1][rt][r]);
+            v[r] = fmaf(lo, 0x1p-7f, (float)ia[0][rt][r]) * st;
+        }
+        *reinterpret_cast<float4 *>(p.y + (size_t)t * p.ldy + o) = make_float4(v[0] * sc.x, v[1] * sc.y, v[2] * sc.z, v[3] * sc.w);
+    }
+}
+
+// Taken for 5..64 tokens of x split per token (not the decode core's
+// per-head planes) with the tiled weight copy, k a multiple of 128 kDqX and
+// the exact-int32 range (OMH_I8_DQ=0 turns it off, for comparison).
+constexpr int kDqRT = 4;
+bool use_i8_dq(const ProjArgs &p) {
+    if (p.T > 64 || p.T <= 4 || p.x_split || !p.Qt || p.I % (kI8Blk * kDqX) != 0 || p.I > (1 << 25) / 127) return false;
+    if (const char *e = getenv("OMH_I8_DQ"))
+        if (e[0] == '0') return false;
+    return true;
+}
+void launch_i8_dq(const ProjArgs &p, const F32Part &f, hipStream_t st) {
+    const int nrg = (p.O + 16 * kDqRT - 1) / (16 * kDqRT);
+    hipLaunchKernelGGL(proj_i8_dq_kernel<kDqRT>, dim3(f.nwg + nrg), dim3(8 * OMH_WAVE), 0, st, p, f);
+}
+
 // Plan of the streaming kernel: T <= 64 tokens, RT row tiles per workgroup,
 // a k split over G workgroups, NB = 1, 2 or 4 blocks per wave.  Measured at
 // the 35B shapes (B = 64, weights from HBM): the launch should fill the
@@ -2016,7 +2160,10 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         F32Part fs{};
         const int nf32 = i8 ? f32_beside(p.O > p.n_q ? &f : nullptr, &fs) : 0;
         const StPlan sp = i8 ? i8_stream_plan(q.O, p.T, p.I, nf32) : StPlan{0, 0, 0, 1};
-        if (sp.rt > 0) {
+        if (i8 && use_i8_dq(q)) {
+            launch_i8_dq(q, fs, st);
+            f32_done = nf32 > 0;
+        } else if (sp.rt > 0) {
             launch_i8_stream(q, sp, fs, st);
             f32_done = nf32 > 0;
         } else if (i8 && use_i8_gemm(q)) launch_i8_gemm(q, st);

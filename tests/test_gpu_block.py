@@ -210,3 +210,34 @@ def test_int8_gemm_matches_wave_kernel(shape, T, monkeypatch):
         L.free()
     assert_close(outs["1"][0], outs["0"][0], atol=2e-5, rtol=2e-5, what=f"{T} gemm vs wave out")
     assert_close(outs["1"][1], outs["0"][1], atol=2e-5, rtol=2e-5, what=f"{T} gemm vs wave S")
+
+
+@pytest.mark.parametrize("shape,B", [((16, 32, 128, 128, 2048), 64), ((16, 32, 128, 128, 2048), 17),
+                                     ((3, 6, 64, 64, 1024), 40)],
+                         ids=["35b-B64", "35b-B17", "kh3-B40"])
+def test_int8_decode_batch_kernel_matches_stream_kernel(shape, B, monkeypatch):
+    """The split-queue int8 kernel for decode batches of 5..64 tokens (one
+    set of waves copies the tiled weights into LDS, the other loads x and
+    runs the products) against the streaming kernel it replaces
+    (OMH_I8_DQ=0): both sum the plane products exactly in int32, so two
+    decode steps agree to fp32 rounding (B = 17: a partial token tile;
+    kh3: 1152 in_proj int8 rows, not a multiple of the 64-row workgroup
+    tile).  test_35b_int8_block_batch64 pins the same kernel to the oracle."""
+    from overhang_amd.dims import GdnDims
+    kh, vh, kd, vd, hidden = shape
+    d = GdnDims(kh=kh, vh=vh, kd=kd, vd=vd, K=4, hidden=hidden)
+    seed = 7800 + B
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed, B=B)
+    x = _x(d, seed, (2, B))
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("OMH_I8_DQ", mode)
+        L = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
+        for s in range(B):
+            L.set_state(s, conv0[s], S0[s])
+        o = np.stack([L.decode(x[t]) for t in range(2)])
+        outs[mode] = (o, np.stack([L.get_state(s)[1] for s in (0, B - 1)]))
+        L.free()
+    assert_close(outs["1"][0], outs["0"][0], atol=2e-5, rtol=2e-5, what=f"B={B} split-queue vs stream out")
+    assert_close(outs["1"][1], outs["0"][1], atol=2e-5, rtol=2e-5, what=f"B={B} split-queue vs stream S")
