@@ -38,6 +38,20 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// s_waitcnt immediate for vmcnt(n) alone (expcnt and lgkmcnt not waited)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// s_waitcnt vmcnt(min(n, N)) for a wave-uniform n in 0..N (the count must be
+// an immediate: a chain of compares)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    if (n >= N) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(N));
+        return;
+    }
+    if constexpr (N > 0) wait_vmcnt<N - 1>(n);
+}
+
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>)
 template <int N, int I = 0, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -1727,19 +1741,20 @@ void proj_i8_stream_kernel(const ProjArgs p, const F32Part f) {
 // per ring slot.  Here the two streams are on different waves: a workgroup
 // of 8 waves owns RT 16-row tiles x all (up to 64) tokens over the whole k
 // range; waves 4..7 only copy the weights (from the tiled copy, straight into
-// an LDS ring of kDqAhead + 1 128-wide blocks, kDqAhead blocks ahead), waves
+// an LDS ring of kDqAhead + 2 128-wide blocks, kDqAhead blocks ahead), waves
 // 0..3 only load x (token tile w, three int8 planes, from L2 into a register
 // ring kDqX blocks ahead) and run the products.  One barrier per block: a
-// loader reaches it once its copies of the block have landed, a compute wave
-// when it is about to read the block (so it has finished the previous one,
-// whose slot the loaders refill next).  Plane sums are exact in int32 over
-// the whole k range (per-token scales), combined once at the end.
+// loader reaches barrier b once its copies of block b have landed, a compute
+// wave when it is about to read block b from LDS, which it does while block
+// b - 1's products run (so its reads of block b - 2 have completed, and the
+// loaders refill that slot next).  Plane sums are exact in int32 over the
+// whole k range (per-token scales), combined once at the end.
 constexpr int kDqAhead = 8, kDqX = 4;
 
-template <int RT>
+template <int RT, int NBC>
 __global__ __launch_bounds__(8 * OMH_WAVE, 1)
 void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
-    constexpr int NP = kI8Planes, SL = kDqAhead + 1;
+    constexpr int NP = kI8Planes, SL = kDqAhead + 2;
     constexpr int WB = RT * 2 * 1024;                        // bytes of one block of the workgroup's weights
     const int tid = threadIdx.x, lane = tid % OMH_WAVE;
     const int w = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
@@ -1750,7 +1765,7 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
     }
     __shared__ __attribute__((aligned(16))) int8_t s_w[SL * WB];
     const int rg = blockIdx.x - f.nwg, r0 = rg * RT * 16;
-    const int NB = p.I / kI8Blk;                             // 128-wide blocks
+    const int NB = NBC > 0 ? NBC : p.I / kI8Blk;             // 128-wide blocks
     const int l16 = lane % 16, gq = lane / 16;
 
     if (w >= 4) {
@@ -1761,7 +1776,7 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
         const __amdgpu_buffer_rsrc_t wrs =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.Qt), 0, (int)tile_q8_bytes(p.O, p.I), 0x00020000);
         auto copy = [&](int b) __attribute__((always_inline)) {
-            const int bb = min(b, NB - 1);                   // (past the end: the last block again, unused)
+            const int bb = b;
             int8_t *dst = s_w + (b % SL) * WB;
 #pragma unroll
             for (int q = 0; q < FPL; q++) {
@@ -1771,17 +1786,16 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
                                                          16, vo, (2 * bb + h) * 1024, 0, 0);
             }
         };
-        for (int b = 0; b < kDqAhead; b++) copy(b);
+        for (int b = 0; b < min(kDqAhead, NB); b++) copy(b);
         for (int b = 0; b < NB; b++) {
             asm volatile("" ::: "memory");
-            // this wave's copies of block b have landed: kDqAhead - 1 later blocks in flight
-            if constexpr (FPL == 1) __builtin_amdgcn_s_waitcnt(0x0F77);          // vmcnt(7)
-            else __builtin_amdgcn_s_waitcnt(0x0F7E);                             // vmcnt(14)
+            // this wave's copies of block b have landed (those of the later
+            // blocks issued so far may be in flight)
+            wait_vmcnt<(kDqAhead - 1) * FPL>(min(kDqAhead - 1, NB - 1 - b) * FPL);
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            copy(b + kDqAhead);                              // into the slot of block b - 1 (read before this barrier)
+            if (b + kDqAhead < NB) copy(b + kDqAhead);       // into the slot of block b - 2 (its products are issued)
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);                  // (the last, unused copies land before the wave ends)
         return;
     }
 
@@ -1791,6 +1805,16 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
     const float *scl = reinterpret_cast<const float *>(X + NP * plane);
     const int u = min(w, i8_tiles(p.T) - 1);
     const int8_t *xp = X + (size_t)u * 2048 + 16 * lane;
+    // the epilogue's scales, fetched now (they come from HBM: one more
+    // round trip at the end otherwise)
+    const int t = 16 * w + l16;
+    const float st = scl[min(t, p.T - 1)];                   // the token's scale (block 0's entry)
+    float4 rsc[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int o = r0 + 16 * rt + 4 * gq;
+        rsc[rt] = *reinterpret_cast<const float4 *>(p.scale + (o < p.O ? o : 0));
+    }
     v4i xq[kDqX][NP][2];
     auto x_load = [&](int b, auto slot_c) __attribute__((always_inline)) {
         constexpr int sl = decltype(slot_c)::value;
@@ -1805,40 +1829,55 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
     for (int pl = 0; pl < NP; pl++)
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) ia[pl][rt] = v4i{0, 0, 0, 0};
-    auto block = [&](int b, auto slot_c) __attribute__((always_inline)) {
-        constexpr int sl = decltype(slot_c)::value;
+    // weight fragments of two blocks: block b + 1's are read from LDS while
+    // block b's products run (kDqX is even, so b's parity is static)
+    v4i wf[2][RT][2];
+    auto w_read = [&](int b, auto par_c) __attribute__((always_inline)) {
+        constexpr int par = decltype(par_c)::value;
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();                        // block b's weights are in LDS
         asm volatile("" ::: "memory");
         const int8_t *src = s_w + (b % SL) * WB + 16 * lane;
-        v4i wf[RT][2];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) wf[rt][h] = *reinterpret_cast<const v4i *>(src + (2 * rt + h) * 1024);
+            for (int h = 0; h < 2; h++) wf[par][rt][h] = *reinterpret_cast<const v4i *>(src + (2 * rt + h) * 1024);
+        __builtin_amdgcn_sched_barrier(0);                   // (all reads in flight before the products)
+    };
+    auto block = [&](int b, auto slot_c) __attribute__((always_inline)) {
+        constexpr int sl = decltype(slot_c)::value;
+        if (b + 1 < NB) w_read(b + 1, std::integral_constant<int, (sl + 1) % 2>{});
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
 #pragma unroll
             for (int pl = 0; pl < NP; pl++)
 #pragma unroll
                 for (int h = 0; h < 2; h++)
-                    ia[pl][rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[rt][h], xq[sl][pl][h], ia[pl][rt], 0, 0, 0);
+                    ia[pl][rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[sl % 2][rt][h], xq[sl][pl][h], ia[pl][rt], 0, 0, 0);
         x_load(b + kDqX, slot_c);                            // the ring slot just used, kDqX blocks ahead
     };
     static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { x_load(decltype(sc)::value, sc); });
+    w_read(0, std::integral_constant<int, 0>{});
+    if constexpr (NBC > 0) {
+        // (straight-line code: the x ring's waits count exactly the loads
+        // issued after the block's own, which they do not across a loop's
+        // back edge)
+#pragma unroll
+        for (int b = 0; b < NBC; b += kDqX)
+            static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { block(b + decltype(sc)::value, sc); });
+    } else {
 #pragma unroll 1
-    for (int b = 0; b < NB; b += kDqX)
-        static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { block(b + decltype(sc)::value, sc); });
+        for (int b = 0; b < NB; b += kDqX)
+            static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { block(b + decltype(sc)::value, sc); });
+    }
 
     // lane holds rows 4gq .. 4gq+3 of row tile rt for token l16 of token tile w
-    const int t = 16 * w + l16;
     if (t >= p.T) return;
-    const float st = scl[t];                                 // the token's scale (block 0's entry)
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int o = r0 + 16 * rt + 4 * gq;
         if (o >= p.O) continue;
-        const float4 sc = *reinterpret_cast<const float4 *>(p.scale + o);
+        const float4 sc = rsc[rt];
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -1861,7 +1900,9 @@ bool use_i8_dq(const ProjArgs &p) {
 }
 void launch_i8_dq(const ProjArgs &p, const F32Part &f, hipStream_t st) {
     const int nrg = (p.O + 16 * kDqRT - 1) / (16 * kDqRT);
-    hipLaunchKernelGGL(proj_i8_dq_kernel<kDqRT>, dim3(f.nwg + nrg), dim3(8 * OMH_WAVE), 0, st, p, f);
+    const dim3 grid(f.nwg + nrg), blk(8 * OMH_WAVE);
+    if (p.I == 16 * kI8Blk) hipLaunchKernelGGL((proj_i8_dq_kernel<kDqRT, 16>), grid, blk, 0, st, p, f);
+    else hipLaunchKernelGGL((proj_i8_dq_kernel<kDqRT, 0>), grid, blk, 0, st, p, f);
 }
 
 // Plan of the streaming kernel: T <= 64 tokens, RT row tiles per workgroup,
