@@ -113,12 +113,67 @@ __global__ __launch_bounds__(OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
     }
 }
 
+// One q or k row of the prep above by one wave, into an LDS row (the RoPE
+// pairs are read back from it): the same operations in the same order, so
+// the row is bit for bit the prep kernel's.  w = null: no norm, no RoPE (v).
+template <int HD>
+__device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, const float *w, int p, float *row,
+                                         int lane) {
+    constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
+    float v[NE];
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+        const int j = lane + OMH_WAVE * i;
+        v[i] = j < HD ? src[j] : 0.f;
+    }
+    if (w) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NE; i++) ss += v[i] * v[i];
+        ss = omh_xor_sum_from<1>(ss);
+        const float rr = 1.f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            const int j = lane + OMH_WAVE * i;
+            if (j < HD) {
+                v[i] = v[i] * rr * (1.f + w[j]);
+                row[j] = v[i];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");   // the wave's row is in LDS
+        __builtin_amdgcn_wave_barrier();
+        const int half = a.rot / 2;
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            const int j = lane + OMH_WAVE * i;
+            if (j < a.rot) {
+                const int jj = j < half ? j : j - half;
+                const float ang = (float)p * a.inv[jj];
+                const float cs = cosf(ang), sn = sinf(ang);
+                const float a0 = row[jj], b0 = row[jj + half];
+                v[i] = j < half ? a0 * cs - b0 * sn : b0 * cs + a0 * sn;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");   // every lane has read its pair
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+        const int j = lane + OMH_WAVE * i;
+        if (j < HD) row[j] = v[i];
+    }
+}
+
 // GPW = query heads per wave (the group's heads grp spread over the NW
 // waves: head wave + NW*i).  The hot loops carry no per-head conditions (a
 // branch there serialises every LDS read behind its own wait): a wave
 // whose head index runs past grp computes a copy of head grp-1 and does not
 // write it.
-template <int HD, int GPW>
+// PREP (decode steps, T = 1): the prep kernel's work is done here instead
+// of in a launch of its own: every workgroup forms its group's q rows
+// straight into LDS, and the workgroup whose split holds position pos writes
+// the new k and v rows into the cache before it reads any tile.
+template <int HD, int GPW, bool PREP = false>
 __global__ __launch_bounds__(AttnShape<HD>::NW * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all of each SIMD's registers
     using S = AttnShape<HD>;
@@ -147,10 +202,32 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
         }
         return;
     }
-    for (int e = tid; e < grp * NG4; e += NT) {
-        const int i = e / NG4, c = e % NG4;
-        *reinterpret_cast<float4 *>(qs + i * HD + 4 * c) =
-            *reinterpret_cast<const float4 *>(a.qb + ((size_t)t * H + (size_t)g * grp + i) * HD + 4 * c);
+    if constexpr (PREP) {
+        const int p = a.pos + t;
+        const float *row = a.qkv + (size_t)t * a.ld_qkv;
+        if (k0 <= p && p < k1) {
+            // the new k (wave 0, normed and rotated through a scratch LDS row)
+            // and v (wave 1) of kv head g go into the cache rows p
+            const size_t crow = (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
+            if (wave == 0) {
+                prep_row<HD>(a, row + (size_t)2 * H * HD + (size_t)g * HD, a.kn, p, Ks, lane);
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                for (int j = lane; j < HD; j += OMH_WAVE) a.Kc[crow + j] = Ks[j];
+            } else if (wave == 1) {
+                for (int j = lane; j < HD; j += OMH_WAVE) a.Vc[crow + j] = row[(size_t)2 * H * HD + (size_t)(KV + g) * HD + j];
+            }
+            __threadfence();                       // the rows are in memory before any tile load reads them
+            __syncthreads();
+        }
+        for (int i = wave; i < grp; i += NW)
+            prep_row<HD>(a, row + (size_t)(g * grp + i) * 2 * HD, a.qn, p, qs + i * HD, lane);
+    } else {
+        for (int e = tid; e < grp * NG4; e += NT) {
+            const int i = e / NG4, c = e % NG4;
+            *reinterpret_cast<float4 *>(qs + i * HD + 4 * c) =
+                *reinterpret_cast<const float4 *>(a.qb + ((size_t)t * H + (size_t)g * grp + i) * HD + 4 * c);
+        }
     }
     const float *qh[GPW];                          // this wave's heads' q rows in LDS
 #pragma unroll
@@ -307,6 +384,11 @@ struct FlashShape {
     static constexpr int PER = KT * HD / 4 / (8 * OMH_WAVE);   // float4 pieces of K (and of V) per thread
 };
 constexpr int kFlashMinT = 64;
+// decode steps fold the prep into the split kernel unless OMH_ATTN_FUSE=0 (comparison)
+bool fuse_prep() {
+    const char *e = getenv("OMH_ATTN_FUSE");
+    return !(e && e[0] == '0');
+}
 // the fp32-product flash kernel instead of the bf16 x 3 one (OMH_ATTN_FLASH=fp32, for comparison)
 bool flash_fp32() {
     const char *e = getenv("OMH_ATTN_FLASH");
@@ -694,13 +776,18 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     static const bool lds_ok = [] {
         bool ok = true;
         for (const void *f : {(const void *)attn_split_kernel<HD, 1>, (const void *)attn_split_kernel<HD, 2>,
-                              (const void *)attn_split_kernel<HD, 3>, (const void *)attn_split_kernel<HD, 4>})
+                              (const void *)attn_split_kernel<HD, 3>, (const void *)attn_split_kernel<HD, 4>,
+                              (const void *)attn_split_kernel<HD, 1, true>, (const void *)attn_split_kernel<HD, 2, true>,
+                              (const void *)attn_split_kernel<HD, 3, true>, (const void *)attn_split_kernel<HD, 4, true>})
             ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)AttnShape<HD>::LDS) == hipSuccess;
         return ok;
     }();
     if (!lds_ok) return hipErrorInvalidValue;
     static_assert(kAttnMaxGroup <= 4 * AttnShape<HD>::NW, "heads per wave");
-    hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
+    // decode steps: the prep is done inside the split kernel (OMH_ATTN_FUSE=0: its own launch, for comparison)
+    const bool flash = HD >= 128 && attn_uses_flash(a.T, HD);
+    const bool fuse = a.T == 1 && !flash && fuse_prep();
+    if (!fuse) hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
     if constexpr (HD >= 128) {
         if (attn_uses_flash(a.T, HD)) {
             const int wpg = ((a.T + 15) / 16 * (a.H / a.KV) + 7) / 8;
@@ -723,11 +810,21 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     }
     const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(AttnShape<HD>::NW * OMH_WAVE);
     const size_t lds = AttnShape<HD>::LDS;
-    switch ((a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, blk, lds, st, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, blk, lds, st, a); break;
-    case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3>), grid, blk, lds, st, a); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
+    const int gpw = (a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW;
+    if (fuse) {
+        switch (gpw) {
+        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1, true>), grid, blk, lds, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2, true>), grid, blk, lds, st, a); break;
+        case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3, true>), grid, blk, lds, st, a); break;
+        default: hipLaunchKernelGGL((attn_split_kernel<HD, 4, true>), grid, blk, lds, st, a); break;
+        }
+    } else {
+        switch (gpw) {
+        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, blk, lds, st, a); break;
+        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, blk, lds, st, a); break;
+        case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3>), grid, blk, lds, st, a); break;
+        default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
+        }
     }
     constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;
     hipLaunchKernelGGL((attn_combine_kernel<HD>), dim3((unsigned)(a.T * a.H * NCB)), dim3(kCombineWaves * OMH_WAVE), 0, st, a);

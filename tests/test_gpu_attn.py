@@ -231,3 +231,33 @@ def test_flash_bf16x3_matches_fp32_products(monkeypatch):
         finally:
             L.free()
     assert_close(outs["bf16x3"], outs["fp32"], atol=2e-5, rtol=2e-4, what="flash bf16x3 vs fp32")
+
+
+@pytest.mark.parametrize("shape", [Q35B_ATTN, (256, 8, 8, 32, 32), (512, 16, 1, 128, 128), (1024, 4, 4, 256, 256)],
+                         ids=["35b", "hd32-grp1", "hd128-grp16", "hd256-fullrope"])
+def test_decode_prep_in_split_kernel_matches_prep_launch(shape, monkeypatch):
+    """Decode steps form q, and the new k / v cache rows, inside the split
+    kernel (the workgroup whose key split holds the position writes the
+    rows); OMH_ATTN_FUSE=0 keeps the prep launch.  Same operations in the
+    same order: the outputs and the cache rows are equal bit for bit, over
+    decode steps at positions 62..65 after a 62-token prompt: the last rows
+    of the first 64-key split and the first of the second."""
+    D, H, KV, hd, rot = shape
+    rng = np.random.default_rng(29)
+    w = _weights(rng, D, H, KV, hd)
+    xs = [rng.normal(0, 1, (62, D)).astype(np.float32)] + [rng.normal(0, 1, (1, D)).astype(np.float32) for _ in range(4)]
+    outs = {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("OMH_ATTN_FUSE", mode)
+        L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, 80, w)
+        try:
+            got, pos = [], 0
+            for x in xs:
+                got.append(L.forward(0, pos, x))
+                pos += x.shape[0]
+            K, V = L.cache_get(0, 0, 0, pos)
+            outs[mode] = (np.concatenate(got), K, V)
+        finally:
+            L.free()
+    for a, b, nm in zip(outs["1"], outs["0"], ("out", "K cache", "V cache")):
+        np.testing.assert_array_equal(a, b, err_msg=f"{shape} fused prep vs prep launch: {nm}")
