@@ -5,7 +5,9 @@
 //
 // After the qkv projection (one launch_proj over the concatenated rows
 // [H x (q | gate), KV x k, KV x v], qwen.c:370-374) three launches:
-//  1. attn_prep_kernel, one wave per (token, head): RMSNorm of q and k with
+//  1. attn_prep_kernel, one workgroup per token (its RoPE cos / sin computed
+//     once, then a wave per head row; decode steps do this inside the split
+//     kernel instead): RMSNorm of q and k with
 //     (1 + w) weights (qwen.c:148-152, 385-386), partial RoPE over the first
 //     rot dims as two non-interleaved halves (qwen.c:388-398, inverse
 //     frequencies computed on the host as there), then q into a scratch row
@@ -48,77 +50,24 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-template <int HD>
-__global__ __launch_bounds__(OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
-    constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
-    __shared__ float sv[HD];
-    const int H = a.H, KV = a.KV, nr = H + 2 * KV;
-    const int t = blockIdx.x / nr, r = blockIdx.x % nr, lane = threadIdx.x;
-    const int p = a.pos + t;
-    const float *row = a.qkv + (size_t)t * a.ld_qkv;
-    const float *src, *w = nullptr;
-    float *dst;
-    if (r < H) {                                   // q of head r (then its gate)
-        src = row + (size_t)r * 2 * HD;
-        w = a.qn;
-        dst = a.qb + ((size_t)t * H + r) * HD;
-    } else if (r < H + KV) {                       // k of kv head g
-        const int g = r - H;
-        src = row + (size_t)2 * H * HD + (size_t)g * HD;
-        w = a.kn;
-        dst = a.Kc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
-    } else {                                       // v of kv head g
-        const int g = r - H - KV;
-        src = row + (size_t)2 * H * HD + (size_t)(KV + g) * HD;
-        dst = a.Vc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
-    }
-    float v[NE];
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int j = lane + OMH_WAVE * i;
-        v[i] = j < HD ? src[j] : 0.f;
-    }
-    if (w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < NE; i++) ss += v[i] * v[i];
-        ss = omh_xor_sum_from<1>(ss);
-        const float rr = 1.f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-        for (int i = 0; i < NE; i++) {
-            const int j = lane + OMH_WAVE * i;
-            if (j < HD) {
-                v[i] = v[i] * rr * (1.f + w[j]);
-                sv[j] = v[i];
-            }
-        }
-        __syncthreads();
-        const int half = a.rot / 2;
-#pragma unroll
-        for (int i = 0; i < NE; i++) {
-            const int j = lane + OMH_WAVE * i;
-            if (j < a.rot) {
-                const int jj = j < half ? j : j - half;
-                const float ang = (float)p * a.inv[jj];
-                const float cs = cosf(ang), sn = sinf(ang);
-                const float a0 = sv[jj], b0 = sv[jj + half];
-                v[i] = j < half ? a0 * cs - b0 * sn : b0 * cs + a0 * sn;
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int j = lane + OMH_WAVE * i;
-        if (j < HD) dst[j] = v[i];
-    }
+// cos and sin of p * inv[j] for j < rot / 2 into LDS tables, by the threads
+// of a workgroup.  One out-of-line function computes them wherever a kernel
+// needs them, so every kernel rotates with the same bits.
+__device__ __attribute__((noinline)) void rope_cos_sin(float ang, float *c, float *s) {
+    *c = cosf(ang);
+    *s = sinf(ang);
+}
+__device__ __forceinline__ void rope_table(const AttnArgs &a, int p, float *cs, float *sn, int tid, int nthreads) {
+    for (int j = tid; j < a.rot / 2; j += nthreads) rope_cos_sin((float)p * a.inv[j], cs + j, sn + j);
 }
 
-// One q or k row of the prep above by one wave, into an LDS row (the RoPE
-// pairs are read back from it): the same operations in the same order, so
-// the row is bit for bit the prep kernel's.  w = null: no norm, no RoPE (v).
+// One q or k row of the prep (RMSNorm with 1 + w, then partial RoPE as two
+// non-interleaved halves), or a v row (w = null: copied), by one wave, into
+// an LDS row (the RoPE pairs are read back from it).  cs_t / sn_t: the
+// token's rope_table.
 template <int HD>
-__device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, const float *w, int p, float *row,
-                                         int lane) {
+__device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, const float *w, float *row, int lane,
+                                         const float *cs_t, const float *sn_t) {
     constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
     float v[NE];
 #pragma unroll
@@ -131,7 +80,7 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
 #pragma unroll
         for (int i = 0; i < NE; i++) ss += v[i] * v[i];
         ss = omh_xor_sum_from<1>(ss);
-        const float rr = 1.f / sqrtf(ss / (float)HD + a.eps);
+        const float rr = 1.f / sqrtf(ss / (float)HD + a.eps);   // qwen.c:148-152
 #pragma unroll
         for (int i = 0; i < NE; i++) {
             const int j = lane + OMH_WAVE * i;
@@ -146,10 +95,9 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
 #pragma unroll
         for (int i = 0; i < NE; i++) {
             const int j = lane + OMH_WAVE * i;
-            if (j < a.rot) {
+            if (j < a.rot) {                                     // qwen.c:388-398
                 const int jj = j < half ? j : j - half;
-                const float ang = (float)p * a.inv[jj];
-                const float cs = cosf(ang), sn = sinf(ang);
+                const float cs = cs_t[jj], sn = sn_t[jj];
                 const float a0 = row[jj], b0 = row[jj + half];
                 v[i] = j < half ? a0 * cs - b0 * sn : b0 * cs + a0 * sn;
             }
@@ -163,6 +111,45 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
         if (j < HD) row[j] = v[i];
     }
 }
+
+// The prep: one workgroup of kPrepWaves waves per token.  The token's RoPE
+// cos and sin (rot / 2 frequencies) go into LDS once, then wave w takes rows
+// w, w + kPrepWaves, ... of [H q heads, KV k heads, KV v heads]: q into the
+// scratch, k and v into the cache rows pos + t.
+constexpr int kPrepWaves = 4;
+template <int HD>
+__global__ __launch_bounds__(kPrepWaves * OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
+    __shared__ float cs[HD / 2], sn[HD / 2], sv[kPrepWaves][HD];
+    const int H = a.H, KV = a.KV, nr = H + 2 * KV;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int p = a.pos + t;
+    rope_table(a, p, cs, sn, tid, kPrepWaves * OMH_WAVE);
+    __syncthreads();
+    const float *row = a.qkv + (size_t)t * a.ld_qkv;
+    for (int r = wv; r < nr; r += kPrepWaves) {
+        const float *src, *w = nullptr;
+        float *dst;
+        if (r < H) {                                   // q of head r (then its gate)
+            src = row + (size_t)r * 2 * HD;
+            w = a.qn;
+            dst = a.qb + ((size_t)t * H + r) * HD;
+        } else if (r < H + KV) {                       // k of kv head g
+            const int g = r - H;
+            src = row + (size_t)2 * H * HD + (size_t)g * HD;
+            w = a.kn;
+            dst = a.Kc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
+        } else {                                       // v of kv head g
+            const int g = r - H - KV;
+            src = row + (size_t)2 * H * HD + (size_t)(KV + g) * HD;
+            dst = a.Vc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
+        }
+        prep_row<HD>(a, src, w, sv[wv], lane, cs, sn);
+        // (each lane copies the entries it wrote itself)
+        for (int j = lane; j < HD; j += OMH_WAVE) dst[j] = sv[wv][j];
+    }
+}
+
 
 // GPW = query heads per wave (the group's heads grp spread over the NW
 // waves: head wave + NW*i).  The hot loops carry no per-head conditions (a
@@ -205,12 +192,15 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
     if constexpr (PREP) {
         const int p = a.pos + t;
         const float *row = a.qkv + (size_t)t * a.ld_qkv;
+        float *cs = Ks + HD, *sn = cs + HD / 2;     // (the K tile region is free until the first tile)
+        rope_table(a, p, cs, sn, tid, NT);
+        __syncthreads();
         if (k0 <= p && p < k1) {
             // the new k (wave 0, normed and rotated through a scratch LDS row)
             // and v (wave 1) of kv head g go into the cache rows p
             const size_t crow = (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
             if (wave == 0) {
-                prep_row<HD>(a, row + (size_t)2 * H * HD + (size_t)g * HD, a.kn, p, Ks, lane);
+                prep_row<HD>(a, row + (size_t)2 * H * HD + (size_t)g * HD, a.kn, Ks, lane, cs, sn);
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
                 __builtin_amdgcn_wave_barrier();
                 for (int j = lane; j < HD; j += OMH_WAVE) a.Kc[crow + j] = Ks[j];
@@ -221,7 +211,7 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
             __syncthreads();
         }
         for (int i = wave; i < grp; i += NW)
-            prep_row<HD>(a, row + (size_t)(g * grp + i) * 2 * HD, a.qn, p, qs + i * HD, lane);
+            prep_row<HD>(a, row + (size_t)(g * grp + i) * 2 * HD, a.qn, qs + i * HD, lane, cs, sn);
     } else {
         for (int e = tid; e < grp * NG4; e += NT) {
             const int i = e / NG4, c = e % NG4;
@@ -787,7 +777,7 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     // decode steps: the prep is done inside the split kernel (OMH_ATTN_FUSE=0: its own launch, for comparison)
     const bool flash = HD >= 128 && attn_uses_flash(a.T, HD);
     const bool fuse = a.T == 1 && !flash && fuse_prep();
-    if (!fuse) hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)(a.T * (a.H + 2 * a.KV))), dim3(OMH_WAVE), 0, st, a);
+    if (!fuse) hipLaunchKernelGGL((attn_prep_kernel<HD>), dim3((unsigned)a.T), dim3(kPrepWaves * OMH_WAVE), 0, st, a);
     if constexpr (HD >= 128) {
         if (attn_uses_flash(a.T, HD)) {
             const int wpg = ((a.T + 15) / 16 * (a.H / a.KV) + 7) / 8;
