@@ -1903,8 +1903,7 @@ void launch_i8_dq(const ProjArgs &p, const F32Part &f, hipStream_t st) {
 // device in one round of workgroups (one per CU, 256, the fp32-row ones
 // included), and a k split or more rows per workgroup only pay where they
 // are needed for that.  So: the most workgroups up to 256, then the
-// smallest G, then the smallest RT.  rt = 0: not taken.  OMH_I8_RT /
-// OMH_I8_G restrict the choice (tuning).
+// smallest G, then the smallest RT.  rt = 0: not taken.
 struct StPlan {
     int rt, nt, nb, G;
 };
@@ -1912,17 +1911,12 @@ constexpr int kCUs = 256;
 StPlan i8_stream_plan(int O, int T, int I, int nf32) {
     StPlan best{0, 0, 0, 1};
     if (T > 64 || I % (4 * kI8Blk) != 0) return best;
-    if (const char *e = getenv("OMH_I8_STREAM"))
-        if (e[0] == '0') return best;
-    const int want_rt = getenv("OMH_I8_RT") ? atoi(getenv("OMH_I8_RT")) : 0;
-    const int want_g = getenv("OMH_I8_G") ? atoi(getenv("OMH_I8_G")) : 0;
     const int tiles = (O + 15) / 16, nblk = I / kI8Blk, nt = T <= 16 ? 1 : 4;
     long best_wgs = 0;
     for (int G = 1; G <= 8; G *= 2)
         for (int rt = 1; rt <= 4; rt++) {
             const int nb = nblk / (4 * G);
             if (nb * 4 * G != nblk || (nb != 1 && nb != 2 && nb != 4)) continue;
-            if ((want_rt && rt != want_rt) || (want_g && G != want_g)) continue;
             const long wgs = (long)(tiles + rt - 1) / rt * G + nf32;
             if (wgs > kCUs || wgs <= best_wgs) continue;
             best = StPlan{rt, nt, nb, G};
@@ -1972,7 +1966,6 @@ void launch_i8_stream(const ProjArgs &p, const StPlan &sp, const F32Part &f, hip
 // kI8Waves waves, then a k split over G workgroups while there are fewer
 // than kI8Waves waves and every wave keeps at least two 128-wide blocks.
 // TT = 0: the kernel does not take the shape (I not a multiple of 1024).
-// OMH_I8_TT / OMH_I8_G override the choice (tuning).
 constexpr int kI8Waves = 1024;
 WvPlan i8_plan(int O, int T, int I) {
     WvPlan w{0, 1};
@@ -1981,25 +1974,17 @@ WvPlan i8_plan(int O, int T, int I) {
     auto waves = [&](int tt) { return rg * ((T + 16 * tt - 1) / (16 * tt)) * 4; };
     int tt = T <= 16 ? 1 : 2;                     // (a 64-token tile needs more registers than a wave has)
     while (tt > 1 && waves(tt) < kI8Waves) tt /= 2;
-    if (const char *e = getenv("OMH_I8_TT")) tt = atoi(e) == 2 ? 2 : 1;
     // (a wave's k range is an even number of 128-wide blocks: I % (1024 G) == 0)
     if (I % (8 * kI8Blk) != 0) return w;
     while (w.G < 8 && waves(tt) * w.G < kI8Waves && I % (8 * kI8Blk * 2 * w.G) == 0) w.G *= 2;
-    if (const char *e = getenv("OMH_I8_G")) {
-        const int gg = atoi(e);
-        if ((gg == 1 || gg == 2 || gg == 4 || gg == 8) && I % (8 * kI8Blk * gg) == 0) w.G = gg;
-    }
     w.TT = tt;
     return w;
 }
 
 // The projection variant for int8 rows with T > 4: the int8-core kernel
-// where it takes the shape, else the bf16 x 3 kernels (OMH_PROJ_Q8=bf16x3
-// selects those everywhere, for comparison).
+// where it takes the shape, else the bf16 x 3 kernels.
 bool use_i8(int T, int I, int n_q) {
-    if (n_q <= 0 || T <= 4 || i8_plan(n_q, T, I).TT == 0) return false;
-    const char *e = getenv("OMH_PROJ_Q8");
-    return !(e && strcmp(e, "bf16x3") == 0);
+    return n_q > 0 && T > 4 && i8_plan(n_q, T, I).TT != 0;
 }
 
 template <int TT, bool PT>

@@ -917,6 +917,10 @@ static int attn_cache_copy(int li, int seq, int t0, int n, float *K, float *V, i
         return fail(OMH_ERR_ARG, "attn cache: rows %d..%d outside the cache of %d (host rows %d)", t0, t0 + n - 1,
                     d.max_t, ld_t);
     if (n == 0) return OMH_OK;
+    // Work a caller enqueued on its own streams (omh_attn_forward_dev) may
+    // still be writing or reading these rows: wait for the whole device
+    // first, as omh_gdn_state_get / _set do.
+    HIP_OK(hipDeviceSynchronize());
     const size_t hd = d.head_dim, row = hd * sizeof(float), w = (size_t)n * row;
     for (int h = 0; h < d.n_kv; h++) {
         const size_t dev_off = (((size_t)seq * d.n_kv + h) * d.max_t + t0) * hd;

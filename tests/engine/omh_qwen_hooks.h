@@ -39,11 +39,31 @@ static int omh_ready(Model *m) {
     return omh_on == 1;
 }
 
+/* Test-only fault injection, from the host (no GPU call is made for it):
+ * OMH_TEST_FAIL_LAYER=k makes the GPU call of engine layer k report a
+ * failure, so the fallback below runs mid-step.  Unset: never. */
+static int omh_fail_layer = -2;          /* -2: not read yet; -1: off */
+static int omh_injected = 0;             /* the last failure was injected */
+static int omh_injected_failure(int li) {
+    if (omh_fail_layer == -2) {
+        const char *e = getenv("OMH_TEST_FAIL_LAYER");
+        omh_fail_layer = e && e[0] ? atoi(e) : -1;
+    }
+    omh_injected = li == omh_fail_layer;
+    return omh_injected;
+}
+
 /* Hand every uploaded layer's state back to the engine's arrays and stay on
- * the CPU from here on. */
-static void omh_fallback(Model *m, const char *where) {
-    fprintf(stderr, "om_hip: %s failed (%s); continuing on the CPU\n", where, omh_last_error());
-    int rows = m->pos + 1 < m->max_t ? m->pos + 1 : m->max_t;   /* row pos: written or rewritten next */
+ * the CPU from here on.  nt: tokens of the step in progress (1 for step(),
+ * T for a batched prompt step), so attention layers that ran earlier in it
+ * have written cache rows up to pos + nt - 1 on the device: all of rows
+ * 0 .. pos + nt - 1 come back (the failing layer's own rows are rewritten by
+ * its CPU body next). */
+static void omh_fallback(Model *m, const char *where, int nt) {
+    fprintf(stderr, "om_hip: %s failed (%s); continuing on the CPU\n", where,
+            omh_injected ? "injected by OMH_TEST_FAIL_LAYER" : omh_last_error());
+    const long want = (long)m->pos + (nt > 0 ? nt : 1);
+    int rows = want < m->max_t ? (int)want : m->max_t;
     for (int i = 0; i < omh_nl; i++) {
         if (!omh_up[i]) continue;
         if (m->L[i].is_full) omh_attn_cache_get(i, 0, 0, rows, m->K[i], m->V[i], m->max_t);
@@ -88,11 +108,13 @@ static int omh_attn_upload(Model *m, Layer *l, int li) {
     return omh_attn_cache_set(li, 0, 0, m->pos, m->K[li], m->V[li], m->max_t) == 0 ? 0 : -1;
 }
 
-static int omh_layer_on(Model *m, Layer *l, int li) {
+/* Whether layer li runs on the GPU; uploads it on first use.  nt: tokens of
+ * the step in progress (see omh_fallback). */
+static int omh_layer_on(Model *m, Layer *l, int li, int nt) {
     if (!omh_ready(m) || li < 0 || li >= omh_nl) return 0;
     if (!omh_up[li]) {
         if ((l->is_full ? omh_attn_upload(m, l, li) : omh_gdn_upload(m, l, li)) != 0) {
-            omh_fallback(m, l->is_full ? "attention layer upload" : "GDN layer upload");
+            omh_fallback(m, l->is_full ? "attention layer upload" : "GDN layer upload", nt);
             return 0;
         }
         omh_up[li] = 1;
@@ -102,17 +124,17 @@ static int omh_layer_on(Model *m, Layer *l, int li) {
 
 /* deltanet_step's hook: 1 = done on the GPU. */
 static int omh_gdn_hook(Model *m, Layer *l, int li, const float *x, float *out) {
-    if (!omh_layer_on(m, l, li)) return 0;
-    if (omh_gdn_decode(li, 1, x, out) == 0) return 1;
-    omh_fallback(m, "omh_gdn_decode");
+    if (!omh_layer_on(m, l, li, 1)) return 0;
+    if (!omh_injected_failure(li) && omh_gdn_decode(li, 1, x, out) == 0) return 1;
+    omh_fallback(m, "omh_gdn_decode", 1);
     return 0;
 }
 
 /* attn_step's hook: 1 = done on the GPU. */
 static int omh_attn_hook(Model *m, Layer *l, int li, const float *x, int pos, float *out) {
-    if (!omh_layer_on(m, l, li)) return 0;
-    if (omh_attn_forward(li, 0, pos, 1, x, out) == 0) return 1;
-    omh_fallback(m, "omh_attn_forward");
+    if (!omh_layer_on(m, l, li, 1)) return 0;
+    if (!omh_injected_failure(li) && omh_attn_forward(li, 0, pos, 1, x, out) == 0) return 1;
+    omh_fallback(m, "omh_attn_forward", 1);
     return 0;
 }
 
@@ -122,7 +144,7 @@ static void omh_reset(Model *m) {
     if (omh_on != 1) return;
     for (int i = 0; i < omh_nl; i++)
         if (omh_up[i] && !m->L[i].is_full && omh_gdn_state_reset(i, 0) != 0) {
-            omh_fallback(m, "omh_gdn_state_reset");
+            omh_fallback(m, "omh_gdn_state_reset", 1);
             return;
         }
 }

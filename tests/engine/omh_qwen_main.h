@@ -1,5 +1,6 @@
 /* omh_qwen_main.h — the batched prompt step and the teacher-forced gate for
- * the reference engine (engines/qwen.c), included right before its main().
+ * the reference engine (engines/qwen.c), included right before its serve()
+ * (qwen.c:566), so both serve() and the validation main() can use them.
  *
  * The reference feeds a prompt token by token through step() (qwen.c:588,
  * 637).  omh_step_batch() runs T tokens through the stack layer by layer,
@@ -10,8 +11,15 @@
  * OM_HIP=0, or a fallback) runs its T tokens through the engine's own
  * deltanet_step / attn_step in order, which is the same recurrence.
  *
+ *   serve (--serve)           each request's ids (qwen.c:588) are one
+ *                             omh_step_batch call, continuing from the
+ *                             current position and state (reset:false) or
+ *                             from zero (reset:true); OMH_BATCH_PROMPT=0
+ *                             keeps the reference's token-by-token loop;
  *   OMH_BATCH_PROMPT=1        the validation main prefills its prompt in
- *                             one omh_step_batch call instead of np step()s;
+ *                             one omh_step_batch call instead of np step()s
+ *                             (off by default, so the reference's own gate
+ *                             runs as the reference runs it);
  *   <engine> --tf ref.json    teacher-forced gate: one omh_step_batch over
  *                             full_ids, argmax per position against the
  *                             reference's tf_argmax (transformers' chunked
@@ -20,6 +28,8 @@
  */
 #ifndef OMH_QWEN_MAIN_H
 #define OMH_QWEN_MAIN_H
+
+static int *read_ints(jval *o, const char *key, int *n);   /* defined by the engine after serve() */
 
 /* T tokens at positions m->pos ..; logits of every position into
  * all_logits [T][vocab] when it is not NULL; returns the last position's
@@ -36,11 +46,12 @@ static float *omh_step_batch(Model *m, const int *ids, int T, float *all_logits)
         double tt = now_s();
         int done = 0;
 #ifdef OM_HIP
-        if (omh_layer_on(m, l, i)) {
+        if (omh_layer_on(m, l, i, T)) {
             /* the GPU writes out[T][D] densely; tmp rows are D apart here */
-            done = (l->is_full ? omh_attn_forward(i, 0, m->pos, T, nrm, tmp)
+            done = !omh_injected_failure(i) &&
+                   (l->is_full ? omh_attn_forward(i, 0, m->pos, T, nrm, tmp)
                                : omh_gdn_prefill(i, 0, T, nrm, tmp)) == 0;
-            if (!done) omh_fallback(m, l->is_full ? "omh_attn_forward (prompt)" : "omh_gdn_prefill");
+            if (!done) omh_fallback(m, l->is_full ? "omh_attn_forward (prompt)" : "omh_gdn_prefill", T);
         }
 #endif
         if (!done) {
@@ -85,6 +96,23 @@ static int omh_batch_prompt(void) {
  * OMH_BATCH_PROMPT=1 the prompt is one batched step, else the loop runs. */
 #define OMH_PROMPT(m, ids, n, logit) \
     if (omh_batch_prompt()) { free(logit); logit = omh_step_batch((m), (ids), (n), NULL); } else
+
+/* serve()'s request ids (a JSON array, PROTOCOL.md) as one batched step. */
+static int omh_serve_batch(void) {
+    const char *e = getenv("OMH_BATCH_PROMPT");
+    return !(e && e[0] == '0');
+}
+static float *omh_serve_prompt(Model *m, jval *jids, int nids) {
+    int *ids = malloc((size_t)nids * sizeof(int));
+    for (int i = 0; i < nids; i++) ids[i] = (int)jids->kids[i]->num;
+    float *logit = omh_step_batch(m, ids, nids, NULL);
+    free(ids);
+    return logit;
+}
+
+/* Placed in front of serve()'s prompt loop (qwen.c:588). */
+#define OMH_SERVE_PROMPT(m, jids, nids, logit) \
+    if (omh_serve_batch() && (nids) > 0) { free(logit); logit = omh_serve_prompt((m), (jids), (nids)); } else
 
 /* Teacher-forced gate over ref.json's full_ids against tf_argmax. */
 static int omh_tf_gate(const char *snap, const char *refpath) {

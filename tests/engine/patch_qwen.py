@@ -12,7 +12,11 @@ messages keep pointing at the reference file's own lines.
 Hook points (each must match exactly once, or the build fails):
   - deltanet_step (qwen.c:301): the GDN layer's GPU call;
   - attn_step (qwen.c:367): the attention layer's GPU call;
+  - serve (qwen.c:566): the batched prompt step and the teacher-forced gate
+    (omh_qwen_main.h) are included in front of it;
   - the reset branch of serve (qwen.c:576): device states reset too;
+  - serve's prompt loop (qwen.c:588): the prompt as one batched step (unless
+    OMH_BATCH_PROMPT=0);
   - main (qwen.c:616): the teacher-forced gate (--tf) and, in front of the
     prompt loop (qwen.c:637), the batched prompt step (OMH_BATCH_PROMPT=1).
 
@@ -27,10 +31,14 @@ HOOKS = [
      ['#include "omh_qwen_hooks.h"'], ["    OMH_GDN_HOOK(m, l, li, x, out);"]),
     (r"static void attn_step\(Model \*m, Layer \*l, int li, const float \*x, int pos, float \*out\) \{",
      [], ["    OMH_ATTN_HOOK(m, l, li, x, pos, out);"]),
+    (r"static int serve\(const char \*snap\) \{",
+     ['#include "omh_qwen_main.h"'], []),
     (r"\s*if \(reset\) \{",
      [], ["            OMH_RESET(&m);"]),
+    (r"\s*for \(int i = 0; i < nids; i\+\+\) \{ free\(logit\); logit = step\(&m,\(int\)jids->kids\[i\]->num\); \}",
+     ["        OMH_SERVE_PROMPT(&m, jids, nids, logit)"], []),
     (r"int main\(int argc, char \*\*argv\) \{",
-     ['#include "omh_qwen_main.h"'], ["    OMH_MAIN_HOOK(argc, argv);"]),
+     [], ["    OMH_MAIN_HOOK(argc, argv);"]),
     (r"\s*for \(int i = 0; i < np; i\+\+\) \{ free\(logit\); logit = step\(&m, prompt\[i\]\); \}",
      ["    OMH_PROMPT(&m, prompt, np, logit)"], []),
 ]

@@ -101,9 +101,18 @@ def test_tiny_teacher_forced_with_gpu_attention_prompt_step():
 @pytest.mark.parametrize("steps", [[1, 1, 1], [37, 1, 1], [200, 1, 64, 1], [37, 100, 1, 71]],
                          ids=["decode", "prompt37", "prompt200", "prompt-after-prompt"])
 def test_35b_shape_prompt_then_decode(steps):
-    """Prompt steps of 64 tokens and more run on the flash kernel (fp32
-    matrix cores), shorter ones and decode steps on the split kernel; a
-    prompt step may start after earlier tokens (pos > 0)."""
+    """Prompt steps of 64 tokens and more run on a flash kernel (the
+    default bf16 x 3 one, three bf16 products per fp32 product, and the
+    fp32-product one that OMH_ATTN_FLASH=fp32 selects), shorter ones and
+    decode steps on the split kernel; a prompt step may start after earlier
+    tokens (pos > 0)."""
+    _run(Q35B_ATTN, steps)
+
+
+@pytest.mark.parametrize("steps", [[200, 1, 64, 1], [37, 100, 1, 71]], ids=["prompt200", "prompt-after-prompt"])
+def test_35b_shape_prompt_then_decode_fp32_flash(steps, monkeypatch):
+    """The same sequences with prompt steps on the fp32-product flash kernel."""
+    monkeypatch.setenv("OMH_ATTN_FLASH", "fp32")
     _run(Q35B_ATTN, steps)
 
 
@@ -182,6 +191,34 @@ def test_device_pointer_entry_matches_host_entry():
             st.synchronize()
             np.testing.assert_array_equal(od.numpy((T, D)), B.forward(0, pos, x))
             pos += T
+    finally:
+        A.free()
+        B.free()
+
+
+def test_cache_get_waits_for_device_pointer_calls():
+    """omh_attn_cache_get right after omh_attn_forward_dev on a caller's
+    stream, with no synchronisation in between: the copy waits for the
+    device (as omh_gdn_state_get does), so it returns the rows the step
+    wrote, equal to those of the same step run through the host entry."""
+    from overhang_amd import hip
+    D, H, KV, hd, rot = Q35B_ATTN
+    rng = np.random.default_rng(22)
+    w = _weights(rng, D, H, KV, hd)
+    T = 2048
+    A = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, T, w)
+    B = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, T, w)
+    st = hip.Stream()
+    try:
+        x = rng.normal(0, 1, (T, D)).astype(np.float32)
+        B.forward(0, 0, x)
+        Kb, Vb = B.cache_get(0, 0, T)
+        xd, od = hip.Buffer.from_numpy(x), hip.Buffer(T * D * 4)
+        gdn.attn_forward_dev(A.li, 0, 0, T, xd, od, stream=st)
+        Ka, Va = A.cache_get(0, 0, T)            # no st.synchronize() before it
+        np.testing.assert_array_equal(Ka, Kb)
+        np.testing.assert_array_equal(Va, Vb)
+        st.synchronize()
     finally:
         A.free()
         B.free()
