@@ -226,11 +226,12 @@ __device__ __forceinline__ float4 delta_rule(float4 (&s)[RPT], float *Sp, const 
     const float4 delta = f4_scale(f4_sub(vv, kv), hc.beta);
     const float4 o = f4_fma(delta, hc.kq, f4_scale(aq, hc.gam * hc.rq));
     const float4 d2 = f4_scale(delta, hc.rk);
+    const __amdgpu_buffer_rsrc_t rs = omh_rsrc(Sp, KD * VD * 4);
 #pragma unroll
     for (int m = 0; m < RPT; m++) {
         const int i = rg + RG * m;
         s[m] = f4_fma(d2, s_k[i], f4_scale(s[m], hc.gam));
-        omh_st_stream(Sp + (size_t)i * VD + c4 * 4, s[m]);
+        omh_st_stream_buf(rs, (i * VD + c4 * 4) * 4, s[m]);
     }
     return o;
 }
@@ -243,8 +244,9 @@ template <int KD, int VD, int RPT>
 __device__ __forceinline__ void load_head(float4 (&s)[RPT], const float *Sp, int rg, int c4) {
     using Sh = PairShape<KD, VD>;
     static_assert(RPT == Sh::RPT, "tile rows");
+    const __amdgpu_buffer_rsrc_t rs = omh_rsrc(Sp, KD * VD * 4);
 #pragma unroll
-    for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream(Sp + (size_t)(rg + Sh::RG * m) * VD + c4 * 4);
+    for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream_buf(rs, ((rg + Sh::RG * m) * VD + c4 * 4) * 4);
 }
 
 // Where the core output also goes, when the decode step feeds an int8
@@ -502,8 +504,9 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     const float galog = L.A_log[h], gdt = L.dt_bias[h];
 
     float4 s[RPT];
+    const __amdgpu_buffer_rsrc_t rs = omh_rsrc(Sp, (KD * VD - col0) * 4);
 #pragma unroll
-    for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream(Sp + (size_t)(rg + RG * m) * VD + c4 * 4);
+    for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream_buf(rs, ((rg + RG * m) * VD + c4 * 4) * 4);
     __builtin_amdgcn_sched_barrier(0);           // keep prologue arithmetic after the state requests
 
     const bool own_qk = (h % rep == 0) && cs == 0;

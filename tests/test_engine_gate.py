@@ -153,3 +153,52 @@ def test_engine_fallback_mid_step_hands_state_back(layer, batched):
     r = run([REFJ], OMH_BATCH_PROMPT=batched, OMH_TEST_FAIL_LAYER=str(layer))
     assert ON_GPU in r.stderr and "injected by OMH_TEST_FAIL_LAYER" in r.stderr, r.stderr[-300:]
     assert r.returncode == 0 and "greedy match: 20/20" in r.stdout, r.stdout[-300:]
+
+
+# ---- the engine's int8 container (stream mode, qwen.c:213-218, 269-274) ----
+
+@pytest.fixture(scope="module")
+def int8_container(tmp_path_factory):
+    """The reference tiny model rewritten as an int8 container
+    (tests/golden/make_int8_container.py: routed experts as row-wise int8 +
+    .qs scales, the reference converter's layout).  Loading it puts the
+    engine in stream mode: it quantises the GDN in_proj_qkv / in_proj_z /
+    out_proj and the attention projections to int8 twins at load, so the
+    hooks upload those twins (the m->stream branches of omh_gdn_upload and
+    omh_attn_upload)."""
+    from tests.golden.make_int8_container import write_container
+    dst = str(tmp_path_factory.mktemp("qwen_tiny_i8"))
+    write_container(TINY, dst)
+    return dst
+
+
+STREAM = "streaming experts: int8 container"
+
+
+def test_engine_int8_container_cpu_gates(int8_container):
+    """OM_HIP=0 on the int8 container: the engine runs in stream mode and
+    still reproduces the reference's greedy 20/20 and teacher-forced 28/28."""
+    r = run([REFJ], OM_HIP="0", SNAP=int8_container)
+    assert STREAM in r.stderr and r.returncode == 0 and "greedy match: 20/20" in r.stdout, r.stdout[-300:]
+    r = run(["--tf", REFJ], OM_HIP="0", SNAP=int8_container)
+    assert r.returncode == 0 and "teacher-forced match: 28/28" in r.stdout, r.stdout[-300:]
+
+
+def _engine_line(out):
+    return [ln for ln in out.splitlines() if ln.startswith("engine   :")][0]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("args,env", [([REFJ], {}), ([REFJ], {"OMH_BATCH_PROMPT": "1"}), (["--tf", REFJ], {})],
+                         ids=["greedy", "greedy-batched-prompt", "teacher-forced"])
+def test_engine_int8_container_on_gpu(int8_container, args, env):
+    """Stream mode with the GDN and attention layers on the GPU as int8
+    twins (in_proj / out_proj and q/k/v/o through the int8 kernels): the
+    same ids as the CPU engine on the same container, and the reference's
+    gates (greedy 20/20, teacher-forced 28/28)."""
+    gpu = run(args, SNAP=int8_container, **env)
+    cpu = run(args, SNAP=int8_container, OM_HIP="0", **env)
+    assert STREAM in gpu.stderr and ON_GPU in gpu.stderr, gpu.stderr[-300:]
+    assert "continuing on the CPU" not in gpu.stderr, gpu.stderr[-300:]
+    assert _engine_line(gpu.stdout) == _engine_line(cpu.stdout)
+    assert gpu.returncode == 0, gpu.stdout[-300:]

@@ -155,12 +155,13 @@ def test_35b_block_drop_in_small_batch(B, int8):
     L.free()
 
 
-@pytest.mark.parametrize("T", [256, 333, 1024])
+@pytest.mark.parametrize("T", [65, 128, 255, 256, 333, 1024])
 def test_35b_int8_prefill_block_matches_oracle(T):
     """Row f2 at prefill size: the 35B-A3B int8 layer through
     omh_gdn_prefill, whose int8 projections (in_proj 2048 -> 12352 with the
-    fp32 b/a rows beside, out_proj 4096 -> 2048) run on the int8 matrix-core
-    GEMM from 256 tokens (T = 333: partial token tiles), continuing from a
+    fp32 b/a rows beside, out_proj 4096 -> 2048) run on the int8 wave-tile
+    kernel for 65..255 tokens and on the int8 matrix-core GEMM from 256
+    tokens (T = 65, 255, 333: partial token tiles), continuing from a
     nonzero state.  Every token's output and the final state and conv
     history are compared with the per-token oracle (engines/qwen.c:301-364
     with matmul_q, qwen.c:94-122)."""
