@@ -108,9 +108,22 @@ __device__ __forceinline__ void load_x16(const float *src, float (&x)[16]) {
 }
 
 // ---------------------------------------------------------------- GEMV
-// A workgroup is 4 waves = RG row groups of kGemvRows rows x KS k-slices;
-// each wave covers its k-slice in chunks of 1024 (16 per lane).
+// Up to 4 tokens (decode).  int8 rows: a workgroup is 4 waves = RG row
+// groups of kGemvRows rows x KS k-slices; a wave covers its k-slice in
+// chunks of 1024 (16 per lane; one chunk per slice at the engine's shapes,
+// where the slices are 1024 wide).  Per chunk the wave requests x first (an L2 hit after the launch's first
+// waves), then every weight fragment of its rows, and sums the rows in
+// that order: the load counter completes in issue order, so the
+// conversion and products of the first rows run while the later rows'
+// weights still stream in.  fp32 rows (in_proj's b/a rows, or a whole fp32
+// matrix) take workgroups of their own, one row per wave over the full k,
+// so their four-times wider weights do not leave a few workgroups
+// straggling.  35B in_proj at one token with its weights from HBM (12288
+// int8 rows + 64 fp32 rows, 25.7 MB), MI355X: 6.9 us, against 10.4 us with
+// the fp32 rows inside the int8 workgroups and x requested after the
+// weights (a plain read of the same bytes: 5.3 us).
 constexpr int kGemvRows = 8;
+constexpr int kGemvCB = 1;            // chunks per request group
 
 // Sum of v[i] over the 64 lanes for 8 values at once, halving the set at
 // each of the first three exchanges: lane L ends with the total of value
@@ -135,35 +148,51 @@ __device__ __forceinline__ float sum8_over_lanes(const float (&v)[8], int lane) 
     return r;
 }
 
-template <int NT, bool Q8, int KS>
-__device__ __forceinline__ void gemv_rows(const ProjArgs &p, int r0, int ks, int lane, float (*red)[NT][OMH_WAVE],
-                                          int rg, bool store) {
+// kGemvRows int8 rows r0.. over k-slice ks of KS, NT tokens; the k-slices
+// meet in LDS (red) and the first slice's wave stores (unless !store).
+template <int NT, int KS>
+__device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, int lane,
+                                             float (*red)[NT][OMH_WAVE], int rg, bool store) {
     float acc[kGemvRows][NT];
 #pragma unroll
     for (int i = 0; i < kGemvRows; i++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[i][t] = 0.f;
-    const int nrow = min(kGemvRows, p.O - r0);
-    const int klen = p.I / KS;
-    for (int kc = ks * klen; kc < (ks + 1) * klen; kc += 16 * OMH_WAVE) {
-        const int k = kc + 16 * lane;
-        if (k < (ks + 1) * klen) {
-            WFrag<Q8> wf[kGemvRows];                 // every row's weights in flight together
+    const int nrow = min(kGemvRows, p.n_q - r0);
+    const int klen = p.I / KS, kbeg = ks * klen, kend = kbeg + klen;
+    for (int kc = kbeg; kc < kend; kc += kGemvCB * 16 * OMH_WAVE) {
+        int kk[kGemvCB];
+        bool live[kGemvCB];
 #pragma unroll
-            for (int i = 0; i < kGemvRows; i++) wf[i].load(p, r0 + min(i, nrow - 1), k);
-            float x[NT][16];
+        for (int c = 0; c < kGemvCB; c++) {
+            const int k = kc + c * 16 * OMH_WAVE + 16 * lane;
+            live[c] = k < kend;
+            kk[c] = live[c] ? k : kend - 16;          // (in range; its products are skipped)
+        }
+        float x[kGemvCB][NT][16];
 #pragma unroll
-            for (int t = 0; t < NT; t++) load_x16(p.x + (size_t)t * p.ldx + k, x[t]);
+        for (int c = 0; c < kGemvCB; c++)
 #pragma unroll
-            for (int i = 0; i < kGemvRows; i++) {
+            for (int t = 0; t < NT; t++) load_x16(p.x + (size_t)t * p.ldx + kk[c], x[c][t]);
+        __builtin_amdgcn_sched_barrier(0);            // x first, then the weights
+        WFrag<true> wf[kGemvRows][kGemvCB];
+#pragma unroll
+        for (int i = 0; i < kGemvRows; i++)
+#pragma unroll
+            for (int c = 0; c < kGemvCB; c++) wf[i][c].load(p, r0 + min(i, nrow - 1), kk[c]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < kGemvRows; i++)
+#pragma unroll
+            for (int c = 0; c < kGemvCB; c++) {
+                if (!live[c]) continue;
                 float w[16];
-                wf[i].unpack(w);
+                wf[i][c].unpack(w);
 #pragma unroll
                 for (int t = 0; t < NT; t++)
 #pragma unroll
-                    for (int e = 0; e < 16; e++) acc[i][t] = fmaf(x[t][e], w[e], acc[i][t]);
+                    for (int e = 0; e < 16; e++) acc[i][t] = fmaf(x[c][t][e], w[e], acc[i][t]);
             }
-        }
     }
     // lane L holds row 4*bit5(L) + 2*bit4(L) + bit3(L) after the reduction
     const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
@@ -188,26 +217,79 @@ __device__ __forceinline__ void gemv_rows(const ProjArgs &p, int r0, int ks, int
     }
     if (store && (lane & 7) == 0 && myrow < nrow) {
         const int o = r0 + myrow;
-        const float sc = Q8 ? p.scale[o] : 1.f;
+        const float sc = p.scale[o];
 #pragma unroll
         for (int t = 0; t < NT; t++) p.y[(size_t)t * p.ldy + o] = tot[t] * sc;
     }
 }
 
+// One fp32 row over the full k, one wave, NT tokens: chunks of 256 (4 per
+// lane), eight per request group, x first.
+template <int NT>
+__device__ __forceinline__ void gemv_f32_row(const ProjArgs &p, int row, int lane) {
+    const float *W = p.W + (size_t)(row - p.n_q) * p.I;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = 0.f;
+    for (int kc = 0; kc < p.I; kc += 8 * 4 * OMH_WAVE) {
+        int kk[8];
+        bool live[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int k = kc + c * 4 * OMH_WAVE + 4 * lane;
+            live[c] = k < p.I;
+            kk[c] = live[c] ? k : p.I - 4;
+        }
+        float4 xv[NT][8], wv[8];
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) xv[t][c] = *reinterpret_cast<const float4 *>(p.x + (size_t)t * p.ldx + kk[c]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 8; c++) wv[c] = *reinterpret_cast<const float4 *>(W + kk[c]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            if (!live[c]) continue;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                acc[t] = fmaf(xv[t][c].x, wv[c].x, acc[t]);
+                acc[t] = fmaf(xv[t][c].y, wv[c].y, acc[t]);
+                acc[t] = fmaf(xv[t][c].z, wv[c].z, acc[t]);
+                acc[t] = fmaf(xv[t][c].w, wv[c].w, acc[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        float a = acc[t];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, OMH_WAVE);
+        if (lane == 0) p.y[(size_t)t * p.ldy + row] = a;
+    }
+}
+
+// Workgroups 0 .. nwg8-1: the int8 rows; the rest: the fp32 rows, four per
+// workgroup (one per wave).
 template <int NT, int KS>
 __global__ __launch_bounds__(4 * OMH_WAVE)
-void proj_gemv_kernel(const ProjArgs p) {
+void proj_gemv_kernel(const ProjArgs p, int nwg8) {
     constexpr int RG = 4 / KS;
     __shared__ float red[KS > 1 ? (KS - 1) * 4 : 1][NT][OMH_WAVE];
     const int lane = threadIdx.x % OMH_WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / OMH_WAVE);
+    if ((int)blockIdx.x >= nwg8) {
+        const int row = p.n_q + ((int)blockIdx.x - nwg8) * 4 + wv;
+        if (row < p.O) gemv_f32_row<NT>(p, row, lane);
+        return;
+    }
     const int rg = wv % RG, ks = wv / RG;
-    // a row group past the end works on the last group instead (the
+    // a row group past the int8 rows works on the last group instead (the
     // workgroup stays together for the k-slice reduction) and stores nothing
     const int rs = (blockIdx.x * RG + rg) * kGemvRows;
-    const int r0 = min(rs, ((p.O - 1) / kGemvRows) * kGemvRows);
-    if (r0 < p.n_q) gemv_rows<NT, true, KS>(p, r0, ks, lane, red, rg, rs < p.O);
-    else gemv_rows<NT, false, KS>(p, r0, ks, lane, red, rg, rs < p.O);
+    const int r0 = min(rs, ((p.n_q - 1) / kGemvRows) * kGemvRows);
+    gemv_q8_rows<NT, KS>(p, r0, ks, lane, red, rg, rs < p.n_q);
 }
 
 // ---------------------------------------------------------------- MFMA
@@ -2122,11 +2204,12 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         // k-slices: as many 1024-wide chunks as there are, up to 4 per row group
         const int ks = p.I >= 4096 ? 4 : (p.I >= 2048 ? 2 : 1);
         const int rows_per_wg = (4 / ks) * kGemvRows;
-        const dim3 grid((p.O + rows_per_wg - 1) / rows_per_wg), blk(4 * OMH_WAVE);
-#define OMH_GEMV(NT)                                                                        \
-    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4>), grid, blk, 0, st, p);       \
-    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2>), grid, blk, 0, st, p);  \
-    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1>), grid, blk, 0, st, p);
+        const int nwg8 = (p.n_q + rows_per_wg - 1) / rows_per_wg, nf = (p.O - p.n_q + 3) / 4;
+        const dim3 grid(nwg8 + nf), blk(4 * OMH_WAVE);
+#define OMH_GEMV(NT)                                                                              \
+    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4>), grid, blk, 0, st, p, nwg8);       \
+    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2>), grid, blk, 0, st, p, nwg8);  \
+    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1>), grid, blk, 0, st, p, nwg8);
         switch (p.T) {
         case 1: OMH_GEMV(1) break;
         case 2: OMH_GEMV(2) break;
