@@ -75,6 +75,8 @@ struct Scratch {
     size_t n = 0;
 };
 Scratch g_x, g_out, g_in, g_core, g_qkv, g_z, g_a, g_b, g_pre, g_xb, g_dec;
+
+
 // k-split arrival counters of the projections: zeroed once at init and
 // zero between launches (each tile's last arriver resets its own), shared
 // by every call (calls that may overlap must come from one stream)
@@ -89,6 +91,49 @@ int ensure(Scratch &s, size_t bytes) {
     size_t want = bytes < 4096 ? 4096 : bytes;
     if (hipMalloc(&s.p, want) != hipSuccess) return fail(OMH_ERR_ALLOC, "scratch alloc of %zu bytes failed", want);
     s.n = want;
+    return OMH_OK;
+}
+
+// Pinned, device-mapped host staging for the synchronous small calls (one
+// decode token, a short attention step): x is copied into it on the CPU and
+// sent with one asynchronous copy; the last projection writes its output
+// straight into the mapped output buffer, so no device-to-host copy is
+// queued.  One call of the 35B GDN layer at one token: 31.5 us against
+// 47 us with pageable copies both ways (MI355X).  Grow-only.
+struct Pinned {
+    float *h = nullptr;         // host address
+    float *d = nullptr;         // the device's address of the same memory
+    size_t n = 0;               // bytes
+};
+Pinned g_hx, g_hout;
+constexpr size_t kPinnedMaxBytes = size_t(1) << 20;   // calls above this use pageable copies
+
+int ensure_pinned(Pinned &b, size_t bytes) {
+    if (bytes <= b.n) return OMH_OK;
+    if (b.h) (void)hipHostFree(b.h);
+    b = Pinned{};
+    void *h = nullptr, *d = nullptr;
+    if (hipHostMalloc(&h, bytes, hipHostMallocMapped) != hipSuccess) return fail(OMH_ERR_ALLOC, "pinned staging of %zu bytes failed", bytes);
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+        (void)hipHostFree(h);
+        return fail(OMH_ERR_ALLOC, "pinned staging: no device address");
+    }
+    b.h = static_cast<float *>(h);
+    b.d = static_cast<float *>(d);
+    b.n = bytes;
+    return OMH_OK;
+}
+
+// Stage n floats of x for the device (pinned copy, then one async copy into
+// g_x) and make sure the mapped output buffer holds n_out floats.  Small
+// calls only (kPinnedMaxBytes), whose last projection is the register GEMV
+// (up to 4 tokens): it writes each output once, 16 rows per store wave.
+int stage_small(const float *x, size_t n, size_t n_out) {
+    if (int rc = ensure_pinned(g_hx, n * 4)) return rc;
+    if (int rc = ensure_pinned(g_hout, n_out * 4)) return rc;
+    if (int rc = ensure(g_x, n * 4)) return rc;
+    memcpy(g_hx.h, x, n * 4);
+    HIP_OK(hipMemcpyAsync(g_x.p, g_hx.h, n * 4, hipMemcpyHostToDevice, g_stream));
     return OMH_OK;
 }
 
@@ -749,6 +794,13 @@ int omh_gdn_decode(int li, int B, const float *x, float *out) {
     if (B < 1 || B > L.max_seqs) return fail(OMH_ERR_ARG, "decode: B=%d outside [1, %d]", B, L.max_seqs);
     if (!x || !out) return fail(OMH_ERR_ARG, "decode: null pointer");
     const size_t n = (size_t)B * L.d.hidden;
+    if (B <= 4 && n * 4 <= kPinnedMaxBytes) {
+        if (int rc = stage_small(x, n, n)) return rc;
+        if (int rc = decode_full(li, B, (const float *)g_x.p, g_hout.d, g_stream)) return rc;
+        HIP_OK(hipStreamSynchronize(g_stream));
+        memcpy(out, g_hout.h, n * 4);
+        return OMH_OK;
+    }
     if (int rc = ensure(g_x, n * 4)) return rc;
     if (int rc = ensure(g_out, n * 4)) return rc;
     HIP_OK(hipMemcpyAsync(g_x.p, x, n * 4, hipMemcpyHostToDevice, g_stream));
@@ -957,6 +1009,13 @@ int omh_attn_forward(int li, int seq, int pos, int T, const float *x, float *out
     if (T < 0 || (T > 0 && (!x || !out))) return fail(OMH_ERR_ARG, "attn: bad arguments");
     if (T == 0) return OMH_OK;
     const size_t n = (size_t)T * g_A[li].d.hidden;
+    if (T <= 4 && n * 4 <= kPinnedMaxBytes) {      // the engine's decode step (o_proj on the GEMV)
+        if (int rc = stage_small(x, n, n)) return rc;
+        if (int rc = attn_forward(li, seq, pos, T, (const float *)g_x.p, g_hout.d, g_stream)) return rc;
+        HIP_OK(hipStreamSynchronize(g_stream));
+        memcpy(out, g_hout.h, n * 4);
+        return OMH_OK;
+    }
     if (int rc = ensure(g_x, n * 4)) return rc;
     if (int rc = ensure(g_out, n * 4)) return rc;
     HIP_OK(hipMemcpyAsync(g_x.p, x, n * 4, hipMemcpyHostToDevice, g_stream));
