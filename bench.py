@@ -97,27 +97,31 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
     d = Q35B
     per_layer = d.state_bytes + 4 * d.conv_dim * (d.K - 1)
     R = math.ceil(ROTATE_BYTES / (N_LAYERS * per_layer))
-    log(f"decode: {R} x {N_LAYERS} layers, {R * N_LAYERS * per_layer / 2**30:.2f} GiB of state")
+    log(f"decode: {N_LAYERS} layers x {R} sequence slots, {R * N_LAYERS * per_layer / 2**30:.2f} GiB of state")
     w = synth.layer_weights(d, 0, projections=False)
     conv0, S0 = synth.states(d, 0)
-    lays = make_layers(gdn, d, 0, R * N_LAYERS, 1, w, conv0, S0)
+    # one model of 30 GDN layers (one set of weights per layer), R sequence
+    # slots per layer; step k decodes slot k % R in every layer, so a slot's
+    # state comes back every R steps, after more than 1 GiB of other states
+    # has streamed through: the state reads and writes go to HBM
+    lays = make_layers(gdn, d, 0, N_LAYERS, R, w, conv0, S0)
     inp = synth.core_inputs(d, N_LAYERS, 1)                # [30][...] = [nl][B=1][...]
     dev = {k: hip.Buffer.from_numpy(v) for k, v in inp.items()}
     row = {k: v.shape[1] * 4 for k, v in inp.items()}
     core = hip.Buffer(N_LAYERS * d.val_dim * 4)
     st = hip.Stream()
-    groups = [[lays[r * N_LAYERS + l].li for l in range(N_LAYERS)] for r in range(R)]
+    lis = [L.li for L in lays]
 
-    # the entry point bound once, its layer-id arrays and pointers built up
+    # the entry point bound once, its layer-id array and pointers built up
     # front, so the host issues a launch in a few microseconds and the
     # back-to-back launches keep the GPU busy
     import ctypes as C
-    fn = gdn.lib().omh_gdn_decode_core_dev
-    arrs = [(C.c_int * N_LAYERS)(*g) for g in groups]
+    fn = gdn.lib().omh_gdn_decode_core_seq_dev
+    arr = (C.c_int * N_LAYERS)(*lis)
     args = [gdn._ptr(dev[k]) for k in ("qkv", "z", "a", "b")] + [gdn._ptr(core), gdn._stream(st)]
 
     def step_fused(k):
-        gdn.check(fn(N_LAYERS, arrs[k % R], 1, *args))
+        gdn.check(fn(N_LAYERS, arr, k % R, 1, *args))
 
     el, durs, wall = time_launches(hip, st, step_fused, steps, warmup)
     # host time to issue one launch (no synchronisation inside the loop)
@@ -136,6 +140,8 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
     log(f"decode fused 30-layer launch: {fused['tok_s']:.0f} tok/s, kernel {fused['kernel_us']:.1f} us, "
         f"{fused['achieved_GBs']:.0f} GB/s, host issue {issue_us:.1f} us per launch")
 
+    fused["weights_rotated"] = bench_decode_weights_rotated(hip, gdn, synth, d, w, conv0, S0, inp, core, st,
+                                                            steps, warmup)
     if not full:
         for L in lays:
             L.free()
@@ -144,10 +150,9 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
 
     # engine order: one launch per layer (the order an engine issues them)
     def step_layers(k):
-        g = groups[k % R]
         for l in range(N_LAYERS):
-            gdn.decode_core_dev([g[l]], 1, *(dev[nm].at(l * row[nm]) for nm in ("qkv", "z", "a", "b")),
-                                core.at(l * d.val_dim * 4), stream=st)
+            gdn.decode_core_seq_dev([lis[l]], k % R, 1, *(dev[nm].at(l * row[nm]) for nm in ("qkv", "z", "a", "b")),
+                                    core.at(l * d.val_dim * 4), stream=st)
 
     n2 = max(steps // 2, 5)
     el2, durs2, _ = time_launches(hip, st, step_layers, n2, warmup)
@@ -198,6 +203,30 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
             L.free()
         hip.device_synchronize()
     return fused, {"ctypes": engine, "graph": engine_graph}, sweep, alg_bytes, R
+
+
+def bench_decode_weights_rotated(hip, gdn, synth, d, w, conv0, S0, inp, core, st, steps, warmup):
+    """The headline launch with every rotation group a separate set of 30
+    layers, each with its own copy of the conv weights as well as its own
+    state (one slot each): the form earlier measurements of this build used.
+    Every launch then also reads 30 x 128 KiB of conv weights from HBM."""
+    import ctypes as C
+    per_layer = d.state_bytes + 4 * d.conv_dim * (d.K - 1)
+    R = math.ceil(ROTATE_BYTES / (N_LAYERS * per_layer))
+    lays = make_layers(gdn, d, 3000, R * N_LAYERS, 1, w, conv0, S0)
+    dev = {k: hip.Buffer.from_numpy(v) for k, v in inp.items()}
+    fn = gdn.lib().omh_gdn_decode_core_dev
+    arrs = [(C.c_int * N_LAYERS)(*[lays[r * N_LAYERS + l].li for l in range(N_LAYERS)]) for r in range(R)]
+    args = [gdn._ptr(dev[k]) for k in ("qkv", "z", "a", "b")] + [gdn._ptr(core), gdn._stream(st)]
+    el, _, _ = time_launches(hip, st, lambda k: gdn.check(fn(N_LAYERS, arrs[k % R], 1, *args)), steps, warmup)
+    kern = el / steps
+    gbs = N_LAYERS * 2 * d.state_bytes / kern / 1e9
+    log(f"decode fused 30-layer launch, weights rotated with the states ({R} x 30 layers): kernel "
+        f"{1e6 * kern:.1f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}%)")
+    for L in lays:
+        L.free()
+    hip.device_synchronize()
+    return {"kernel_us": 1e6 * kern, "achieved_GBs": gbs, "frac_hbm": gbs / HBM_PEAK_GBS, "rotation_groups": R}
 
 
 def quantized(w):
@@ -817,7 +846,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (splitmix64/Box-Muller, seeded); random-init GDN weights of the 35B GDN shape",
-        "config": {"workload": "GDN core decode, 1 token x 30 layers (one launch), B=1, "
+        "config": {"workload": "GDN core decode, 1 token x 30 layers (one launch), B=1 (one of R sequence slots "
+                               "per step, rotating), "
                                "kh=16 vh=32 kd=vd=128, fp32 state, pre-projected inputs",
                    "layers": N_LAYERS, "batch": 1,
                    "state_rotation_GiB": round(R * N_LAYERS * 2.19e6 / 2**30, 2)},
@@ -843,6 +873,7 @@ def main():
         "attn_prefill_T4096": attnp,
         "gdn_state_snapshot_30layers": snap,
         "decode_engine_order": engine,
+        "decode_weights_rotated": fused.get("weights_rotated"),
         "engine_block_B1": eng,
         "prefill_block_int8_T4096": preb,
         "decode_batch_sweep": sweep,

@@ -144,6 +144,12 @@ int omh_gdn_prefill_core(int li, int seq, int T, const float *qkv, const float *
  * here (pre-projected inputs), so one launch serves them all. */
 int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
                             const float *a, const float *b, float *core, void *stream);
+/* The same for sequences seq0 .. seq0+B-1 of every listed layer (a server
+ * stepping some of its sequence slots); inputs and core are [nl][B][...]
+ * as above.  omh_gdn_decode_core_dev is seq0 = 0.  No counterpart in the
+ * reference, which runs one sequence (engines/qwen.c:566-607). */
+int omh_gdn_decode_core_seq_dev(int nl, const int *lis, int seq0, int B, const float *qkv, const float *z,
+                                const float *a, const float *b, float *core, void *stream);
 int omh_gdn_prefill_core_dev(int li, int seq, int T, const float *qkv, const float *z,
                              const float *a, const float *b, float *core, void *stream);
 int omh_gdn_decode_dev(int li, int B, const float *x, float *out, void *stream);

@@ -734,14 +734,19 @@ int omh_gdn_state_copy(int nl, const int *lis, int src_seq, int dst_seq) {
     return OMH_OK;
 }
 
-int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
-                            const float *a, const float *b, float *core, void *stream) {
+int omh_gdn_decode_core_seq_dev(int nl, const int *lis, int seq0, int B, const float *qkv, const float *z,
+                                const float *a, const float *b, float *core, void *stream) {
     if (!omh_init()) return OMH_ERR_DEVICE;
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core_dev: nl=%d", nl);
     if (int rc = check_layer(lis[0])) return rc;
     const DevLayer &L = g_L[lis[0]];
     return decode_core(nl, lis, B, qkv, L.conv_dim, z, L.vdim, a, b, L.d.vh, core,
-                       static_cast<hipStream_t>(stream));
+                       static_cast<hipStream_t>(stream), nullptr, seq0);
+}
+
+int omh_gdn_decode_core_dev(int nl, const int *lis, int B, const float *qkv, const float *z,
+                            const float *a, const float *b, float *core, void *stream) {
+    return omh_gdn_decode_core_seq_dev(nl, lis, 0, B, qkv, z, a, b, core, stream);
 }
 
 int omh_gdn_decode_core(int li, int B, const float *qkv, const float *z, const float *a,

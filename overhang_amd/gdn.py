@@ -29,7 +29,7 @@ EXPORTS = (
     "omh_gdn_prefill_dev", "omh_sync",
     "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
     "omh_gdn_state_copy", "omh_gdn_state_copy_dev", "omh_attn_cache_get", "omh_attn_cache_set",
-    "omh_gdn_decode_noalloc_dev", "omh_gdn_set_prefill_math",
+    "omh_gdn_decode_noalloc_dev", "omh_gdn_set_prefill_math", "omh_gdn_decode_core_seq_dev",
 )
 OMH_PREFILL_FP32, OMH_PREFILL_BF16 = 0, 1
 
@@ -89,6 +89,7 @@ def lib() -> C.CDLL:
         L.omh_gdn_decode_core.argtypes = [i, i, vp, vp, vp, vp, vp]
         L.omh_gdn_prefill_core.argtypes = [i, i, i, vp, vp, vp, vp, vp]
         L.omh_gdn_decode_core_dev.argtypes = [i, C.POINTER(C.c_int), i, vp, vp, vp, vp, vp, vp]
+        L.omh_gdn_decode_core_seq_dev.argtypes = [i, C.POINTER(C.c_int), i, i, vp, vp, vp, vp, vp, vp]
         L.omh_gdn_prefill_core_dev.argtypes = [i, i, i, vp, vp, vp, vp, vp, vp]
         L.omh_gdn_decode_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_gdn_prefill_dev.argtypes = [i, i, i, vp, vp, vp]
@@ -243,6 +244,13 @@ def decode_core_dev(lis, B: int, qkv, z, a, b, core, stream=None) -> None:
     arr = (C.c_int * len(lis))(*lis)
     check(lib().omh_gdn_decode_core_dev(len(lis), arr, B, _ptr(qkv), _ptr(z), _ptr(a), _ptr(b),
                                         _ptr(core), _stream(stream)))
+
+
+def decode_core_seq_dev(lis, seq0: int, B: int, qkv, z, a, b, core, stream=None) -> None:
+    """decode_core_dev for sequences seq0 .. seq0+B-1 of every listed layer."""
+    arr = (C.c_int * len(lis))(*lis)
+    check(lib().omh_gdn_decode_core_seq_dev(len(lis), arr, seq0, B, _ptr(qkv), _ptr(z), _ptr(a), _ptr(b),
+                                            _ptr(core), _stream(stream)))
 
 
 def prefill_core_dev(li: int, seq: int, T: int, qkv, z, a, b, core, stream=None) -> None:

@@ -352,3 +352,51 @@ def test_decode_core_dev_30_layers_35b_vs_oracle(B):
             assert np.array_equal(conv, cref), f"layer {l} seq {s} conv history"
     for L in lays:
         L.free()
+
+
+def test_decode_core_seq_dev_30_layers_rotating_slots():
+    """The headline's launch: the cores of 30 GDN layers of the 35B-A3B shape
+    stepping one sequence slot per call (omh_gdn_decode_core_seq_dev, B = 1,
+    seq0 in a rotating order), so each call touches one slot's state in
+    every layer and leaves the other slots (and their ring phases) alone.
+    Every (layer, slot) output, final state and conv history against the
+    oracle run over that slot's own tokens in order."""
+    from overhang_amd import hip
+    d = Q35B
+    nl, S = 30, 4
+    order = [0, 2, 1, 2, 3, 0, 2]
+    lays, ws, st0 = [], [], []
+    for l in range(nl):
+        w = synth.layer_weights(d, 700 + l, gnorm_std=0.1, projections=False)
+        conv0, S0 = synth.states(d, 700 + l, B=S)
+        L = gdn.GdnLayer(new_li(), d, w, max_seqs=S)
+        for s in range(S):
+            L.set_state(s, conv0[s], S0[s])
+        lays.append(L)
+        ws.append(w)
+        st0.append((conv0, S0))
+    T = len(order)
+    inp = [synth.core_inputs(d, T, 800 + l, B=1) for l in range(nl)]      # per layer [1][T][...]
+    core = hip.Buffer(nl * d.val_dim * 4)
+    st = hip.Stream()
+    got = {}
+    for t, s in enumerate(order):
+        dev = {k: hip.Buffer.from_numpy(np.ascontiguousarray(np.stack([inp[l][k][0, t] for l in range(nl)])))
+               for k in ("qkv", "z", "a", "b")}
+        gdn.decode_core_seq_dev([L.li for L in lays], s, 1, dev["qkv"], dev["z"], dev["a"], dev["b"], core, stream=st)
+        st.synchronize()
+        got[t] = core.numpy((nl, d.val_dim))
+    for s in range(S):
+        ts = [t for t, q in enumerate(order) if q == s]
+        for l in (0, 13, 29):
+            conv, Sst = lays[l].get_state(s)
+            if not ts:
+                assert np.array_equal(Sst, st0[l][1][s]) and np.array_equal(conv, st0[l][0][s])
+                continue
+            ref, cref, Sref = oracle.core_seq(d, ws[l], *(inp[l][k][0, ts] for k in ("qkv", "z", "a", "b")),
+                                              st0[l][0][s], st0[l][1][s])
+            assert_close(np.stack([got[t][l] for t in ts]), ref, what=f"layer {l} slot {s} core")
+            assert_close(Sst, Sref, what=f"layer {l} slot {s} S")
+            assert np.array_equal(conv, cref), f"layer {l} slot {s} conv history"
+    for L in lays:
+        L.free()
