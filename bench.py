@@ -38,7 +38,6 @@ sys.path.insert(0, ROOT)
 METRIC = "GDN tok/s: prefill T=4096 + decode B=1..64; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_TFLOPS = 157.3
-BF16_MFMA_TFLOPS = 2500.0
 INT8_MFMA_TOPS = 5000.0
 N_LAYERS = 30
 ROTATE_BYTES = 1 << 30
@@ -366,13 +365,6 @@ def prefill_flops(d, T, C=64):
     return d.vh * nc * (2 * C * C * (3 * d.kd + 2 * d.vd) + 6 * C * d.kd * d.vd + C ** 3 / 3)
 
 
-def prefill_scan_flops(d, T, C=64):
-    """The part of prefill_flops done by the inter-chunk scan: W S, (Q e^g) S
-    and the state update (6 C kd vd) and Aqk v_new (2 C^2 vd)."""
-    nc = -(-T // C)
-    return d.vh * nc * (6 * C * d.kd * d.vd + 2 * C * C * d.vd)
-
-
 def prefill_bytes(d, T):
     """Compulsory HBM bytes of a core prefill of T tokens: q, k (read as
     mixed_qkv), v, z in; core out; a, b in; the state read and written."""
@@ -380,13 +372,11 @@ def prefill_bytes(d, T):
             + 2 * d.state_bytes)
 
 
-def bench_prefill(hip, gdn, synth, T, steps, warmup, math="fp32"):
+def bench_prefill(hip, gdn, synth, T, steps, warmup):
     from overhang_amd.dims import Q35B
     d = Q35B
     w = synth.layer_weights(d, 0, projections=False)
     L = gdn.GdnLayer(2000, d, w, max_seqs=1)
-    if math == "bf16":
-        L.set_prefill_math(gdn.OMH_PREFILL_BF16)
     inp = synth.core_inputs(d, T, 7)
     dev = {k: hip.Buffer.from_numpy(v) for k, v in inp.items()}
     core = hip.Buffer(T * d.val_dim * 4)
@@ -401,27 +391,17 @@ def bench_prefill(hip, gdn, synth, T, steps, warmup, math="fp32"):
     fl = prefill_flops(d, T)
     by = prefill_bytes(d, T)
     tf = fl / t / 1e12
-    if math == "bf16":
-        # the scan's products run at the bf16 peak, the WY kernel's at fp32:
-        # the matrix-core bound is the sum of the two parts' times
-        sc = prefill_scan_flops(d, T)
-        peak = fl / ((fl - sc) / FP32_MFMA_TFLOPS + sc / BF16_MFMA_TFLOPS)
-    else:
-        peak = FP32_MFMA_TFLOPS
+    peak = FP32_MFMA_TFLOPS
     # attainable roofline at this arithmetic intensity
     attain = min(peak, fl / by * HBM_PEAK_GBS / 1e3)
-    out = {"T": T, "chunk": 64, "math": math, "tok_s": T * steps / el, "us_per_call": 1e6 * t,
+    out = {"T": T, "chunk": 64, "math": "fp32", "tok_s": T * steps / el, "us_per_call": 1e6 * t,
            "flops_per_call": fl, "TFLOPs": tf, "peak_TFLOPs": round(peak, 1),
            "frac_fp32_mfma": tf / FP32_MFMA_TFLOPS, "frac_peak": tf / peak, "frac_attainable": tf / attain,
            "hbm_bytes_alg": by, "recurrent_equiv_GFLOP": 7 * d.vh * T * d.kd * d.vd / 1e9,
            "note": "one GDN layer core (4 launches: WY/chunk (conv, norms, gates, triangular solve, "
                    "panels), conv-history commit, scan, gated norm), "
-                   "kh=16 vh=32 kd=vd=128, fp32 I/O, state carried across calls, "
-                   + ("fp32 MFMA" if math == "fp32" else
-                      "scan products on bf16 MFMA (fp32 accumulate, fp32 state), WY kernel fp32; "
-                      "peak_TFLOPs = flops over the fp32-part time at the fp32 peak plus the scan "
-                      "part's at the bf16 peak")}
-    log(f"prefill T={T} ({math}): {1e6 * t:.0f} us/layer, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
+                   "kh=16 vh=32 kd=vd=128, fp32 I/O, state carried across calls, fp32 MFMA"}
+    log(f"prefill T={T}: {1e6 * t:.0f} us/layer, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
         f"({100 * out['frac_peak']:.1f}% of the {peak:.0f} TFLOP/s matrix-core bound)")
     return out
 
@@ -779,9 +759,8 @@ def main():
     log("device: gfx950 ready")
     if a.part == "prefill":
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 3), a.warmup)
-        pre16 = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 3), a.warmup, math="bf16")
         warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 3, 1)
-        print(json.dumps({"prefill": pre, "prefill_T4096_bf16": pre16, "prefill_T32768_warm": warm}), flush=True)
+        print(json.dumps({"prefill": pre, "prefill_T32768_warm": warm}), flush=True)
         return
     if a.part == "attn":
         print(json.dumps({"attn_decode_n32768": bench_attn(hip, gdn, 32768, max(a.steps // 2, 10), a.warmup)}),
@@ -804,7 +783,7 @@ def main():
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
                                                       full=a.part == "all")
-    pre = pre16 = warm = block = attn = attnp = snap = eng = preb = None
+    pre = warm = block = attn = attnp = snap = eng = preb = None
     if a.part == "all":
         eng = bench_engine_block(hip, gdn, synth, a.steps, a.warmup)
         preb = bench_prefill_block(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
@@ -812,7 +791,6 @@ def main():
         attnp = bench_attn_prefill(hip, gdn, 4096, 5, 1)
         snap = bench_snapshot(hip, gdn, synth, max(a.steps // 2, 10), a.warmup)
         pre = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup)
-        pre16 = bench_prefill(hip, gdn, synth, 4096, max(a.steps // 5, 5), a.warmup, math="bf16")
         warm = bench_prefill_warm(hip, gdn, synth, 32768, 8192, 5, 1)
         block = bench_block(hip, gdn, synth, 64, max(a.steps // 2, 10), a.warmup)
     probe = copy_probe(hip, 1 << 29, 20, 3)
@@ -866,7 +844,6 @@ def main():
         "cpu_baseline": cpu,
         "hbm_copy_probe": probe,
         "prefill_T4096": pre,
-        "prefill_T4096_bf16": pre16,
         "prefill_T32768_warm": warm,
         "block_int8_B64": block,
         "attn_decode_n32768": attn,

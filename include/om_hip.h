@@ -78,21 +78,6 @@ typedef struct {
 int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, int max_seqs);
 int omh_gdn_layer_free(int li);
 
-/* Arithmetic of this layer's chunked prefill (omh_gdn_prefill*).
- * OMH_PREFILL_FP32 (the default): every product on fp32 MFMA; matches the
- *   reference recurrence (engines/qwen.c:339-352) within max-abs 2e-3 /
- *   rel 1e-3 on outputs and state.
- * OMH_PREFILL_BF16: the inter-chunk scan's products (W S, Q S, Aqk v_new and
- *   the state update, most of the prefill's matrix work) take bf16 operands
- *   with fp32 accumulation; the state stays fp32 and the intra-chunk solve
- *   stays fp32.  Tolerance against the reference recurrence: see the
- *   measured bound in the tests (looser than the fp32 contract).
- * No counterpart in the reference, which prefills token by token
- * (qwen.c:588, 637). */
-#define OMH_PREFILL_FP32 0
-#define OMH_PREFILL_BF16 1
-int omh_gdn_set_prefill_math(int li, int math);
-
 /* Zero one sequence's conv and recurrent state (seq < 0: every sequence):
  * the reset branch of serve() (engines/qwen.c:576-582). */
 int omh_gdn_state_reset(int li, int seq);

@@ -44,21 +44,6 @@ __device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
 }
 __device__ __forceinline__ v4f v4zero() { v4f z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
-// bf16 operands (round to nearest even) of v_mfma_f32_16x16x16_bf16: its
-// lane group g holds k = 4g .. 4g+3, the k order of four consecutive fp32
-// k-steps s = 0..3 above (lane group g, register s), so one bf16 product
-// replaces the four fp32 ones with the same operand registers, packed.
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ v4s bf4(float a, float b, float c, float d) {
-    const v4bf r = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
-    return __builtin_bit_cast(v4s, r);
-}
-__device__ __forceinline__ v4s bf4(v4f x) { return bf4(x[0], x[1], x[2], x[3]); }
-__device__ __forceinline__ v4f mfma16(v4s a, v4s b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
 // Scan work split for head dim D: eight waves per workgroup, which owns a
 // D x 16 column slice of S; wave w < NST = D/16 holds row tile w (16 kd
 // rows) in registers.  Per chunk, waves 0-3 form v_new of token tile w
@@ -766,63 +751,54 @@ struct ScanIn {
     }
 };
 
-// LDS of one scan workgroup (as bf16 operands in the bf16 variant: each is
-// only ever read as the B operand of a product)
-template <int D, bool BF>
+// LDS of one scan workgroup (each tile is only ever read as the B operand
+// of a product)
+template <int D>
 struct ScanLds {
-    using T = std::conditional_t<BF, v4s, v4f>;
-    T S[ScanShape<D>::NST][OMH_WAVE];        // S row tiles at the start of the chunk
-    T V[4][OMH_WAVE];                        // v_new token tiles
-    T Vs[4][OMH_WAVE];                       // the same rows scaled by e^{gl-gc}
-    __device__ __forceinline__ static T put(v4f x) {
-        if constexpr (BF) return bf4(x);
-        else return x;
-    }
+    v4f S[ScanShape<D>::NST][OMH_WAVE];      // S row tiles at the start of the chunk
+    v4f V[4][OMH_WAVE];                      // v_new token tiles
+    v4f Vs[4][OMH_WAVE];                     // the same rows scaled by e^{gl-gc}
+    __device__ __forceinline__ static v4f put(v4f x) { return x; }
 };
 
 // c + (16 x 16 A fragment held as four k-step values a[0..3]) x (B tile of
-// one k-step group): four fp32 products, or one bf16 product
-template <bool BF, typename TB>
-__device__ __forceinline__ v4f mm4(const float *a, const TB &b, v4f c) {
-    if constexpr (BF) {
-        return mfma16(bf4(a[0], a[1], a[2], a[3]), b, c);
-    } else {
+// one k-step group): four fp32 products
+__device__ __forceinline__ v4f mm4(const float *a, const v4f &b, v4f c) {
 #pragma unroll
-        for (int s = 0; s < 4; s++) c = mfma4(a[s], b[s], c);
-        return c;
-    }
+    for (int s = 0; s < 4; s++) c = mfma4(a[s], b[s], c);
+    return c;
 }
 
 // S <- e^{gl} S + (K e^{gl-gc})^T v_new for the wave's row tile (two chains)
-template <int D, bool V, bool BF, typename TB>
-__device__ __forceinline__ void scan_update_s(const ScanIn<D, V> &f, const TB (&VN)[4], v4f &S) {
+template <int D, bool V>
+__device__ __forceinline__ void scan_update_s(const ScanIn<D, V> &f, const v4f (&VN)[4], v4f &S) {
     v4f S2 = v4zero();
     S *= f.eg;
 #pragma unroll
     for (int tt = 0; tt < 4; tt += 2) {
-        S = mm4<BF>(f.Kf + tt * 4, VN[tt], S);
-        S2 = mm4<BF>(f.Kf + (tt + 1) * 4, VN[tt + 1], S2);
+        S = mm4(f.Kf + tt * 4, VN[tt], S);
+        S2 = mm4(f.Kf + (tt + 1) * 4, VN[tt + 1], S2);
     }
     S += S2;
 }
 
 // (token tile) x S over all of kd: the B operand of k-step (kt, s) is
 // register s of S row tile kt (D layout), read from LDS; two chains
-template <int D, bool V, bool BF, typename TB>
-__device__ __forceinline__ void scan_times_s(const ScanIn<D, V> &f, const TB (&Ss)[ScanShape<D>::NST][OMH_WAVE], int lane,
+template <int D, bool V>
+__device__ __forceinline__ void scan_times_s(const ScanIn<D, V> &f, const v4f (&Ss)[ScanShape<D>::NST][OMH_WAVE], int lane,
                                              v4f &P0, v4f &P1) {
 #pragma unroll
     for (int kt = 0; kt < ScanShape<D>::NST; kt++) {
-        const TB sf = Ss[kt][lane];
-        if (kt & 1) P1 = mm4<BF>(f.Mf + kt * 4, sf, P1);
-        else P0 = mm4<BF>(f.Mf + kt * 4, sf, P0);
+        const v4f sf = Ss[kt][lane];
+        if (kt & 1) P1 = mm4(f.Mf + kt * 4, sf, P1);
+        else P0 = mm4(f.Mf + kt * 4, sf, P0);
     }
 }
 
 // Instruction order for a product over NST row tiles read from LDS, with NL
 // of the next chunk's loads spread over its MFMAs (the L1 return path then
 // works while the matrix cores do, instead of every wave queueing its loads
-// at once).  MPK: MFMAs per row tile (4 fp32, 1 bf16).
+// at once).  MPK: MFMAs per row tile.
 template <int NST, int NL, int MPK = 4>
 __device__ __forceinline__ void scan_interleave_s() {
     constexpr int PER = (NL + NST - 1) / NST;
@@ -861,7 +837,7 @@ __device__ __forceinline__ void scan_interleave_r() {
 // The two roles run separate loops with the same barriers; each loads the
 // operands of the chunk after next into a third register set (two chunks of
 // lead time for HBM latency), spread over its own products.
-template <int D, bool BF>
+template <int D>
 __global__ __launch_bounds__((ScanShape<D>::NWV * OMH_WAVE), 1)
 void prefill_scan_kernel(const PrefillArgs a) {
     constexpr int NST = ScanShape<D>::NST;
@@ -894,9 +870,8 @@ void prefill_scan_kernel(const PrefillArgs a) {
     const __amdgpu_buffer_rsrc_t grs =
         __builtin_amdgcn_make_buffer_rsrc(a.glast, 0, (int)((size_t)vh * nc * sizeof(float)), 0x00020000);
 
-    using Lds = ScanLds<D, BF>;
-    using TB = typename Lds::T;
-    constexpr int MPK = BF ? 1 : 4;                      // MFMAs per 16x16x16 step
+    using Lds = ScanLds<D>;
+    constexpr int MPK = 4;                               // MFMAs per 16x16x16 step
     __shared__ Lds sm;
 
     // S rows 16w + 4g + r, column 16cb + l%16
@@ -916,7 +891,7 @@ void prefill_scan_kernel(const PrefillArgs a) {
             omh_lds_barrier();                   // B1: S tiles of chunk c
             fn.load_m(a, hc0 + cn, hq0 + cn, w, lane);
             v4f P0 = v4zero(), P1 = v4zero();
-            scan_times_s<D, true, BF>(f, sm.S, lane, P0, P1);
+            scan_times_s<D, true>(f, sm.S, lane, P0, P1);
             scan_interleave_s<NST, NST, MPK>();
             v4f vn, vs;
 #pragma unroll
@@ -930,10 +905,10 @@ void prefill_scan_kernel(const PrefillArgs a) {
             fn.load_x(a, hc0 + cn, cb, w, lane);
             fn.load_k(a, grs, hc0 + cn, hq0 + cn, w, lane);
             if (owns) {
-                TB VN[4];
+                v4f VN[4];
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) VN[tt] = sm.Vs[tt][lane];
-                scan_update_s<D, true, BF>(f, VN, S);
+                scan_update_s<D, true>(f, VN, S);
                 scan_interleave_r<4 * MPK, 7>();
                 sm.S[w][lane] = Lds::put(S);
             }
@@ -971,7 +946,7 @@ void prefill_scan_kernel(const PrefillArgs a) {
             fn.load_m(a, hc0 + cn, hq0 + cn, w, lane);
             fn.load_x(a, hc0 + cn, cb, w, lane);
             v4f O0 = v4zero(), O1 = v4zero();
-            scan_times_s<D, false, BF>(f, sm.S, lane, O0, O1);
+            scan_times_s<D, false>(f, sm.S, lane, O0, O1);
             scan_interleave_s<NST, NST + 5, MPK>();
 #pragma unroll
             for (int r = 0; r < 4; r++) O0[r] = (O0[r] + O1[r]) * f.sc[r];
@@ -979,19 +954,19 @@ void prefill_scan_kernel(const PrefillArgs a) {
             omh_lds_barrier();                   // B2: v_new of chunk c
             fn.load_k(a, grs, hc0 + cn, hq0 + cn, w, lane);
             if (owns) {
-                TB VS[4];
+                v4f VS[4];
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) VS[tt] = sm.Vs[tt][lane];
-                scan_update_s<D, false, BF>(f, VS, S);
+                scan_update_s<D, false>(f, VS, S);
                 sm.S[w][lane] = Lds::put(S);
             }
-            TB VN[4];
+            v4f VN[4];
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) VN[tt] = sm.V[tt][lane];
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) {
-                if (kt & 1) O1 = mm4<BF>(f.Xf + kt * 4, VN[kt], O1);
-                else O0 = mm4<BF>(f.Xf + kt * 4, VN[kt], O0);
+                if (kt & 1) O1 = mm4(f.Xf + kt * 4, VN[kt], O1);
+                else O0 = mm4(f.Xf + kt * 4, VN[kt], O0);
             }
             scan_interleave_r<8 * MPK, 5>();
             o = O0 + O1;
@@ -1042,8 +1017,7 @@ hipError_t launch_prefill_d(const PrefillArgs &a, hipStream_t st) {
     if (a.K == 4) hipLaunchKernelGGL((prefill_wy_kernel<D, 4>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     else if (a.K == 3) hipLaunchKernelGGL((prefill_wy_kernel<D, 3>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
     else hipLaunchKernelGGL((prefill_wy_kernel<D, 2>), dim3(grid), dim3(WyShape<D>::NT), WyShape<D>::LDS, st, a);
-    if (a.bf16) hipLaunchKernelGGL((prefill_scan_kernel<D, true>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
-    else hipLaunchKernelGGL((prefill_scan_kernel<D, false>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
+    hipLaunchKernelGGL((prefill_scan_kernel<D>), dim3(a.vh * (D / 16)), dim3(ScanShape<D>::NWV * OMH_WAVE), 0, st, a);
     constexpr int RPB = 256 / (D / 4);
     const size_t rows = (size_t)a.T * a.vh;
     const int nnorm = (int)((rows + RPB - 1) / RPB), ncommit = (conv_dim + 255) / 256;

@@ -54,7 +54,6 @@ struct DevLayer {
     float *o_raw = nullptr, *ssq = nullptr;
     int *cnt = nullptr;
     // projections: in_proj rows [qkv | z | b | a]; rows < in_nq are int8
-    bool prefill_bf16 = false;             // omh_gdn_set_prefill_math
     bool has_proj = false;
     int in_rows = 0, in_nq = 0;
     int8_t *Qin = nullptr;
@@ -366,7 +365,6 @@ int prefill_core(int li, int seq, int T, const float *qkv, int64_t ld_qkv, const
     A.L = ptrs(L);
     A.seq = seq; A.T = T; A.nc = (T + kChunk - 1) / kChunk; A.Tp = A.nc * kChunk;
     A.kh = d.kh; A.vh = d.vh; A.K = d.conv_k; A.eps = d.eps;
-    A.bf16 = L.prefill_bf16;
     if (int rc = ensure(g_pre, prefill_scratch_bytes(D, d.kh, d.vh, T))) return rc;
     prefill_bind_scratch(A, D, g_pre.p);
     HIP_OK(launch_prefill_core(A, D, st));
@@ -617,14 +615,6 @@ int omh_gdn_layer_init(int li, const omh_gdn_dims *d, const omh_gdn_weights *w, 
 #undef UP
     L.live = true;
     g_L[li] = L;
-    return OMH_OK;
-}
-
-int omh_gdn_set_prefill_math(int li, int math) {
-    if (!omh_init()) return OMH_ERR_DEVICE;
-    if (int rc = check_layer(li)) return rc;
-    if (math != OMH_PREFILL_FP32 && math != OMH_PREFILL_BF16) return fail(OMH_ERR_ARG, "prefill math %d unknown", math);
-    g_L[li].prefill_bf16 = math == OMH_PREFILL_BF16;
     return OMH_OK;
 }
 

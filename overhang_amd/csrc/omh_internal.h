@@ -168,7 +168,6 @@ struct PrefillArgs {
     int T, Tp, nc;                       // tokens, padded to kChunk, chunks
     int kh, vh, K;
     float eps;
-    bool bf16;                           // the scan's products on bf16 operands (fp32 accumulation)
     // scratch (device), sized by prefill_scratch_bytes()
     float *glast;                        // exp(cumulative log-decay at chunk end) [vh][nc]
     float *pg, *pe;                      // e^{gc}, e^{gc_last - gc} per token [vh][nc][C]

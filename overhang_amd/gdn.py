@@ -29,9 +29,8 @@ EXPORTS = (
     "omh_gdn_prefill_dev", "omh_sync",
     "omh_attn_layer_init", "omh_attn_layer_free", "omh_attn_forward", "omh_attn_forward_dev",
     "omh_gdn_state_copy", "omh_gdn_state_copy_dev", "omh_attn_cache_get", "omh_attn_cache_set",
-    "omh_gdn_decode_noalloc_dev", "omh_gdn_set_prefill_math", "omh_gdn_decode_core_seq_dev",
+    "omh_gdn_decode_noalloc_dev", "omh_gdn_decode_core_seq_dev",
 )
-OMH_PREFILL_FP32, OMH_PREFILL_BF16 = 0, 1
 
 
 class OmhError(RuntimeError):
@@ -94,7 +93,6 @@ def lib() -> C.CDLL:
         L.omh_gdn_decode_dev.argtypes = [i, i, vp, vp, vp]
         L.omh_gdn_prefill_dev.argtypes = [i, i, i, vp, vp, vp]
         L.omh_gdn_decode_noalloc_dev.argtypes = [i, i, vp, vp, vp]
-        L.omh_gdn_set_prefill_math.argtypes = [i, i]
         L.omh_sync.argtypes = [vp]
         L.omh_gdn_state_copy.argtypes = [i, C.POINTER(C.c_int), i, i]
         L.omh_gdn_state_copy_dev.argtypes = [i, C.POINTER(C.c_int), i, i, vp]
@@ -176,10 +174,6 @@ class GdnLayer:
 
     def free(self) -> None:
         check(lib().omh_gdn_layer_free(self.li))
-
-    def set_prefill_math(self, math: int) -> None:
-        """OMH_PREFILL_FP32 (default) or OMH_PREFILL_BF16 for this layer's prefill."""
-        check(lib().omh_gdn_set_prefill_math(self.li, math))
 
     def reset(self, seq: int = -1) -> None:
         check(lib().omh_gdn_state_reset(self.li, seq))
