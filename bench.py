@@ -91,7 +91,7 @@ def time_launches(hip, st, fn, steps, warmup):
     return max(el, 1e-12), durs, wall
 
 
-def bench_decode(hip, gdn, synth, steps, warmup, full=True):
+def bench_decode(hip, gdn, synth, steps, warmup, full=True, rotated=True):
     from overhang_amd.dims import Q35B
     d = Q35B
     per_layer = d.state_bytes + 4 * d.conv_dim * (d.K - 1)
@@ -122,7 +122,9 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
     def step_fused(k):
         gdn.check(fn(N_LAYERS, arr, k % R, 1, *args))
 
-    el, durs, wall = time_launches(hip, st, step_fused, steps, warmup)
+    # (untimed warm-up: at least two passes over the slots, so every slot's
+    # state has been through the kernel and the clocks have settled)
+    el, durs, wall = time_launches(hip, st, step_fused, steps, max(warmup, 2 * R))
     # host time to issue one launch (no synchronisation inside the loop)
     hip.device_synchronize()
     h0 = time.perf_counter()
@@ -139,8 +141,9 @@ def bench_decode(hip, gdn, synth, steps, warmup, full=True):
     log(f"decode fused 30-layer launch: {fused['tok_s']:.0f} tok/s, kernel {fused['kernel_us']:.1f} us, "
         f"{fused['achieved_GBs']:.0f} GB/s, host issue {issue_us:.1f} us per launch")
 
-    fused["weights_rotated"] = bench_decode_weights_rotated(hip, gdn, synth, d, w, conv0, S0, inp, core, st,
-                                                            steps, warmup)
+    if rotated:
+        fused["weights_rotated"] = bench_decode_weights_rotated(hip, gdn, synth, d, w, conv0, S0, inp, core, st,
+                                                                steps, warmup)
     if not full:
         for L in lays:
             L.free()
@@ -742,9 +745,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--part", choices=("all", "decode", "prefill", "block", "attn", "attnp", "engine", "proj"),
+    ap.add_argument("--part", choices=("all", "decode", "headline", "prefill", "block", "attn", "attnp", "engine",
+                                       "proj"),
                     default="all",
-                    help="decode: the headline only (for profiling); prefill: the T=4096 and T=32768 "
+                    help="decode: the headline and its weights-rotated form; headline: the headline launch "
+                         "alone (for profiling); prefill: the T=4096 and T=32768 "
                          "prefills only; block: the config 5 int8 block at B=64 only; attn: the gated "
                          "attention layer's decode token at 32768 positions only; engine: the 30-layer "
                          "whole-block B=1 chain in a HIP graph; proj: the T=4096 int8 layer prefill; attnp: the "
@@ -782,7 +787,7 @@ def main():
               flush=True)
         return
     fused, engine, sweep, alg_bytes, R = bench_decode(hip, gdn, synth, a.steps, a.warmup,
-                                                      full=a.part == "all")
+                                                      full=a.part == "all", rotated=a.part != "headline")
     pre = warm = block = attn = attnp = snap = eng = preb = None
     if a.part == "all":
         eng = bench_engine_block(hip, gdn, synth, a.steps, a.warmup)

@@ -213,6 +213,61 @@ def test_long_warm_append_matches_recurrent_oracle():
     L.free()
 
 
+def _key_head_slice(d, w, inp, conv0, S0, j):
+    """The layer restricted to key head j and its value heads: their conv
+    channels (q and k of key head j, v of its value heads), gates, z
+    columns and states.  The core couples nothing across key-head groups
+    (qwen.c:331-357: each value head reads only its key head's q, k), so the
+    oracle on this one-key-head layer gives the full layer's values for
+    those heads."""
+    kd, vd, rep = d.kd, d.vd, d.vh // d.kh
+    key_dim = d.kh * kd
+    hs = np.arange(j * rep, (j + 1) * rep)
+    ch = np.r_[j * kd:(j + 1) * kd, key_dim + j * kd:key_dim + (j + 1) * kd,
+               2 * key_dim + j * rep * vd:2 * key_dim + (j + 1) * rep * vd]
+    zc = np.arange(j * rep * vd, (j + 1) * rep * vd)
+    ds = GdnDims(1, rep, kd, vd, d.K, 0)
+    ws = {"conv_w": np.ascontiguousarray(w["conv_w"][ch]), "A_log": w["A_log"][hs], "dt_bias": w["dt_bias"][hs],
+          "gnorm": w["gnorm"]}
+    ins = [np.ascontiguousarray(inp["qkv"][:, ch]), np.ascontiguousarray(inp["z"][:, zc]),
+           np.ascontiguousarray(inp["a"][:, hs]), np.ascontiguousarray(inp["b"][:, hs])]
+    return ds, ws, ins, np.ascontiguousarray(conv0[ch]), np.ascontiguousarray(S0[hs]), hs, ch, zc
+
+
+def test_long_warm_append_35b_full_width_vs_oracle():
+    """Config 4 at the full 35B-A3B width (16 key / 32 value heads): an
+    8192-token prefill, then 32768 tokens continuing from its state, gate
+    logits a ~ N(-2, 1), every input seeded over all 40960 tokens (no
+    repeated block).  The oracle recurrence runs over three key-head groups
+    of the same layer (key heads 0, 9, 15 with their value heads, sliced out
+    as one-key-head layers), token by token over all 40960 tokens; their
+    outputs of the 32768-token call, final states and conv histories must
+    match."""
+    d = Q35B
+    seed = 6200
+    L, w, conv0, S0 = _layer(d, seed)
+    Tw, T = 8192, 32768
+    # (numpy's generator: 335 M normals in seconds, where the repository's
+    # splitmix64 generator takes a minute)
+    rng = np.random.default_rng(seed)
+    N = Tw + T
+    inp = {"qkv": rng.standard_normal((N, d.conv_dim), dtype=np.float32),
+           "z": rng.standard_normal((N, d.val_dim), dtype=np.float32),
+           "a": rng.standard_normal((N, d.vh), dtype=np.float32) - np.float32(2.0),
+           "b": rng.standard_normal((N, d.vh), dtype=np.float32)}
+    part = lambda lo, hi: [np.ascontiguousarray(inp[k][lo:hi]) for k in ("qkv", "z", "a", "b")]
+    L.prefill_core(0, *part(0, Tw))
+    got = L.prefill_core(0, *part(Tw, Tw + T))
+    conv, S = L.get_state(0)
+    L.free()
+    for j in (0, 9, 15):
+        ds, ws, ins, c0, s0, hs, ch, zc = _key_head_slice(d, w, inp, conv0, S0, j)
+        ref, cref, Sref = oracle.core_seq(ds, ws, *ins, c0, s0)
+        assert_close(got[:, zc], ref[Tw:], what=f"35B warm-append key head {j} core")
+        assert_close(S[hs], Sref, what=f"35B warm-append key head {j} S")
+        assert np.array_equal(conv[ch], cref), f"key head {j} conv history"
+
+
 @pytest.mark.parametrize("split", [8192, 8200])
 def test_long_warm_append_35b_split_invariance(split):
     """Config 4 at the 35B shape: prefill(split) then prefill(40960 - split)
