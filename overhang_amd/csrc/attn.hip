@@ -12,12 +12,15 @@
 //     rot dims as two non-interleaved halves (qwen.c:388-398, inverse
 //     frequencies computed on the host as there), then q into a scratch row
 //     and k, v into the sequence's cache rows pos + t (qwen.c:400-404).
-//  2. attn_split_kernel, flash-decoding: one workgroup per (key split, kv
-//     head, token) stages 64-key tiles of K and V through LDS once for all
-//     the query heads of its group (GQA, qwen.c:408-409), keeps a running
-//     max and sum per head (online softmax) and writes unnormalised
-//     partials.  Lane = key for the scores (q broadcast from LDS), lane =
-//     4 output columns for P.V (each key's weight broadcast by readlane).
+//  2. the split kernel, flash-decoding: one workgroup per (key split, kv
+//     head, token) reads the split's K and V rows once for all the query
+//     heads of its group (GQA, qwen.c:408-409), keeps a running max and sum
+//     per head (online softmax) and writes unnormalised partials.  Head
+//     widths of 64 and more: attn_split_mfma_kernel, K and V from HBM
+//     straight into fp32 MFMA operands (the heads of the group are the
+//     products' 16 columns).  Width 32: attn_split_kernel, 64-key tiles
+//     staged through LDS, lane = key for the scores (q broadcast from LDS),
+//     lane = 4 output columns for P.V (each key's weight by readlane).
 //  3. attn_combine_kernel, per (token, head, 64 columns): merges the splits,
 //     normalises, and applies the output gate sigmoid(gate) (qwen.c:421).
 // The o_proj is a second launch_proj.
@@ -62,20 +65,17 @@ __device__ __forceinline__ void rope_table(const AttnArgs &a, int p, float *cs, 
 }
 
 // One q or k row of the prep (RMSNorm with 1 + w, then partial RoPE as two
-// non-interleaved halves), or a v row (w = null: copied), by one wave, into
-// an LDS row (the RoPE pairs are read back from it).  cs_t / sn_t: the
-// token's rope_table.
+// non-interleaved halves), or a v row (no weights: copied), by one wave,
+// into an LDS row (the RoPE pairs are read back from it).  cs_t / sn_t: the
+// token's rope_table.  prep_row_regs takes the row (v, element lane + 64 i
+// in v[i]) and the weights (wv, likewise) already in registers, so a caller
+// can issue those loads ahead of others; prep_row loads them itself.
 template <int HD>
-__device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, const float *w, float *row, int lane,
-                                         const float *cs_t, const float *sn_t) {
+__device__ __forceinline__ void prep_row_regs(const AttnArgs &a, float (&v)[(HD + OMH_WAVE - 1) / OMH_WAVE],
+                                              const float (&wv)[(HD + OMH_WAVE - 1) / OMH_WAVE], bool norm, float *row,
+                                              int lane, const float *cs_t, const float *sn_t) {
     constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
-    float v[NE];
-#pragma unroll
-    for (int i = 0; i < NE; i++) {
-        const int j = lane + OMH_WAVE * i;
-        v[i] = j < HD ? src[j] : 0.f;
-    }
-    if (w) {
+    if (norm) {
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NE; i++) ss += v[i] * v[i];
@@ -85,7 +85,7 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
         for (int i = 0; i < NE; i++) {
             const int j = lane + OMH_WAVE * i;
             if (j < HD) {
-                v[i] = v[i] * rr * (1.f + w[j]);
+                v[i] = v[i] * rr * (1.f + wv[i]);
                 row[j] = v[i];
             }
         }
@@ -110,6 +110,19 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
         const int j = lane + OMH_WAVE * i;
         if (j < HD) row[j] = v[i];
     }
+}
+template <int HD>
+__device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, const float *w, float *row, int lane,
+                                         const float *cs_t, const float *sn_t) {
+    constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
+    float v[NE], wv[NE];
+#pragma unroll
+    for (int i = 0; i < NE; i++) {
+        const int j = lane + OMH_WAVE * i;
+        v[i] = j < HD ? src[j] : 0.f;
+        wv[i] = w && j < HD ? w[j] : 0.f;
+    }
+    prep_row_regs<HD>(a, v, wv, w != nullptr, row, lane, cs_t, sn_t);
 }
 
 // The prep: one workgroup of kPrepWaves waves per token.  The token's RoPE
@@ -343,6 +356,260 @@ void attn_split_kernel(const AttnArgs a) {   // one workgroup per CU (LDS): all 
     }
 }
 #undef OMH_ATTN_LOAD_PIECE
+
+// ---------------------------------------------------------------- decode on the matrix cores
+// The split kernel for head widths of 64 and more: the same work unit (one
+// key split of one kv head for one token, the prep folded in for decode
+// steps), with K and V going from HBM straight into fp32 MFMA operands, so
+// every key row is read once for all the group's query heads (no LDS
+// staging, no per-head re-reads).  Each of the NW waves streams its own
+// 16-key blocks (blocks w, w + NW, ...) and keeps its own online softmax.
+// A wave holds one operand set: a block's K rows, then (once the scores are
+// formed) its V rows in the same registers; the two waves of a SIMD overlap
+// one's loads with the other's products:
+//   S^T = K Q^T   (v_mfma_f32_16x16x4_f32; A = K rows, lane l16 = key;
+//                  B = q from LDS, lane l16 = query head of the group, heads
+//                  past the group zero; head dims taken in the order 16 i + 4 g + s
+//                  on both operands, one 16-byte K load per 4 products),
+//   O += P V      (A = the probabilities as the score product left them:
+//                  key 4 g + s of lane group g is register s; B = V rows
+//                  4 g + s, lane l16 = output columns 64 q + 4 l16 + c of
+//                  tile 4 q + c, so one 16-byte V load serves 4 tiles).
+// The waves' (max, sum, O) then merge through LDS into the split's partial,
+// which the combine kernel merges with the other splits as before.  Keys
+// past the split's end or the token's position are masked (their rows
+// repeat a visible row, so every operand is finite).
+template <int HD>
+struct MfmaSplitShape {
+    static constexpr int NW = 8;                   // waves, two per SIMD
+    static constexpr int QS = HD + 4;              // padded q row in LDS
+    static constexpr int NI = HD / 16;             // K float4s per lane per block (4 k-steps each)
+    static constexpr int NQ = HD / 64;             // V float4s per lane per key step
+    static constexpr size_t LDS = (size_t)(kAttnMaxGroup * QS + NW * 16 * HD + 2 * NW * 16) * sizeof(float);
+    static_assert(HD % 64 == 0, "64-column V groups");
+};
+
+__device__ __forceinline__ omh_v4f ld_stream_v4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(omh_v4f, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kOmhNT));
+}
+
+template <int HD, bool PREP>
+__global__ __launch_bounds__(MfmaSplitShape<HD>::NW * OMH_WAVE, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_split_mfma_kernel(const AttnArgs a) {
+    using S = MfmaSplitShape<HD>;
+    constexpr int NW = S::NW, NT = NW * OMH_WAVE, QS = S::QS, NI = S::NI, NQ = S::NQ;
+    extern __shared__ float smem[];
+    float *qs = smem;                              // [kAttnMaxGroup][QS] the group's q rows
+    float *mo = qs + kAttnMaxGroup * QS;           // [NW][16][HD] the waves' outputs (the prep's scratch before)
+    float *mm = mo + NW * 16 * HD;                 // [NW][16] running max, then [NW][16] sums
+
+    const int H = a.H, KV = a.KV, grp = H / KV, ns = a.ns;
+    const int s = blockIdx.x % ns, g = (blockIdx.x / ns) % KV, t = blockIdx.x / (ns * KV);
+    const int tid = threadIdx.x, lane = tid % OMH_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
+    const int l16 = lane % 16, g4 = lane / 16;
+    const int n = a.pos + t + 1;                   // keys token t sees
+    const int k0 = s * a.kps, k1 = min(n, k0 + a.kps);
+    const size_t pb = ((size_t)t * H + (size_t)g * grp) * ns + s;
+    if (k0 >= k1) {                                // an empty split: weight zero in the merge
+        for (int e = tid; e < grp * (HD / 4); e += NT) {
+            const size_t pi = pb + (size_t)(e / (HD / 4)) * ns;
+            *reinterpret_cast<float4 *>(a.po + pi * HD + 4 * (e % (HD / 4))) = f4_zero();
+            if (e % (HD / 4) == 0) {
+                a.pml[2 * pi] = -INFINITY;
+                a.pml[2 * pi + 1] = 0.f;
+            }
+        }
+        return;
+    }
+    const size_t cache0 = ((size_t)a.seq * KV + g) * a.max_t * HD;
+    const int cbytes = a.max_t * HD * (int)sizeof(float);          // (launch_attn_d checks the range)
+    const __amdgpu_buffer_rsrc_t krs = omh_rsrc(a.Kc + cache0, cbytes), vrs = omh_rsrc(a.Vc + cache0, cbytes);
+    const int nb = (k1 - k0 + 15) / 16;            // 16-key blocks of the split
+    // one operand set: a block's K rows (lane (l16, g4): key l16, dims
+    // 16 i + 4 g4 .. +3 in kv[i]), then its V rows (key 4 g4 + st, columns
+    // 64 q + 4 l16 .. +3 in kv[NQ st + q])
+    static_assert(NI == 4 * NQ, "K and V fill the same registers");
+    omh_v4f kv[NI];
+    auto load_k = [&](int b) __attribute__((always_inline)) {
+        const int kk = min(k0 + 16 * b + l16, k1 - 1);
+#pragma unroll
+        for (int i = 0; i < NI; i++) kv[i] = ld_stream_v4(krs, (kk * HD + 16 * i + 4 * g4) * 4);
+    };
+    auto load_v = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int kr = min(k0 + 16 * b + 4 * g4 + st, k1 - 1);
+#pragma unroll
+            for (int q = 0; q < NQ; q++) kv[NQ * st + q] = ld_stream_v4(vrs, (kr * HD + 64 * q + 4 * l16) * 4);
+        }
+    };
+    // Prologue.  A decode step's RoPE table comes first (its out-of-line
+    // cos / sin call waits for every load the wave has in flight), and the
+    // split holding the step's position writes the new k / v cache rows.
+    // Then the loads the q prep needs (the group's q rows, the norm weights)
+    // and the first K / V block of the wave go out, in that order, in
+    // straight-line code: loads complete in issue order, so the prep's waits
+    // leave the block's loads in flight.  A prompt step's prepared q rows go
+    // to LDS before the block loads.
+    const int p = a.pos + t;
+    if constexpr (PREP) {
+        const float *row = a.qkv + (size_t)t * a.ld_qkv;
+        float *krow = mo, *cs = mo + HD, *sn = cs + HD / 2;
+        rope_table(a, p, cs, sn, tid, NT);
+        __syncthreads();
+        if (k0 <= p && p < k1) {
+            // the new k (wave 0, normed and rotated through a scratch LDS row)
+            // and v (wave 1) of kv head g go into the cache rows p
+            const size_t crow = (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
+            if (wave == 0) {
+                prep_row<HD>(a, row + (size_t)2 * H * HD + (size_t)g * HD, a.kn, krow, lane, cs, sn);
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                for (int j = lane; j < HD; j += OMH_WAVE) a.Kc[crow + j] = krow[j];
+            } else if (wave == 1) {
+                for (int j = lane; j < HD; j += OMH_WAVE) a.Vc[crow + j] = row[(size_t)2 * H * HD + (size_t)(KV + g) * HD + j];
+            }
+            __threadfence();                       // the rows are in memory before any block load reads them
+            __syncthreads();
+        }
+        constexpr int NE = HD / OMH_WAVE, MAXH = (kAttnMaxGroup + NW - 1) / NW;
+        float xv[MAXH][NE], wn[NE];
+#pragma unroll
+        for (int k = 0; k < MAXH; k++) {
+            const int i = min(wave + NW * k, grp - 1);
+#pragma unroll
+            for (int e = 0; e < NE; e++) xv[k][e] = row[(size_t)(g * grp + i) * 2 * HD + lane + OMH_WAVE * e];
+        }
+#pragma unroll
+        for (int e = 0; e < NE; e++) wn[e] = a.qn[lane + OMH_WAVE * e];
+#pragma unroll
+        for (int k = 0; k < MAXH; k++) {
+            const int i = wave + NW * k;
+            if (i < grp) prep_row_regs<HD>(a, xv[k], wn, true, qs + i * QS, lane, cs, sn);
+        }
+        load_k(wave);
+    } else {
+        for (int e = tid; e < grp * (HD / 4); e += NT) {
+            const int i = e / (HD / 4), c = e % (HD / 4);
+            *reinterpret_cast<float4 *>(qs + i * QS + 4 * c) =
+                *reinterpret_cast<const float4 *>(a.qb + ((size_t)t * H + (size_t)g * grp + i) * HD + 4 * c);
+        }
+        load_k(wave);
+    }
+    // (LDS-only barriers from here on: a full __syncthreads would also wait
+    // for the block loads in flight)
+    omh_lds_barrier();
+    // q as the B operand: lane (g4, head l16) reads q[l16][16 i + 4 g4 .. +3]
+    // (rows past the group read as zero)
+    if (grp < 16) {
+        for (int e = tid; e < (16 - grp) * (HD / 4); e += NT)
+            *reinterpret_cast<float4 *>(qs + (grp + e / (HD / 4)) * QS + 4 * (e % (HD / 4))) = f4_zero();
+        omh_lds_barrier();
+    }
+    const float *qrow = qs + l16 * QS + 4 * g4;
+
+    float m = -INFINITY, l = 0.f;                  // of head l16 (the same in the four lane groups)
+    omh_v4f o[NI];                                 // O rows 4 g4 + r, columns 64 q + 4 l16 + c of tile 4 q + c
+#pragma unroll
+    for (int dt = 0; dt < NI; dt++) o[dt] = omh_v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto step = [&](int b) __attribute__((always_inline)) {
+        // scores of keys kb + 4 g4 + r for head l16 (two product chains)
+        omh_v4f sa = omh_v4f{0.f, 0.f, 0.f, 0.f}, sb = sa;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const omh_v4f qf = *reinterpret_cast<const omh_v4f *>(qrow + 16 * i);
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                if (i & 1) sb = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i][st], qf[st], sb, 0, 0, 0);
+                else sa = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[i][st], qf[st], sa, 0, 0, 0);
+            }
+        }
+        load_v(b);                                 // (into the registers the scores have read)
+        const int kb = k0 + 16 * b;
+        float sc[4], mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            sc[r] = kb + 4 * g4 + r < k1 ? (sa[r] + sb[r]) * a.scale : -INFINITY;   // qwen.c:410-414
+            mx = fmaxf(mx, sc[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        // online softmax (qwen.c:413 softmax_ over all keys, merged per block);
+        // the block's first key is visible, so mn is finite
+        const float mn = fmaxf(m, mx);
+        const float corr = expf(m - mn);
+        float pr[4], ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            pr[r] = kb + 4 * g4 + r < k1 ? expf(sc[r] - mn) : 0.f;
+            ps += pr[r];
+        }
+        ps += __shfl_xor(ps, 16, OMH_WAVE);
+        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        l = l * corr + ps;
+        m = mn;
+        // the output rows are heads 4 g4 + r: their corrections from lanes 4 g4 + r
+        float cr[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) cr[r] = __shfl(corr, 4 * g4 + r, OMH_WAVE);
+#pragma unroll
+        for (int dt = 0; dt < NI; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] *= cr[r];
+        // P.V (qwen.c:415-419)
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int st = 0; st < 4; st++)
+                    o[4 * q + c] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[st], kv[NQ * st + q][c], o[4 * q + c], 0, 0, 0);
+    };
+    // the wave's blocks wave, wave + NW, ... (block wave's loads went out above)
+    for (int b = wave; b < nb; b += NW) {
+        if (b != wave) load_k(b);
+        step(b);
+    }
+
+    // merge the waves: the workgroup's max per head, each wave's output scaled to it
+    if (g4 == 0) {
+        mm[wave * 16 + l16] = m;
+        mm[NW * 16 + wave * 16 + l16] = l;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int h = 4 * g4 + r;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mm[w * 16 + h]);
+        const float f = expf(mm[wave * 16 + h] - M);        // 0 for a wave without blocks (its m is -inf)
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            *reinterpret_cast<omh_v4f *>(mo + (wave * 16 + h) * HD + 64 * q + 4 * l16) =
+                omh_v4f{o[4 * q][r] * f, o[4 * q + 1][r] * f, o[4 * q + 2][r] * f, o[4 * q + 3][r] * f};
+    }
+    __syncthreads();
+    for (int e = tid; e < grp * (HD / 4); e += NT) {
+        const int i = e / (HD / 4), c = e % (HD / 4);
+        omh_v4f acc = *reinterpret_cast<const omh_v4f *>(mo + i * HD + 4 * c);
+#pragma unroll
+        for (int w = 1; w < NW; w++) acc += *reinterpret_cast<const omh_v4f *>(mo + (w * 16 + i) * HD + 4 * c);
+        *reinterpret_cast<omh_v4f *>(a.po + (pb + (size_t)i * ns) * HD + 4 * c) = acc;
+    }
+    if (tid < grp) {
+        float M = -INFINITY, L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mm[w * 16 + tid]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) L += mm[NW * 16 + w * 16 + tid] * expf(mm[w * 16 + tid] - M);
+        const size_t pi = pb + (size_t)tid * ns;
+        a.pml[2 * pi] = M;
+        a.pml[2 * pi + 1] = L;
+    }
+}
 
 // ---------------------------------------------------------------- prompt steps
 // Flash attention on the matrix cores for prompt steps of at least
@@ -765,11 +1032,16 @@ template <int HD>
 hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
     static const bool lds_ok = [] {
         bool ok = true;
-        for (const void *f : {(const void *)attn_split_kernel<HD, 1>, (const void *)attn_split_kernel<HD, 2>,
-                              (const void *)attn_split_kernel<HD, 3>, (const void *)attn_split_kernel<HD, 4>,
-                              (const void *)attn_split_kernel<HD, 1, true>, (const void *)attn_split_kernel<HD, 2, true>,
-                              (const void *)attn_split_kernel<HD, 3, true>, (const void *)attn_split_kernel<HD, 4, true>})
-            ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)AttnShape<HD>::LDS) == hipSuccess;
+        if constexpr (HD >= 64) {
+            for (const void *f : {(const void *)attn_split_mfma_kernel<HD, false>, (const void *)attn_split_mfma_kernel<HD, true>})
+                ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)MfmaSplitShape<HD>::LDS) == hipSuccess;
+        } else {
+            for (const void *f : {(const void *)attn_split_kernel<HD, 1>, (const void *)attn_split_kernel<HD, 2>,
+                                  (const void *)attn_split_kernel<HD, 3>, (const void *)attn_split_kernel<HD, 4>,
+                                  (const void *)attn_split_kernel<HD, 1, true>, (const void *)attn_split_kernel<HD, 2, true>,
+                                  (const void *)attn_split_kernel<HD, 3, true>, (const void *)attn_split_kernel<HD, 4, true>})
+                ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)AttnShape<HD>::LDS) == hipSuccess;
+        }
         return ok;
     }();
     if (!lds_ok) return hipErrorInvalidValue;
@@ -798,22 +1070,31 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
             return hipGetLastError();
         }
     }
-    const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(AttnShape<HD>::NW * OMH_WAVE);
-    const size_t lds = AttnShape<HD>::LDS;
-    const int gpw = (a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW;
-    if (fuse) {
-        switch (gpw) {
-        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1, true>), grid, blk, lds, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2, true>), grid, blk, lds, st, a); break;
-        case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3, true>), grid, blk, lds, st, a); break;
-        default: hipLaunchKernelGGL((attn_split_kernel<HD, 4, true>), grid, blk, lds, st, a); break;
-        }
+    if constexpr (HD >= 64) {
+        // the K / V slices of a (sequence, kv head) are addressed by 32-bit byte offsets
+        if ((size_t)a.max_t * HD * sizeof(float) > (size_t)INT32_MAX) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(MfmaSplitShape<HD>::NW * OMH_WAVE);
+        const size_t lds = MfmaSplitShape<HD>::LDS;
+        if (fuse) hipLaunchKernelGGL((attn_split_mfma_kernel<HD, true>), grid, blk, lds, st, a);
+        else hipLaunchKernelGGL((attn_split_mfma_kernel<HD, false>), grid, blk, lds, st, a);
     } else {
-        switch (gpw) {
-        case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, blk, lds, st, a); break;
-        case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, blk, lds, st, a); break;
-        case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3>), grid, blk, lds, st, a); break;
-        default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
+        const dim3 grid((unsigned)(a.ns * a.KV * a.T)), blk(AttnShape<HD>::NW * OMH_WAVE);
+        const size_t lds = AttnShape<HD>::LDS;
+        const int gpw = (a.H / a.KV + AttnShape<HD>::NW - 1) / AttnShape<HD>::NW;
+        if (fuse) {
+            switch (gpw) {
+            case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1, true>), grid, blk, lds, st, a); break;
+            case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2, true>), grid, blk, lds, st, a); break;
+            case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3, true>), grid, blk, lds, st, a); break;
+            default: hipLaunchKernelGGL((attn_split_kernel<HD, 4, true>), grid, blk, lds, st, a); break;
+            }
+        } else {
+            switch (gpw) {
+            case 1: hipLaunchKernelGGL((attn_split_kernel<HD, 1>), grid, blk, lds, st, a); break;
+            case 2: hipLaunchKernelGGL((attn_split_kernel<HD, 2>), grid, blk, lds, st, a); break;
+            case 3: hipLaunchKernelGGL((attn_split_kernel<HD, 3>), grid, blk, lds, st, a); break;
+            default: hipLaunchKernelGGL((attn_split_kernel<HD, 4>), grid, blk, lds, st, a); break;
+            }
         }
     }
     constexpr int NCB = HD < OMH_WAVE ? 1 : HD / OMH_WAVE;
