@@ -1928,7 +1928,9 @@ void proj_i8_dq_kernel(const ProjArgs p, const F32Part f) {
 #pragma unroll
                 for (int h = 0; h < 2; h++)
                     ia[pl][rt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[sl % 2][rt][h], xq[sl][pl][h], ia[pl][rt], 0, 0, 0);
-        x_load(b + kDqX, slot_c);                            // the ring slot just used, kDqX blocks ahead
+        // the ring slot just used, kDqX blocks ahead (none past the last
+        // block: the epilogue would wait for those loads)
+        if (NBC == 0 || b + kDqX < NB) x_load(b + kDqX, slot_c);
     };
     static_for<kDqX>([&](auto sc) __attribute__((always_inline)) { x_load(decltype(sc)::value, sc); });
     w_read(0, std::integral_constant<int, 0>{});
