@@ -431,6 +431,10 @@ void prefill_wy_kernel(const PrefillArgs a) {
         constexpr bool isP = decltype(isPc)::value;
         int ti, tj;
         lower_tile(t, ti, tj);
+        // (the lane indices laundered: the index arithmetic is redone here
+        // rather than kept alive from the first value head's call)
+        int g4 = lane / 16, l16 = lane % 16;
+        asm volatile("" : "+v"(g4), "+v"(l16));
         const float4 gr = *reinterpret_cast<const float4 *>(gt + 16 * ti + 4 * g4);
         const float gcol = gt[16 * tj + l16];
         float4 br = make_float4(1.f, 1.f, 1.f, 1.f);
