@@ -401,8 +401,8 @@ def bench_prefill(hip, gdn, synth, T, steps, warmup):
            "flops_per_call": fl, "TFLOPs": tf, "peak_TFLOPs": round(peak, 1),
            "frac_fp32_mfma": tf / FP32_MFMA_TFLOPS, "frac_peak": tf / peak, "frac_attainable": tf / attain,
            "hbm_bytes_alg": by, "recurrent_equiv_GFLOP": 7 * d.vh * T * d.kd * d.vd / 1e9,
-           "note": "one GDN layer core (4 launches: WY/chunk (conv, norms, gates, triangular solve, "
-                   "panels), conv-history commit, scan, gated norm), "
+           "note": "one GDN layer core (3 launches: WY/chunk (conv, norms, gates, triangular solve, "
+                   "panels), scan, gated norm with the conv-history commit), "
                    "kh=16 vh=32 kd=vd=128, fp32 I/O, state carried across calls, fp32 MFMA"}
     log(f"prefill T={T}: {1e6 * t:.0f} us/layer, {out['tok_s']:.3g} tok/s, {tf:.1f} TFLOP/s "
         f"({100 * out['frac_peak']:.1f}% of the {peak:.0f} TFLOP/s matrix-core bound)")
