@@ -92,13 +92,14 @@ def test_35b_int8_block_batch64():
 @pytest.mark.parametrize("shape,B", [
     ((2, 4, 64, 64, 512), 5),        # sliced core kernel; out_proj on the staged bf16 x 3 kernel
     ((2, 4, 64, 64, 512), 40),
-    ((4, 8, 128, 128, 1024), 64),    # paired core kernel; out_proj wave tiles of 16 tokens
+    ((4, 8, 128, 128, 1024), 64),    # paired core kernel; out_proj on the streaming kernel, k split over 2
     ((16, 32, 128, 128, 2048), 8),   # the 35B shape, sliced core; out_proj with a k split
 ], ids=["d64-B5", "d64-B40", "d128-B64", "35b-B8"])
 def test_int8_block_core_writes_out_proj_planes(shape, B):
-    """int8 blocks whose decode core also writes out_proj's bf16 planes and
-    block sums (so the projection skips its split launch): two steps, three
-    sequences against the per-token oracle."""
+    """int8 blocks whose decode core also writes out_proj's x planes (int8
+    planes with 128-wide block scales where the head width is a multiple of
+    128, else bf16 planes and block sums), so the projection skips its split
+    launch: two steps, three sequences against the per-token oracle."""
     from overhang_amd.dims import GdnDims
     kh, vh, kd, vd, hidden = shape
     d = GdnDims(kh=kh, vh=vh, kd=kd, vd=vd, K=4, hidden=hidden)
