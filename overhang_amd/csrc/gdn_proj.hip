@@ -122,43 +122,62 @@ __device__ __forceinline__ void load_x16(const float *src, float (&x)[16]) {
 // int8 rows + 64 fp32 rows, 25.7 MB), MI355X: 6.9 us, against 10.4 us with
 // the fp32 rows inside the int8 workgroups and x requested after the
 // weights (a plain read of the same bytes: 5.3 us).
-constexpr int kGemvRows = 8;
+
+// Rows per wave.  35B at one token, engine-order chain of 30 layers (in_proj
+// 2048 -> 12352, out_proj 4096 -> 2048), MI355X: 18.2 us per layer with 4
+// rows (in_proj 1536 workgroups, out_proj 512), 18.5 us with 8, 19.3 us
+// with 2.
+constexpr int kGemvRows = 4;
 constexpr int kGemvCB = 1;            // chunks per request group
 
-// Sum of v[i] over the 64 lanes for 8 values at once, halving the set at
-// each of the first three exchanges: lane L ends with the total of value
-// 4*bit5(L) + 2*bit4(L) + bit3(L).
-__device__ __forceinline__ float sum8_over_lanes(const float (&v)[8], int lane) {
-    float u[4], t[2];
+// Sum of v[i] over the 64 lanes for R (1, 2, 4 or 8) values at once,
+// halving the set at each of the first log2 R exchanges (lane offsets 32,
+// 16, 8), then summing the rest: lane L ends with the total of value
+// gemv_row_of_lane<R>(L) (R = 8: 4*bit5(L) + 2*bit4(L) + bit3(L)).  The
+// lane bits are tested once, up front: a test per select costs a compare
+// and a hazard wait each.
+template <int R>
+__device__ __forceinline__ int gemv_row_of_lane(int lane) {
+    const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
+    return R == 8 ? 4 * b5 + 2 * b4 + b3 : (R == 4 ? 2 * b5 + b4 : (R == 2 ? b5 : 0));
+}
+// one halving exchange: lanes with hi keep the upper H values
+template <int OFF, int H>
+__device__ __forceinline__ void gemv_halve(float *c, bool hi) {
+#pragma unroll
+    for (int i = 0; i < H; i++) {
+        const float send = hi ? c[i] : c[i + H];
+        c[i] = (hi ? c[i + H] : c[i]) + __shfl_xor(send, OFF, OMH_WAVE);
+    }
+}
+template <int R>
+__device__ __forceinline__ float sum_rows_over_lanes(const float (&v)[R], int lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "rows per wave");
     const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8;
+    float c[R];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float send = h5 ? v[i] : v[i + 4];
-        u[i] = (h5 ? v[i + 4] : v[i]) + __shfl_xor(send, 32, OMH_WAVE);
-    }
+    for (int i = 0; i < R; i++) c[i] = v[i];
+    constexpr int LG = R == 8 ? 3 : (R == 4 ? 2 : (R == 2 ? 1 : 0));
+    if constexpr (LG >= 1) gemv_halve<32, R / 2>(c, h5);
+    if constexpr (LG >= 2) gemv_halve<16, R / 4>(c, h4);
+    if constexpr (LG >= 3) gemv_halve<8, 1>(c, h3);
+    float r = c[0];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const float send = h4 ? u[i] : u[i + 2];
-        t[i] = (h4 ? u[i + 2] : u[i]) + __shfl_xor(send, 16, OMH_WAVE);
-    }
-    float r = (h3 ? t[1] : t[0]) + __shfl_xor(h3 ? t[0] : t[1], 8, OMH_WAVE);
-    r += __shfl_xor(r, 4, OMH_WAVE);
-    r += __shfl_xor(r, 2, OMH_WAVE);
-    r += __shfl_xor(r, 1, OMH_WAVE);
+    for (int off = 32 >> LG; off >= 1; off >>= 1) r += __shfl_xor(r, off, OMH_WAVE);
     return r;
 }
 
-// kGemvRows int8 rows r0.. over k-slice ks of KS, NT tokens; the k-slices
-// meet in LDS (red) and the first slice's wave stores (unless !store).
-template <int NT, int KS>
+// R int8 rows r0.. over k-slice ks of KS, NT tokens; the k-slices meet in
+// LDS (red) and the first slice's wave stores (unless !store).
+template <int NT, int KS, int R>
 __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, int lane,
                                              float (*red)[NT][OMH_WAVE], int rg, bool store) {
-    float acc[kGemvRows][NT];
+    float acc[R][NT];
 #pragma unroll
-    for (int i = 0; i < kGemvRows; i++)
+    for (int i = 0; i < R; i++)
 #pragma unroll
         for (int t = 0; t < NT; t++) acc[i][t] = 0.f;
-    const int nrow = min(kGemvRows, p.n_q - r0);
+    const int nrow = min(R, p.n_q - r0);
     const int klen = p.I / KS, kbeg = ks * klen, kend = kbeg + klen;
     for (int kc = kbeg; kc < kend; kc += kGemvCB * 16 * OMH_WAVE) {
         int kk[kGemvCB];
@@ -175,14 +194,14 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
 #pragma unroll
             for (int t = 0; t < NT; t++) load_x16(p.x + (size_t)t * p.ldx + kk[c], x[c][t]);
         __builtin_amdgcn_sched_barrier(0);            // x first, then the weights
-        WFrag<true> wf[kGemvRows][kGemvCB];
+        WFrag<true> wf[R][kGemvCB];
 #pragma unroll
-        for (int i = 0; i < kGemvRows; i++)
+        for (int i = 0; i < R; i++)
 #pragma unroll
             for (int c = 0; c < kGemvCB; c++) wf[i][c].load(p, r0 + min(i, nrow - 1), kk[c]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < kGemvRows; i++)
+        for (int i = 0; i < R; i++)
 #pragma unroll
             for (int c = 0; c < kGemvCB; c++) {
                 if (!live[c]) continue;
@@ -194,15 +213,14 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
                     for (int e = 0; e < 16; e++) acc[i][t] = fmaf(x[c][t][e], w[e], acc[i][t]);
             }
     }
-    // lane L holds row 4*bit5(L) + 2*bit4(L) + bit3(L) after the reduction
-    const int myrow = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+    const int myrow = gemv_row_of_lane<R>(lane);
     float tot[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        float v[8];
+        float v[R];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = acc[i][t];
-        tot[t] = sum8_over_lanes(v, lane);
+        for (int i = 0; i < R; i++) v[i] = acc[i][t];
+        tot[t] = sum_rows_over_lanes<R>(v, lane);
     }
     if (KS > 1) {
         if (ks > 0)
@@ -215,7 +233,7 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
 #pragma unroll
             for (int t = 0; t < NT; t++) tot[t] += red[j * 4 + rg][t][lane];
     }
-    if (store && (lane & 7) == 0 && myrow < nrow) {
+    if (store && lane % (OMH_WAVE / R) == 0 && myrow < nrow) {
         const int o = r0 + myrow;
         const float sc = p.scale[o];
 #pragma unroll
@@ -272,7 +290,7 @@ __device__ __forceinline__ void gemv_f32_row(const ProjArgs &p, int row, int lan
 
 // Workgroups 0 .. nwg8-1: the int8 rows; the rest: the fp32 rows, four per
 // workgroup (one per wave).
-template <int NT, int KS>
+template <int NT, int KS, int R>
 __global__ __launch_bounds__(4 * OMH_WAVE)
 void proj_gemv_kernel(const ProjArgs p, int nwg8) {
     constexpr int RG = 4 / KS;
@@ -287,9 +305,9 @@ void proj_gemv_kernel(const ProjArgs p, int nwg8) {
     const int rg = wv % RG, ks = wv / RG;
     // a row group past the int8 rows works on the last group instead (the
     // workgroup stays together for the k-slice reduction) and stores nothing
-    const int rs = (blockIdx.x * RG + rg) * kGemvRows;
-    const int r0 = min(rs, ((p.n_q - 1) / kGemvRows) * kGemvRows);
-    gemv_q8_rows<NT, KS>(p, r0, ks, lane, red, rg, rs < p.n_q);
+    const int rs = (blockIdx.x * RG + rg) * R;
+    const int r0 = min(rs, ((p.n_q - 1) / R) * R);
+    gemv_q8_rows<NT, KS, R>(p, r0, ks, lane, red, rg, rs < p.n_q);
 }
 
 // ---------------------------------------------------------------- MFMA
@@ -2208,10 +2226,10 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         const int rows_per_wg = (4 / ks) * kGemvRows;
         const int nwg8 = (p.n_q + rows_per_wg - 1) / rows_per_wg, nf = (p.O - p.n_q + 3) / 4;
         const dim3 grid(nwg8 + nf), blk(4 * OMH_WAVE);
-#define OMH_GEMV(NT)                                                                              \
-    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4>), grid, blk, 0, st, p, nwg8);       \
-    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2>), grid, blk, 0, st, p, nwg8);  \
-    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1>), grid, blk, 0, st, p, nwg8);
+#define OMH_GEMV(NT)                                                                                          \
+    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4, kGemvRows>), grid, blk, 0, st, p, nwg8);         \
+    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2, kGemvRows>), grid, blk, 0, st, p, nwg8);    \
+    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1, kGemvRows>), grid, blk, 0, st, p, nwg8);
         switch (p.T) {
         case 1: OMH_GEMV(1) break;
         case 2: OMH_GEMV(2) break;
