@@ -29,11 +29,13 @@
 //  * sliced (small launches): one workgroup per value head, or per column
 //    slice of one.  The delta rule couples only the rows of one column, so
 //    a head may split into NCS slices.  The gated RMSNorm needs the whole
-//    row of o: each slice
-//    publishes its raw o and its partial sum of squares (device-coherent
-//    atomic stores), and the last slice of the head to arrive (arrival
-//    counter) applies the norm to all vd columns, summing the partials in
-//    slice order, so the result does not depend on arrival order.
+//    row of o: either each slice writes o * gnorm * silu(z) and its partial
+//    sum of squares of o, and the consumer applies 1 / rms (a whole-layer
+//    step at up to 4 tokens: out_proj's GEMV, as it loads x), or each slice
+//    publishes its raw o and partial sum (device-coherent atomic stores)
+//    and the last slice of the head to arrive (arrival counter) applies the
+//    norm to all vd columns.  Both sum the partials in slice order, so the
+//    result does not depend on arrival order.
 //
 // Conv history lives in a per-channel ring (omh_internal.h): readers use
 // the K-1 history slots, the single owner of a channel writes the new input
@@ -505,8 +507,11 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
              },
              2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, seq, ph, K);
     const int t4 = tid < VD / 4 ? tid : 0;
-    const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + t4 * 4);
-    const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + t4 * 4);
+    // z and gnorm of the columns this thread gates: the head's columns 4 t4
+    // (norm here), or the slice's own columns (1 / rms left to the consumer)
+    const int zc = args.ssq_out ? col0 + 4 * c4 : 4 * t4;
+    const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + zc);
+    const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + zc);
     const float ga = args.a[tok * args.ld_ab + h], gb = args.b[tok * args.ld_ab + h];
     const float galog = L.A_log[h], gdt = L.dt_bias[h];
 
@@ -557,6 +562,12 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
             if constexpr (VD % 64 == 0)
                 if (args.xb) write_x(PlaneOut{args.xb, args.xb_T, vdim, args.xb_i8}, args.xb_t0 + b, h * VD + c4 * 4, c4, y);
         }
+    } else if (args.ssq_out) {
+        // Deferred norm: this slice's o * gnorm * silu(z) and its sum of
+        // squares of o; the next launch (out_proj's GEMV) applies 1 / rms as
+        // it loads them, so no slice waits for another.
+        if (rg == 0) *reinterpret_cast<float4 *>(core + col0 + c4 * 4) = gated(o, 1.f, gn, zz);
+        if (tid == 0) args.ssq_out[(tok * vh + h) * NCS + cs] = ss;
     } else {
         // Cross-slice exchange with device-coherent (agent-scope) relaxed
         // atomics only: they bypass the per-XCD L2s, so no L2 write-back is
@@ -671,8 +682,19 @@ bool decode_planes_supported(int vd, int variant, bool i8) {
     return vd % (i8 ? kI8Blk : 64) == 0 && (variant == 0 || variant == kDecodePaired || variant == 1);
 }
 
+// Column slices for a deferred-norm launch (one layer, up to 4 tokens): 4
+// per value head, no exchange between them.  35B shape, engine-order chain
+// of 30 whole int8 layers at B = 1, MI355X: 17.8 us per layer with 4 slices
+// and the 1 / rms in out_proj's GEMV (core 5.8 us), 18.2 us with one
+// workgroup per value head and the norm in the core (core 6.5 us); timing
+// copies without any norm put 2 and 8 slices behind 4.
+int decode_deferred_slices(int kd, int vd) {
+    return slice_valid(kd, vd, 4) && vd % 16 == 0 ? 4 : 0;
+}
+
 hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, hipStream_t st) {
     if (!decode_core_supported(kd, vd, a.vh / a.kh, a.K)) return hipErrorInvalidValue;
+    if (a.ssq_out && (a.nl != 1 || variant != 4 || a.xb)) return hipErrorInvalidValue;
     if (a.rep != a.vh / a.kh) return hipErrorInvalidValue;
     if (a.xb && (a.nl != 1 || !decode_planes_supported(vd, variant, a.xb_i8))) return hipErrorInvalidValue;
     if (variant == 0) variant = choose_variant(a, kd, vd);

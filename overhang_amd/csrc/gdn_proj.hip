@@ -168,8 +168,12 @@ __device__ __forceinline__ float sum_rows_over_lanes(const float (&v)[R], int la
 }
 
 // R int8 rows r0.. over k-slice ks of KS, NT tokens; the k-slices meet in
-// LDS (red) and the first slice's wave stores (unless !store).
-template <int NT, int KS, int R>
+// LDS (red) and the first slice's wave stores (unless !store).  GN: x is a
+// decode core's gated output before its 1 / rms, which is applied here as
+// x is loaded (ProjArgs::gssq): the lane's 16 inputs lie in one head, whose
+// slices' sums of squares (one 16-byte load) are requested with x, before
+// the weights, and summed in slice order once the weights are requested.
+template <int NT, int KS, int R, bool GN>
 __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, int lane,
                                              float (*red)[NT][OMH_WAVE], int rg, bool store) {
     float acc[R][NT];
@@ -193,6 +197,16 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
         for (int c = 0; c < kGemvCB; c++)
 #pragma unroll
             for (int t = 0; t < NT; t++) load_x16(p.x + (size_t)t * p.ldx + kk[c], x[c][t]);
+        constexpr int NC = GN ? kGemvCB : 1, NTG = GN ? NT : 1;
+        float4 sq[NC][NTG];
+        if constexpr (GN) {
+            const int nh = p.I / p.gvd;
+#pragma unroll
+            for (int c = 0; c < kGemvCB; c++)
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    sq[c][t] = *reinterpret_cast<const float4 *>(p.gssq + ((size_t)t * nh + kk[c] / p.gvd) * 4);
+        }
         __builtin_amdgcn_sched_barrier(0);            // x first, then the weights
         WFrag<true> wf[R][kGemvCB];
 #pragma unroll
@@ -200,6 +214,22 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
 #pragma unroll
             for (int c = 0; c < kGemvCB; c++) wf[i][c].load(p, r0 + min(i, nrow - 1), kk[c]);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (GN) {
+            // the gated RMSNorm's 1 / rms (qwen.c:353-357), its sum in slice order
+#pragma unroll
+            for (int c = 0; c < kGemvCB; c++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    float ss = 0.f;
+                    ss += sq[c][t].x;
+                    ss += sq[c][t].y;
+                    ss += sq[c][t].z;
+                    ss += sq[c][t].w;
+                    const float rn = 1.f / sqrtf(ss / (float)p.gvd + p.geps);
+#pragma unroll
+                    for (int e = 0; e < 16; e++) x[c][t][e] *= rn;
+                }
+        }
 #pragma unroll
         for (int i = 0; i < R; i++)
 #pragma unroll
@@ -290,7 +320,7 @@ __device__ __forceinline__ void gemv_f32_row(const ProjArgs &p, int row, int lan
 
 // Workgroups 0 .. nwg8-1: the int8 rows; the rest: the fp32 rows, four per
 // workgroup (one per wave).
-template <int NT, int KS, int R>
+template <int NT, int KS, int R, bool GN>
 __global__ __launch_bounds__(4 * OMH_WAVE)
 void proj_gemv_kernel(const ProjArgs p, int nwg8) {
     constexpr int RG = 4 / KS;
@@ -307,7 +337,7 @@ void proj_gemv_kernel(const ProjArgs p, int nwg8) {
     // workgroup stays together for the k-slice reduction) and stores nothing
     const int rs = (blockIdx.x * RG + rg) * R;
     const int r0 = min(rs, ((p.n_q - 1) / R) * R);
-    gemv_q8_rows<NT, KS, R>(p, r0, ks, lane, red, rg, rs < p.n_q);
+    gemv_q8_rows<NT, KS, R, GN>(p, r0, ks, lane, red, rg, rs < p.n_q);
 }
 
 // ---------------------------------------------------------------- MFMA
@@ -2220,16 +2250,21 @@ bool proj_x_int8_planes(int T, int I, int n_q) { return use_i8(T, I, n_q); }
 hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
     if (p.O <= 0 || p.T <= 0) return hipSuccess;
     if (!proj_supported(p.I, p.n_q)) return hipErrorInvalidValue;
+    // the deferred gated norm: the GEMV's int8 rows only, heads of whole 16-input pieces
+    if (p.gssq && (p.T > 4 || p.n_q != p.O || p.gvd < 16 || p.gvd % 16 != 0 || p.I % p.gvd != 0 || !al16(p.gssq)))
+        return hipErrorInvalidValue;
     if (p.T <= 4) {
         // k-slices: as many 1024-wide chunks as there are, up to 4 per row group
         const int ks = p.I >= 4096 ? 4 : (p.I >= 2048 ? 2 : 1);
         const int rows_per_wg = (4 / ks) * kGemvRows;
         const int nwg8 = (p.n_q + rows_per_wg - 1) / rows_per_wg, nf = (p.O - p.n_q + 3) / 4;
         const dim3 grid(nwg8 + nf), blk(4 * OMH_WAVE);
-#define OMH_GEMV(NT)                                                                                          \
-    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4, kGemvRows>), grid, blk, 0, st, p, nwg8);         \
-    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2, kGemvRows>), grid, blk, 0, st, p, nwg8);    \
-    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1, kGemvRows>), grid, blk, 0, st, p, nwg8);
+#define OMH_GEMV_KS(NT, GN)                                                                                       \
+    if (ks == 4) hipLaunchKernelGGL((proj_gemv_kernel<NT, 4, kGemvRows, GN>), grid, blk, 0, st, p, nwg8);         \
+    else if (ks == 2) hipLaunchKernelGGL((proj_gemv_kernel<NT, 2, kGemvRows, GN>), grid, blk, 0, st, p, nwg8);    \
+    else hipLaunchKernelGGL((proj_gemv_kernel<NT, 1, kGemvRows, GN>), grid, blk, 0, st, p, nwg8);
+#define OMH_GEMV(NT)                                                                                              \
+    if (p.gssq) { OMH_GEMV_KS(NT, true) } else { OMH_GEMV_KS(NT, false) }
         switch (p.T) {
         case 1: OMH_GEMV(1) break;
         case 2: OMH_GEMV(2) break;
@@ -2237,6 +2272,7 @@ hipError_t launch_proj(const ProjArgs &p, hipStream_t st) {
         default: OMH_GEMV(4) break;
         }
 #undef OMH_GEMV
+#undef OMH_GEMV_KS
         return hipGetLastError();
     }
     // int8 rows on the bf16 matrix cores (bf16 x 3), the fp32 rows after

@@ -197,7 +197,8 @@ int decode_variant() {
 // out_proj scratch's bf16 planes and block sums (DecodeArgs::xb)
 int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv, const float *z,
                 int64_t ld_z, const float *a, const float *b, int64_t ld_ab, float *core,
-                hipStream_t st, uint16_t *planes = nullptr, int b0 = 0, bool planes_i8 = false) {
+                hipStream_t st, uint16_t *planes = nullptr, int b0 = 0, bool planes_i8 = false,
+                int variant_req = 0, float *ssq_out = nullptr) {
     if (nl < 1 || !lis) return fail(OMH_ERR_ARG, "decode_core: nl=%d", nl);
     for (int i = 0; i < nl; i++) {
         if (int rc = check_layer(lis[i])) return rc;
@@ -222,7 +223,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
     if (!aligned16(z) || !aligned16(core) || (ld_z % 4) != 0)
         return fail(OMH_ERR_ARG, "decode_core: z/core must be 16-byte aligned rows");
     const int vdim = L0.vdim;
-    const int variant = decode_variant();
+    const int variant = variant_req ? variant_req : decode_variant();
     // one layer's large batch as launches that each fit one round of
     // resident workgroups (one B = 64 launch at the 35B shape: 52.1 us;
     // two B = 32 launches: 2 x 23.7 us)
@@ -245,6 +246,7 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
             A.xb_T = B;
             A.xb_t0 = c0;
             A.b0 = b0 + c0;
+            A.ssq_out = ssq_out;
             for (int i = 0; i < n; i++) A.L[i] = ptrs(g_L[lis[l0 + i]]);
             HIP_OK(launch_decode_core(A, d.kd, d.vd, variant, st));
             for (int i = 0; i < n; i++) g_L[lis[l0 + i]].epoch ^= 1;
@@ -255,10 +257,11 @@ int decode_core(int nl, const int *lis, int B, const float *qkv, int64_t ld_qkv,
 
 // Scratch of one whole-layer decode call of B sequences, as byte offsets in
 // one region: the in_proj rows [B][in_rows] and core rows [B][vdim] (fp32),
-// then, for int8 rows with B > 4, the projections' bf16 planes, block sums,
+// the core slices' sums of squares [B][vh][slices] (deferred norm), then,
+// for int8 rows with B > 4, the projections' bf16 planes, block sums,
 // k-split partial tiles and arrival counters (proj_xb_bytes).
 struct DecodeScratch {
-    size_t in = 0, core = 0, xb = 0, xb_n = 0, total = 0;
+    size_t in = 0, core = 0, ssq = 0, xb = 0, xb_n = 0, total = 0;
 };
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
@@ -267,7 +270,8 @@ DecodeScratch decode_scratch(const DevLayer &L, int B) {
     DecodeScratch s;
     s.in = 0;
     s.core = align256((size_t)B * L.in_rows * sizeof(float));
-    s.xb = s.core + align256((size_t)B * L.vdim * sizeof(float));
+    s.ssq = s.core + align256((size_t)B * L.vdim * sizeof(float));
+    s.xb = s.ssq + align256((size_t)B * L.d.vh * kMaxSlices * sizeof(float));
     if (B > 4 && (L.in_nq > 0 || L.out_nq > 0))
         s.xb_n = std::max(proj_xb_bytes(B, L.d.hidden, L.in_nq), proj_xb_bytes(B, L.vdim, L.out_nq));
     s.total = s.xb + align256(s.xb_n);
@@ -299,15 +303,24 @@ int decode_full_on(int li, int B, const float *x, float *out, hipStream_t st, ch
     HIP_OK(launch_proj(p, st));
     const int vh = L.d.vh;
     const float *zz = in + L.conv_dim, *bb = zz + L.vdim, *aa = bb + vh;
-    // the core writes out_proj's bf16 planes itself, saving the split launch
+    // the core writes out_proj's bf16 planes itself, saving the split launch;
+    // at up to 4 tokens with int8 out_proj rows (the GEMV) the core runs as
+    // column slices that leave the gated norm's 1 / rms to the GEMV instead
     const bool i8 = proj_x_int8_planes(B, L.vdim, L.out_nq);
     uint16_t *planes = xb && L.out_nq > 0 && decode_planes_supported(L.d.vd, decode_variant(), i8) ? xb : nullptr;
-    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes, 0, i8))
+    const int defer = B <= 4 && L.out_nq == D && !planes && decode_variant() == 0 && L.d.kh * B < 256
+                          ? decode_deferred_slices(L.d.kd, L.d.vd) : 0;
+    float *ssq = defer ? reinterpret_cast<float *>(scr + ds.ssq) : nullptr;
+    if (int rc = decode_core(1, &li, B, in, L.in_rows, zz, L.in_rows, aa, bb, L.in_rows, core, st, planes, 0, i8,
+                             defer, ssq))
         return rc;
     ProjArgs q{};
     q.counters = cnt; q.ncounters = ncnt;
     q.x = core; q.ldx = L.vdim; q.y = out; q.ldy = D; q.xb = xb; q.xb_n = ds.xb_n; q.x_split = planes != nullptr;
     q.Q = L.Qout; q.Qt = L.Qtout; q.scale = L.Sout; q.W = L.Wout; q.T = B; q.I = L.vdim; q.O = D; q.n_q = L.out_nq;
+    if (defer) {
+        q.gssq = ssq; q.gvd = L.d.vd; q.geps = L.d.eps;
+    }
     HIP_OK(launch_proj(q, st));
     return OMH_OK;
 }

@@ -70,6 +70,9 @@ struct DecodeArgs {
     uint16_t *xb;       // or null; with nl = 1, the core output also as the out_proj scratch's x: bf16 planes and block sums (xpiece) or, with xb_i8, int8 planes and block scales (i8_off); I = vh*vd
     int xb_T, xb_t0;    // the planes' token count, and the planes' token of row 0 of this launch
     bool xb_i8;
+    float *ssq_out;     // or null; with 4 column slices and nl = 1: each slice writes o * gnorm * silu(z) of its
+                        // columns to core and its sum of squares of o to ssq_out[(b * vh + h) * 4 + slice]; the
+                        // norm's 1 / rms is left to the consumer (ProjArgs::gssq)
     LayerPtrs L[kMaxDecodeLayers];
 };
 
@@ -136,6 +139,13 @@ struct ProjArgs {
     int ncounters;         //   last arriver resets its own), so no launch has to clear them
     float *part;           // (set by launch_proj from xb)
     int *cnt;
+    // or null: x is a decode core's gated output before its 1 / rms (T <= 4
+    // tokens, int8 rows only), which the GEMV applies as it loads x: x_i * rn,
+    // rn = (sum of the head's 4 partial sums of squares in slice order / gvd
+    // + geps)^-1/2, partial (t, head, slice) at gssq[(t * (I / gvd) + head) * 4 + slice]
+    const float *gssq;
+    int gvd;
+    float geps;
 };
 // bytes of the scratch a projection of T tokens over I inputs into n_q int8 rows uses
 size_t proj_xb_bytes(int T, int I, int n_q);
@@ -224,5 +234,8 @@ bool decode_core_supported(int kd, int vd, int rep, int K);
 bool decode_planes_supported(int vd, int variant, bool i8);
 // sequences per launch for one layer's B sequences: B, or chunks that each fit one round of resident workgroups
 int decode_seqs_per_launch(int kd, int vd, int kh, int vh, int nl, int B, int variant);
+// column slices per value head for a launch whose gated norm is left to the
+// consumer (DecodeArgs::ssq_out), or 0 where the shape has no such form
+int decode_deferred_slices(int kd, int vd);
 
 }  // namespace omh

@@ -29,7 +29,8 @@ def _pair(d, seed, B, int8, li0):
 
 
 @pytest.mark.parametrize("d,int8,sizes", [
-    (Q35B, True, (64, 3)),        # split-queue in_proj, paired core in two launches, streaming out_proj; then the GEMV
+    (Q35B, True, (64, 3)),        # split-queue in_proj, paired core in two launches, streaming out_proj; then the GEMVs
+                                  # around a column-sliced core whose 1 / rms out_proj applies
     (Q35B, True, (17, 8)),        # partial token tiles (17 = 16 + 1), then a sliced-kernel core at B = 8
     (CFG1, False, (40, 1)),       # fp32 MFMA projections, then the GEMV
 ], ids=["35b-int8-64-3", "35b-int8-17-8", "cfg1-f32-40-1"])
