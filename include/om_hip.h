@@ -146,9 +146,8 @@ int omh_gdn_prefill_dev(int li, int seq, int T, const float *x, float *out, void
  * forbid hipMalloc.  Same computation and kernels as omh_gdn_decode_dev, but
  * its scratch (in_proj rows, core rows, the core slices' sums of squares,
  * the int8 projections' x planes, partial tiles and arrival counters) is one
- * static 8 MiB device buffer per
- * GPU, held until the process ends, instead of the library's grow-only
- * scratch.  A call whose scratch would exceed 8 MiB returns OMH_ERR_SHAPE
+ * static 8 MiB device buffer per GPU, held until the process ends, instead
+ * of the library's grow-only scratch.  A call whose scratch would exceed 8 MiB returns OMH_ERR_SHAPE
  * (35B-A3B GDN shape: up to B = 64 fits).  All calls on one GPU share that
  * buffer, so calls that may overlap in time (different streams) race:
  * issue them from one stream. */
