@@ -795,7 +795,13 @@ void attn_flash_kernel(const AttnArgs a) {
 template <int HD>
 struct Flash3Shape {
     static constexpr int KT = 32;                  // keys per tile
-    static constexpr int KLD = 2 * HD + 16;        // bytes of one bf16 K row
+    // bytes of one bf16 K row.  The padding sets the LDS bank conflicts of the
+    // 16-byte K reads (SQ_LDS_BANK_CONFLICT per T = 4096 dispatch at HD = 256):
+    // 270.5 M cycles unpadded, 67.6 M with 16 / 48 / 64 bytes, 33.8 M with 32
+    // or 96 bytes; 96 gave the fastest kernel (499-505 against 521-527 us
+    // under the counters, the fastest of seven calls 539 against 554 us);
+    // the two stages then take 156 KiB of LDS.
+    static constexpr int KLD = 2 * HD + 96;
     static constexpr int VLD = 2 * KT + 16;        // bytes of one bf16 V^T row
     static constexpr int KPL = KT * KLD, VPL = HD * VLD;
     static constexpr int STAGE = 2 * KPL + 2 * VPL;   // K hi, K lo, V^T hi, V^T lo
@@ -804,6 +810,7 @@ struct Flash3Shape {
     static constexpr int NJ = HD / 16;             // 16-dim output tiles
     static constexpr int PK = KT * HD / 4 / (8 * OMH_WAVE);         // K float4 pieces per thread
     static constexpr int PV = KT / 2 * HD / 4 / (8 * OMH_WAVE);     // V (key pair, 4 dims) units per thread
+    static_assert(LDS <= 160 * 1024 && KLD % 16 == 0 && VLD % 16 == 0, "two stages in a CU's LDS, 16-byte rows");
 };
 typedef __bf16 omh_v8bf __attribute__((ext_vector_type(8)));
 
