@@ -134,8 +134,10 @@ def test_35b_block_drop_in_small_batch(B, int8):
     """The engine's own call at the real shape: omh_gdn_decode(li, B, x, out)
     with the 35B-A3B GDN weights.  Up to 4 tokens the projections run on the
     register GEMV, whose k split is 2 for in_proj (I = 2048: 12288 int8 rows
-    plus 64 fp32 b/a rows in one launch) and 4 for out_proj (I = 4096).
-    Three tokens per sequence, each sequence against its own oracle run."""
+    plus 64 fp32 b/a rows in one launch) and 4 for out_proj (I = 4096); with
+    int8 rows the core runs as 4 column slices per value head and out_proj's
+    GEMV applies the gated norm's 1 / rms.  Three tokens per sequence, each
+    sequence against its own oracle run."""
     d = Q35B
     seed = 7100 + B + 10 * int8
     w = synth.layer_weights(d, seed, gnorm_std=0.1)
@@ -154,6 +156,48 @@ def test_35b_block_drop_in_small_batch(B, int8):
         # the history holds in_proj outputs: a floating-point result here
         assert_close(conv, cref, what=f"35B B={B} int8={int8} seq {s} conv")
     L.free()
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_35b_deferred_norm_matches_norm_in_core(B, monkeypatch):
+    """At up to 4 tokens with int8 out_proj rows the decode core runs as 4
+    column slices per value head, each writing o * gnorm * silu(z) and its
+    sum of squares of o, and out_proj's GEMV applies each head's 1 / rms as
+    it loads x.  With OMH_DECODE_KERNEL=sliced and OMH_DECODE_NCS=1 the same
+    call keeps one workgroup per value head with the whole gated norm in the
+    core.  Only the order of fp32 sums and products differs between the two,
+    so they agree far inside the oracle contract: outputs within 2e-5
+    relative, states and conv histories within 1e-5 (a head or slice mixed
+    up would be off by the norm itself)."""
+    d = Q35B
+    seed = 7150 + B
+    w = synth.layer_weights(d, seed, gnorm_std=0.1)
+    conv0, S0 = synth.states(d, seed, B=B)
+    La = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
+    Lb = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
+    try:
+        for s in range(B):
+            La.set_state(s, conv0[s], S0[s])
+            Lb.set_state(s, conv0[s], S0[s])
+        x = _x(d, seed, (3, B))
+        for t in range(3):
+            ya = La.decode(x[t])
+            monkeypatch.setenv("OMH_DECODE_KERNEL", "sliced")
+            monkeypatch.setenv("OMH_DECODE_NCS", "1")
+            yb = Lb.decode(x[t])
+            monkeypatch.delenv("OMH_DECODE_KERNEL")
+            monkeypatch.delenv("OMH_DECODE_NCS")
+            err = float(np.abs(ya - yb).max())
+            print(f"B={B} token {t}: max |deferred - in-core| = {err:.3g} (max |out| {float(np.abs(yb).max()):.3g})")
+            np.testing.assert_allclose(ya, yb, rtol=2e-5, atol=1e-6 * float(np.abs(yb).max()), err_msg=f"token {t}")
+        for s in range(B):
+            ca, Sa = La.get_state(s)
+            cb, Sb = Lb.get_state(s)
+            np.testing.assert_allclose(Sa, Sb, rtol=1e-5, atol=1e-6, err_msg=f"seq {s} S")
+            np.testing.assert_allclose(ca, cb, rtol=1e-5, atol=1e-6, err_msg=f"seq {s} conv")
+    finally:
+        La.free()
+        Lb.free()
 
 
 @pytest.mark.parametrize("T", [65, 128, 255, 256, 333, 1024])
