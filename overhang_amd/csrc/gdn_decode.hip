@@ -709,12 +709,14 @@ hipError_t launch_decode_core(const DecodeArgs &a, int kd, int vd, int variant, 
 
 // State snapshot / rollback: blockIdx.y = layer, one float4 of the S block
 // and of the conv ring per thread (HBM-bound, 2 x 2.2 MB per layer at the
-// 35B shape), and the ring phase by the first thread.
+// 35B shape), and the ring phase by the first thread.  Nontemporal loads and
+// stores: 30 layers of the 35B shape, 536 MB rotated, MI355X: 22.9 us
+// against 26.1 us with plain ones.
 __global__ __launch_bounds__(256) void state_copy_kernel(const StateCopyArgs c) {
     const int l = blockIdx.y;
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;   // one float4 of S and of the ring
-    if (i < c.n4) reinterpret_cast<float4 *>(c.S_dst[l])[i] = reinterpret_cast<const float4 *>(c.S_src[l])[i];
-    if (i < c.r4) reinterpret_cast<float4 *>(c.R_dst[l])[i] = reinterpret_cast<const float4 *>(c.R_src[l])[i];
+    if (i < c.n4) omh_st_stream(c.S_dst[l] + 4 * i, omh_ld_stream(c.S_src[l] + 4 * i));
+    if (i < c.r4) omh_st_stream(c.R_dst[l] + 4 * i, omh_ld_stream(c.R_src[l] + 4 * i));
     if (i == 0) *c.P_dst[l] = *c.P_src[l];
 }
 
