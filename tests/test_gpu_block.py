@@ -158,8 +158,10 @@ def test_35b_block_drop_in_small_batch(B, int8):
     L.free()
 
 
-@pytest.mark.parametrize("B", [1, 3])
-def test_35b_deferred_norm_matches_norm_in_core(B, monkeypatch):
+@pytest.mark.parametrize("shape,B", [(None, 1), (None, 2), (None, 3), (None, 4),
+                                     ((2, 4, 64, 64, 512), 1), ((2, 4, 64, 64, 512), 4)],
+                         ids=["35b-B1", "35b-B2", "35b-B3", "35b-B4", "d64-B1", "d64-B4"])
+def test_deferred_norm_matches_norm_in_core(shape, B, monkeypatch):
     """At up to 4 tokens with int8 out_proj rows the decode core runs as 4
     column slices per value head, each writing o * gnorm * silu(z) and its
     sum of squares of o, and out_proj's GEMV applies each head's 1 / rms as
@@ -168,9 +170,12 @@ def test_35b_deferred_norm_matches_norm_in_core(B, monkeypatch):
     core.  Only the order of fp32 sums and products differs between the two,
     so they agree far inside the oracle contract: outputs within 2e-5
     relative, states and conv histories within 1e-5 (a head or slice mixed
-    up would be off by the norm itself)."""
-    d = Q35B
-    seed = 7150 + B
+    up would be off by the norm itself).  Both are also held to the oracle.
+    The 35B shape (slices of 32 columns, out_proj k = 4096) and 64-wide
+    heads (slices of 16 columns: one GEMV input piece each)."""
+    from overhang_amd.dims import GdnDims
+    d = Q35B if shape is None else GdnDims(kh=shape[0], vh=shape[1], kd=shape[2], vd=shape[3], K=4, hidden=shape[4])
+    seed = 7150 + B + (0 if shape is None else 40)
     w = synth.layer_weights(d, seed, gnorm_std=0.1)
     conv0, S0 = synth.states(d, seed, B=B)
     La = gdn.GdnLayer(new_li(), d, w, max_seqs=B, int8=True)
@@ -179,8 +184,10 @@ def test_35b_deferred_norm_matches_norm_in_core(B, monkeypatch):
         for s in range(B):
             La.set_state(s, conv0[s], S0[s])
             Lb.set_state(s, conv0[s], S0[s])
-        x = _x(d, seed, (3, B))
-        for t in range(3):
+        T = 3
+        x = _x(d, seed, (T, B))
+        ya_all = []
+        for t in range(T):
             ya = La.decode(x[t])
             monkeypatch.setenv("OMH_DECODE_KERNEL", "sliced")
             monkeypatch.setenv("OMH_DECODE_NCS", "1")
@@ -188,13 +195,18 @@ def test_35b_deferred_norm_matches_norm_in_core(B, monkeypatch):
             monkeypatch.delenv("OMH_DECODE_KERNEL")
             monkeypatch.delenv("OMH_DECODE_NCS")
             err = float(np.abs(ya - yb).max())
-            print(f"B={B} token {t}: max |deferred - in-core| = {err:.3g} (max |out| {float(np.abs(yb).max()):.3g})")
+            print(f"{d.kd}/{d.vd} B={B} token {t}: max |deferred - in-core| = {err:.3g} (max |out| {float(np.abs(yb).max()):.3g})")
             np.testing.assert_allclose(ya, yb, rtol=2e-5, atol=1e-6 * float(np.abs(yb).max()), err_msg=f"token {t}")
+            ya_all.append(ya)
+        got = np.stack(ya_all, axis=1)                                    # [B][T][D]
         for s in range(B):
             ca, Sa = La.get_state(s)
             cb, Sb = Lb.get_state(s)
             np.testing.assert_allclose(Sa, Sb, rtol=1e-5, atol=1e-6, err_msg=f"seq {s} S")
             np.testing.assert_allclose(ca, cb, rtol=1e-5, atol=1e-6, err_msg=f"seq {s} conv")
+            ref, cref, Sref = oracle.layer_seq(d, w, x[:, s], conv0[s], S0[s], int8=True)
+            assert_close(got[s], ref, what=f"deferred {d.kd}/{d.vd} B={B} seq {s} out")
+            assert_close(Sa, Sref, what=f"deferred {d.kd}/{d.vd} B={B} seq {s} S")
     finally:
         La.free()
         Lb.free()
