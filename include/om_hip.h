@@ -121,7 +121,13 @@ int omh_gdn_decode_core(int li, int B, const float *qkv, const float *z,
 int omh_gdn_prefill_core(int li, int seq, int T, const float *qkv, const float *z,
                          const float *a, const float *b, float *core);
 
-/* ---- device-pointer, stream-ordered variants (asynchronous) ---- */
+/* ---- device-pointer, stream-ordered variants (asynchronous) ----
+ *
+ * They share the library's scratch and each layer's state with every other
+ * entry point: calls that may overlap in time must be issued on one stream.
+ * The host-pointer calls above run on a stream of the library's own and do
+ * not wait for work a caller enqueued on its streams; call omh_sync() on
+ * those streams first. */
 
 /* Core decode for nl layers at once (nl >= 1, all of identical dims), each
  * with B sequences: inputs [nl][B][...] and core [nl][B][vh*vd] in device
