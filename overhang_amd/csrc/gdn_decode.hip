@@ -91,11 +91,11 @@ constexpr bool slice_valid(int KD, int VD, int NCS) {
 }
 
 template <int C4>
-__device__ __forceinline__ float4 f4_xor_sum_from(float4 x) {
-    x.x = omh_xor_sum_from<C4>(x.x);
-    x.y = omh_xor_sum_from<C4>(x.y);
-    x.z = omh_xor_sum_from<C4>(x.z);
-    x.w = omh_xor_sum_from<C4>(x.w);
+__device__ __forceinline__ float4 f4_lane_sum_from(float4 x) {
+    x.x = omh_lane_sum_from<C4>(x.x);
+    x.y = omh_lane_sum_from<C4>(x.y);
+    x.z = omh_lane_sum_from<C4>(x.z);
+    x.w = omh_lane_sum_from<C4>(x.w);
     return x;
 }
 __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
@@ -105,8 +105,8 @@ __device__ __forceinline__ float4 f4_add(float4 a, float4 b) {
 // Sum two float4 over the row groups of the workgroup (red: [NW][2][C4]).
 template <int C4, int NW>
 __device__ __forceinline__ void colsum2(float4 &a, float4 &b, float4 (*red)[2][C4], int wave, int lane, int c4) {
-    a = f4_xor_sum_from<C4>(a);
-    b = f4_xor_sum_from<C4>(b);
+    a = f4_lane_sum_from<C4>(a);
+    b = f4_lane_sum_from<C4>(b);
     if constexpr (NW > 1) {
         if (lane < C4) { red[wave][0][c4] = a; red[wave][1][c4] = b; }
         omh_lds_barrier();
@@ -132,19 +132,22 @@ __device__ __forceinline__ float4 gated(float4 o, float rn, float4 gn, float4 zz
 // before them).  History is right-aligned: h[it][m] is the input
 // kConvRing-1-m tokens back, in ring slot (ph + 1 + m) mod kConvRing; the
 // taps are stored right-aligned the same way, so tap m multiplies h[m] and
-// the last tap the new input.
-template <int NIT>
+// the last tap the new input.  ALL: every ring slot is requested without
+// the phase (one slot more per channel), and pick() takes the history slots
+// out of them once the phase has arrived, so no load waits for the phase.
+template <int NIT, bool ALL = false>
 struct ConvIn {
     static constexpr int NH = kConvRing - 1;
     float x[NIT], h[NIT][NH];
+    float r[ALL ? NIT : 1][kConvRing];
     float4 w[NIT];
     int gch[NIT];
 
     // gch_of(c) maps the workgroup's channel c < nch to a global channel.
     // The loads are branch-free (out-of-range slots load channel 0 and are
-    // marked gch = -1; history slots a K < kConvRing kernel does not use
-    // repeat the first used slot's address), so the compiler's wait counts
-    // stay exact and no unused bytes are fetched.
+    // marked gch = -1; without ALL, history slots a K < kConvRing kernel
+    // does not use repeat the first used slot's address), so the compiler's
+    // wait counts stay exact and no unused bytes are fetched.
     template <typename F>
     __device__ __forceinline__ void load(F gch_of, int nch, int tid, int tpb, const float *qkv, const float *conv_w,
                                          const float *ring, int conv_dim, int seq, int ph, int K) {
@@ -157,9 +160,31 @@ struct ConvIn {
             x[it] = qkv[g];
             w[it] = *reinterpret_cast<const float4 *>(conv_w + (size_t)g * kConvRing);
             const float *rs = ring + ring_at(seq, 0, g, conv_dim);
+            if constexpr (ALL) {
 #pragma unroll
-            for (int m = 0; m < NH; m++)
-                h[it][m] = rs[(size_t)((ph + 1 + (m < m0 ? m0 : m)) & (kConvRing - 1)) * conv_dim];
+                for (int q = 0; q < kConvRing; q++) r[it][q] = rs[(size_t)q * conv_dim];
+            } else {
+#pragma unroll
+                for (int m = 0; m < NH; m++)
+                    h[it][m] = rs[(size_t)((ph + 1 + (m < m0 ? m0 : m)) & (kConvRing - 1)) * conv_dim];
+            }
+        }
+    }
+    // ALL: the history slots of phase ph (the same slots load() reads
+    // without ALL), by selects on the wave-uniform slot index.
+    __device__ __forceinline__ void pick(int ph, int K) {
+        static_assert(ALL, "pick() needs every slot loaded");
+        const int m0 = kConvRing - K;
+#pragma unroll
+        for (int m = 0; m < NH; m++) {
+            const int q = (ph + 1 + (m < m0 ? m0 : m)) & (kConvRing - 1);
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                float v = r[it][0];
+#pragma unroll
+                for (int qq = 1; qq < kConvRing; qq++) v = q == qq ? r[it][qq] : v;
+                h[it][m] = v;
+            }
         }
     }
     // conv1d + SiLU (op order as engines/qwen.c:311-319) of the it-th channel.
@@ -191,9 +216,9 @@ __device__ __forceinline__ void qk_factors(const float *s_q, const float *s_k, i
         sk += k * k;
         sqk += q * k;
     }
-    sq = omh_xor_sum_below<OMH_WAVE>(sq);
-    sk = omh_xor_sum_below<OMH_WAVE>(sk);
-    sqk = omh_xor_sum_below<OMH_WAVE>(sqk);
+    sq = omh_lane_sum_below<OMH_WAVE>(sq);
+    sk = omh_lane_sum_below<OMH_WAVE>(sk);
+    sqk = omh_lane_sum_below<OMH_WAVE>(sqk);
     rq = (1.f / sqrtf(sq + 1e-6f)) * (1.f / sqrtf((float)KD));
     rk = 1.f / sqrtf(sk + 1e-6f);
     kq = sqk * rq * rk;
@@ -333,7 +358,7 @@ __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *
     const float4 vv = *reinterpret_cast<const float4 *>(&s_v[c4 * 4]);
     const float4 o = delta_rule<KD, VD, Sh::RG, RPT, C4, Sh::NW>(s, Sp, s_q, s_k, vv, hc, red, wave, lane, c4, rg);
     float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
-    ss = omh_xor_sum_below<C4>(ss);
+    ss = omh_lane_sum_below<C4>(ss);
     if (rg == 0) {
         const float rn = 1.f / sqrtf(ss / (float)VD + eps);     // qwen.c:353-357
         const float4 zz = *reinterpret_cast<const float4 *>(&s_z[c4 * 4]);
@@ -478,6 +503,11 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     const LayerPtrs &L = args.L[l];
     float *const Sl = L.S;
     const int kh = args.kh, vh = args.vh, K = args.K, rep = args.rep;
+    // The argument block's other 64-byte lines (the input pointers', the
+    // layer's epoch) are requested in the same batch: read where first used,
+    // each line cost one more dependent round trip before the first load.
+    const float *const qkv_arg = args.qkv;
+    const int epoch = L.epoch, max_seqs = L.max_seqs;
     __builtin_amdgcn_sched_barrier(0);           // the state pointer is requested with the counts
     const int hk = h / rep;                      // key head of value head h (qwen.c:331, 335)
     const int key_dim = kh * KD, vdim = vh * VD, conv_dim = 2 * key_dim + vdim;
@@ -494,32 +524,40 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     __shared__ float4 s_red[NW][2][C4];
     __shared__ int s_last;
 
-    // (1) Prologue inputs first (see ConvIn): the q/k channels of key head
-    // hk (recomputed by every workgroup of the key head, appended by its
-    // first one) and this slice's value channels.
+    // (1) Every prologue request goes out before any of them is waited
+    // for: the q/k channels of key head hk (recomputed by every workgroup of
+    // the key head, appended by its first one) and this slice's value
+    // channels with all their ring slots (ConvIn ALL: the phase only picks
+    // among them afterwards), z and gnorm, then the gate inputs and the ring
+    // phase (wave-uniform loads, issued after the vector requests so that
+    // none of those waits for them), then the state slice.  With the ring
+    // loads behind the phase and the gate loads behind both, one layer at
+    // B = 1 waited for two more dependent round trips.
     constexpr int NIT = (2 * KD + CW + TPB - 1) / TPB;
-    const int ph = L.phase[L.epoch * L.max_seqs + seq];
-    const float *qkv = args.qkv + tok * args.ld_qkv;
-    ConvIn<NIT> cin;
+    const float *qkv = qkv_arg + tok * args.ld_qkv;
+    ConvIn<NIT, true> cin;
     cin.load([&](int c) {
                  return c < KD ? hk * KD + c
                                : (c < 2 * KD ? key_dim + hk * KD + (c - KD) : 2 * key_dim + h * VD + col0 + (c - 2 * KD));
              },
-             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, seq, ph, K);
+             2 * KD + CW, tid, TPB, qkv, L.conv_w, L.conv_st, conv_dim, seq, 0, K);
     const int t4 = tid < VD / 4 ? tid : 0;
     // z and gnorm of the columns this thread gates: the head's columns 4 t4
     // (norm here), or the slice's own columns (1 / rms left to the consumer)
     const int zc = args.ssq_out ? col0 + 4 * c4 : 4 * t4;
     const float4 zz = *reinterpret_cast<const float4 *>(args.z + tok * args.ld_z + (size_t)h * VD + zc);
     const float4 gn = *reinterpret_cast<const float4 *>(L.gnorm + zc);
+    __builtin_amdgcn_sched_barrier(0);
     const float ga = args.a[tok * args.ld_ab + h], gb = args.b[tok * args.ld_ab + h];
     const float galog = L.A_log[h], gdt = L.dt_bias[h];
+    const int ph = L.phase[epoch * max_seqs + seq];
 
     float4 s[RPT];
     const __amdgpu_buffer_rsrc_t rs = omh_rsrc(Sp, (KD * VD - col0) * 4);
 #pragma unroll
     for (int m = 0; m < RPT; m++) s[m] = omh_ld_stream_buf(rs, ((rg + RG * m) * VD + c4 * 4) * 4);
     __builtin_amdgcn_sched_barrier(0);           // keep prologue arithmetic after the state requests
+    cin.pick(ph, K);
 
     const bool own_qk = (h % rep == 0) && cs == 0;
 #pragma unroll
@@ -533,8 +571,9 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
         else s_v[c - 2 * KD] = y;
         if (own) cin.append(it, L.conv_st, conv_dim, seq, ph);
     }
-    if (tid == 0) {
-        // gates (qwen.c:337-338)
+    if (tid == TPB - OMH_WAVE) {
+        // gates (qwen.c:337-338), on the last wave: it converts the fewest
+        // channels above, so this serial chain overlaps the others' work
         const float g = -expf(galog) * omh_softplus(ga + gdt);
         s_gam = expf(g);
         s_beta = omh_sigmoid(gb);
@@ -552,7 +591,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
 
     // (4) gated RMSNorm over the head's vd columns (qwen.c:353-357)
     float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
-    ss = omh_xor_sum_below<C4>(ss);              // this slice's sum of squares
+    ss = omh_lane_sum_below<C4>(ss);              // this slice's sum of squares
     float *core = args.core + tok * vdim + (size_t)h * VD;
     if constexpr (NCS == 1) {
         if (rg == 0) {

@@ -38,6 +38,64 @@ __device__ __forceinline__ float omh_xor_sum_below(float v) {
     return v;
 }
 
+// Lane sums on the VALU: DPP row operations within a 16-lane row and
+// gfx950's permlane swaps across rows, instead of the LDS permutes that
+// __shfl_xor compiles to (each of those waits for an LDS round trip).
+// Layouts (checked on the device): quad_perm 0xB1 / 0x4E = lane ^ 1 / ^ 2;
+// row_ror:8 = lane ^ 8; row_ror:4 = lane - 4 within the row; row_half_mirror
+// = 7 - lane within 8; permlane16_swap / permlane32_swap of (v, v) return
+// v[lane & ~16], v[lane | 16] / v[lane & ~32], v[lane | 32].  Every lane of a
+// summed group gets the same bits: each step adds two values that the two
+// partner lanes hold identically (fp addition commutes).
+template <int CTRL>
+__device__ __forceinline__ float omh_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// The swap's two results pass through an empty asm that takes both in
+// registers of their own: used directly, this compiler gave both results
+// the first one's register (p[0] + p[1] became p[0] + p[0]; seen in the
+// generated code and on the device).
+__device__ __forceinline__ float omh_swap_add(unsigned a, unsigned b) {
+    asm("" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float omh_swap16_sum(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return omh_swap_add(p[0], p[1]);
+}
+__device__ __forceinline__ float omh_swap32_sum(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return omh_swap_add(p[0], p[1]);
+}
+// Sum over the lanes whose index differs in the bits [log2 LO, 6).
+template <int LO>
+__device__ __forceinline__ float omh_lane_sum_from(float v) {
+    static_assert(LO >= 1 && LO <= 32 && (LO & (LO - 1)) == 0, "lane group");
+    if constexpr (LO <= 1) v += omh_dpp<0xB1>(v);
+    if constexpr (LO <= 2) v += omh_dpp<0x4E>(v);
+    if constexpr (LO <= 8) v += omh_dpp<0x128>(v);
+    // lanes i and i ^ 8 now agree, so the rotation by 4 adds the other pair
+    // of the 4-lane group {i, i ^ 4, i ^ 8, i ^ 12}
+    if constexpr (LO <= 4) v += omh_dpp<0x124>(v);
+    if constexpr (LO <= 16) v = omh_swap16_sum(v);
+    return omh_swap32_sum(v);
+}
+// Sum over the lanes whose index differs in the bits [0, log2 HI).
+template <int HI>
+__device__ __forceinline__ float omh_lane_sum_below(float v) {
+    static_assert(HI >= 1 && HI <= OMH_WAVE && (HI & (HI - 1)) == 0, "lane group");
+    if constexpr (HI >= 2) v += omh_dpp<0xB1>(v);
+    if constexpr (HI >= 4) v += omh_dpp<0x4E>(v);
+    // the lanes of a quad now agree, so the mirror adds the other quad
+    if constexpr (HI >= 8) v += omh_dpp<0x141>(v);
+    if constexpr (HI >= 16) v += omh_dpp<0x128>(v);
+    if constexpr (HI >= 32) v = omh_swap16_sum(v);
+    if constexpr (HI >= 64) v = omh_swap32_sum(v);
+    return v;
+}
+
 // Sum over aligned groups of N = 1, 2 or 4 consecutive lanes (DPP quad
 // permutes: no LDS round trip).
 template <int N>
