@@ -141,13 +141,43 @@ __device__ __forceinline__ int gemv_row_of_lane(int lane) {
     const int b5 = (lane >> 5) & 1, b4 = (lane >> 4) & 1, b3 = (lane >> 3) & 1;
     return R == 8 ? 4 * b5 + 2 * b4 + b3 : (R == 4 ? 2 * b5 + b4 : (R == 2 ? b5 : 0));
 }
+// v of lane ^ OFF, on the VALU for OFF = 32 and 16 (permlane swaps; hi =
+// the lane's bit OFF), 8 (row_ror:8), 2 and 1 (quad perms).  The swaps'
+// results pass through an empty asm that keeps them in registers of their
+// own (this compiler otherwise gave both the first one's register).
+template <int OFF>
+__device__ __forceinline__ float gemv_xor(float v, bool hi) {
+    if constexpr (OFF == 32 || OFF == 16) {
+        const unsigned u = __builtin_bit_cast(unsigned, v);
+        unsigned a, b;
+        if constexpr (OFF == 32) {
+            const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+            a = p[0];
+            b = p[1];
+        } else {
+            const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            a = p[0];
+            b = p[1];
+        }
+        asm("" : "+v"(a), "+v"(b));
+        return __builtin_bit_cast(float, hi ? a : b);
+    } else if constexpr (OFF == 8) {
+        return omh_dpp<0x128>(v);
+    } else if constexpr (OFF == 2) {
+        return omh_dpp<0x4E>(v);
+    } else if constexpr (OFF == 1) {
+        return omh_dpp<0xB1>(v);
+    } else {
+        return __shfl_xor(v, OFF, OMH_WAVE);
+    }
+}
 // one halving exchange: lanes with hi keep the upper H values
 template <int OFF, int H>
 __device__ __forceinline__ void gemv_halve(float *c, bool hi) {
 #pragma unroll
     for (int i = 0; i < H; i++) {
         const float send = hi ? c[i] : c[i + H];
-        c[i] = (hi ? c[i + H] : c[i]) + __shfl_xor(send, OFF, OMH_WAVE);
+        c[i] = (hi ? c[i + H] : c[i]) + gemv_xor<OFF>(send, hi);
     }
 }
 template <int R>
@@ -161,9 +191,21 @@ __device__ __forceinline__ float sum_rows_over_lanes(const float (&v)[R], int la
     if constexpr (LG >= 1) gemv_halve<32, R / 2>(c, h5);
     if constexpr (LG >= 2) gemv_halve<16, R / 4>(c, h4);
     if constexpr (LG >= 3) gemv_halve<8, 1>(c, h3);
+    // the rest of the butterfly (offsets 32 >> LG .. 1), each step adding
+    // the partner's value in the same order as a plain xor butterfly
     float r = c[0];
-#pragma unroll
-    for (int off = 32 >> LG; off >= 1; off >>= 1) r += __shfl_xor(r, off, OMH_WAVE);
+    if constexpr (LG == 0) r += gemv_xor<32>(r, h5);
+    if constexpr (LG <= 1) r += gemv_xor<16>(r, h4);
+    if constexpr (LG <= 2) {
+        r += gemv_xor<8>(r, h3);
+        // lanes i and i ^ 8 now agree, so lane i - 4 (row_ror:4) holds the
+        // value of lane i ^ 4
+        r += omh_dpp<0x124>(r);
+    } else {
+        r += gemv_xor<4>(r, false);
+    }
+    r += gemv_xor<2>(r, false);
+    r += gemv_xor<1>(r, false);
     return r;
 }
 
@@ -311,9 +353,14 @@ __device__ __forceinline__ void gemv_f32_row(const ProjArgs &p, int row, int lan
     }
 #pragma unroll
     for (int t = 0; t < NT; t++) {
+        // the xor butterfly over offsets 32 .. 1 on the VALU (gemv_xor)
         float a = acc[t];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) a += __shfl_xor(a, off, OMH_WAVE);
+        a += gemv_xor<32>(a, lane & 32);
+        a += gemv_xor<16>(a, lane & 16);
+        a += gemv_xor<8>(a, false);
+        a += omh_dpp<0x124>(a);        // lane i - 4 holds lane i ^ 4's value once i and i ^ 8 agree
+        a += gemv_xor<2>(a, false);
+        a += gemv_xor<1>(a, false);
         if (lane == 0) p.y[(size_t)t * p.ldy + row] = a;
     }
 }
