@@ -47,11 +47,7 @@ struct AttnShape {
     static constexpr size_t LDS = (size_t)(kAttnMaxGroup * HD + KT * KS + KT * HD) * sizeof(float);
 };
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 1; off < OMH_WAVE; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, OMH_WAVE));
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return omh_lane_max(v); }
 
 // cos and sin of p * inv[j] for j < rot / 2 into LDS tables, by the threads
 // of a workgroup.  One out-of-line function computes them wherever a kernel
@@ -534,8 +530,7 @@ void attn_split_mfma_kernel(const AttnArgs a) {
             sc[r] = kb + 4 * g4 + r < k1 ? (sa[r] + sb[r]) * a.scale : -INFINITY;   // qwen.c:410-414
             mx = fmaxf(mx, sc[r]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        mx = omh_swap32_max(omh_swap16_max(mx));
         // online softmax (qwen.c:413 softmax_ over all keys, merged per block);
         // the block's first key is visible, so mn is finite
         const float mn = fmaxf(m, mx);
@@ -546,8 +541,7 @@ void attn_split_mfma_kernel(const AttnArgs a) {
             pr[r] = kb + 4 * g4 + r < k1 ? expf(sc[r] - mn) : 0.f;
             ps += pr[r];
         }
-        ps += __shfl_xor(ps, 16, OMH_WAVE);
-        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        ps = omh_swap32_sum(omh_swap16_sum(ps));
         l = l * corr + ps;
         m = mn;
         // the output rows are heads 4 g4 + r: their corrections from lanes 4 g4 + r
@@ -733,8 +727,7 @@ void attn_flash_kernel(const AttnArgs a) {
                 sc[n][i] = key <= kmax ? sc[n][i] * a.scale : -INFINITY;
                 mx = fmaxf(mx, sc[n][i]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        mx = omh_swap32_max(omh_swap16_max(mx));
         const float mn = fmaxf(m, mx);             // finite: key 0 is in every token's first tile
         const float corr = expf(m - mn);
         float ps = 0.f;
@@ -745,8 +738,7 @@ void attn_flash_kernel(const AttnArgs a) {
                 sc[n][i] = expf(sc[n][i] - mn);
                 ps += sc[n][i];
             }
-        ps += __shfl_xor(ps, 16, OMH_WAVE);
-        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        ps = omh_swap32_sum(omh_swap16_sum(ps));
         l = fmaf(l, corr, ps);
         m = mn;
         // O^T = corr O^T + V^T P^T (qwen.c:415-419)
@@ -940,8 +932,7 @@ void attn_flash3_kernel(const AttnArgs a) {
                 sc[n][i] = key <= kmax ? sc[n][i] * a.scale : -INFINITY;
                 mx = fmaxf(mx, sc[n][i]);
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, OMH_WAVE));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, OMH_WAVE));
+        mx = omh_swap32_max(omh_swap16_max(mx));
         const float mn = fmaxf(m, mx);             // finite: key 0 is in every token's first tile
         // e^(s - mn) as 2^((s - mn) log2 e) on the hardware exp2 (a masked
         // score, -inf, gives 0; the first tile's corr, 2^-inf, 0)
@@ -957,8 +948,7 @@ void attn_flash3_kernel(const AttnArgs a) {
                 ph[4 * n + i] = (__bf16)pv;
                 pl[4 * n + i] = (__bf16)bf16_rest(pv);
             }
-        ps += __shfl_xor(ps, 16, OMH_WAVE);
-        ps += __shfl_xor(ps, 32, OMH_WAVE);
+        ps = omh_swap32_sum(omh_swap16_sum(ps));
         l = fmaf(l, corr, ps);
         m = mn;
         // O^T = corr O^T + V^T P^T (qwen.c:415-419); the rescale only when a

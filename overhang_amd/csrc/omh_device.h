@@ -59,6 +59,22 @@ __device__ __forceinline__ float omh_swap_add(unsigned a, unsigned b) {
     asm("" : "+v"(a), "+v"(b));
     return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
+__device__ __forceinline__ float omh_swap_max(unsigned a, unsigned b) {
+    asm("" : "+v"(a), "+v"(b));
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+// v + (v of lane ^ 16) and the same for 32, max likewise: the operands a
+// plain xor exchange gives, in one order or the other (both operations commute)
+__device__ __forceinline__ float omh_swap16_max(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return omh_swap_max(p[0], p[1]);
+}
+__device__ __forceinline__ float omh_swap32_max(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return omh_swap_max(p[0], p[1]);
+}
 __device__ __forceinline__ float omh_swap16_sum(float v) {
     const unsigned u = __builtin_bit_cast(unsigned, v);
     const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
@@ -94,6 +110,17 @@ __device__ __forceinline__ float omh_lane_sum_below(float v) {
     if constexpr (HI >= 32) v = omh_swap16_sum(v);
     if constexpr (HI >= 64) v = omh_swap32_sum(v);
     return v;
+}
+
+// Maximum over all 64 lanes (every lane gets it; max is exact, so the
+// order does not matter).
+__device__ __forceinline__ float omh_lane_max(float v) {
+    v = fmaxf(v, omh_dpp<0xB1>(v));
+    v = fmaxf(v, omh_dpp<0x4E>(v));
+    v = fmaxf(v, omh_dpp<0x141>(v));
+    v = fmaxf(v, omh_dpp<0x128>(v));
+    v = omh_swap16_max(v);
+    return omh_swap32_max(v);
 }
 
 // Sum over aligned groups of N = 1, 2 or 4 consecutive lanes (DPP quad
