@@ -117,12 +117,17 @@ __device__ __forceinline__ void colsum2(float4 &a, float4 &b, float4 (*red)[2][C
     }
 }
 
+// FAST: the exp2 / reciprocal SiLU (omh_silu_fast) instead of the
+// correctly rounded one (see qk_factors)
+template <bool FAST>
+__device__ __forceinline__ float silu_of(float z) { return FAST ? omh_silu_fast(z) : omh_silu(z); }
+template <bool FAST>
 __device__ __forceinline__ float4 gated(float4 o, float rn, float4 gn, float4 zz) {
     float4 y;
-    y.x = o.x * rn * gn.x * omh_silu(zz.x);
-    y.y = o.y * rn * gn.y * omh_silu(zz.y);
-    y.z = o.z * rn * gn.z * omh_silu(zz.z);
-    y.w = o.w * rn * gn.w * omh_silu(zz.w);
+    y.x = o.x * rn * gn.x * silu_of<FAST>(zz.x);
+    y.y = o.y * rn * gn.y * silu_of<FAST>(zz.y);
+    y.z = o.z * rn * gn.z * silu_of<FAST>(zz.z);
+    y.w = o.w * rn * gn.w * silu_of<FAST>(zz.w);
     return y;
 }
 
@@ -188,6 +193,7 @@ struct ConvIn {
         }
     }
     // conv1d + SiLU (op order as engines/qwen.c:311-319) of the it-th channel.
+    template <bool FAST>
     __device__ __forceinline__ float conv(int it, int K) const {
         const float wt[kConvRing] = {w[it].x, w[it].y, w[it].z, w[it].w};
         float acc = 0.f;
@@ -195,7 +201,7 @@ struct ConvIn {
         for (int m = 0; m < NH; m++)
             if (m >= kConvRing - K) acc += wt[m] * h[it][m];
         acc += wt[kConvRing - 1] * x[it];
-        return omh_silu(acc);
+        return silu_of<FAST>(acc);
     }
     // Append the new input: it goes to the free slot of phase ph.
     __device__ __forceinline__ void append(int it, float *ring, int conv_dim, int seq, int ph) const {
@@ -206,7 +212,16 @@ struct ConvIn {
 // L2-norm factors of the raw conv outputs q~, k~ of a key head, computed by
 // every wave from LDS: rq = (|q~|^2 + 1e-6)^-1/2 kd^-1/2 (the q scale),
 // rk = (|k~|^2 + 1e-6)^-1/2, and kq = q^.k^ (qwen.c:153-157, 326-329).
-template <int KD>
+// FAST (the sliced kernel): the hardware reciprocal square root here and in
+// the gated norm, and the exp2 / reciprocal SiLU, each within a few ulp.  In
+// a small launch a workgroup's step is a chain of dependent instructions on
+// one wave per SIMD, and the correctly rounded forms are some 40
+// instructions each: 35B engine chain at B = 1 on MI355X 16.66 -> 16.20 us
+// per layer.  The paired kernel keeps the correctly rounded forms: its
+// 30-layer launch ran 22.8 -> 23.4 us with the fast ones (its workgroups'
+// state writes then start while others still read; mixing the two costs
+// HBM turnarounds).
+template <int KD, bool FAST>
 __device__ __forceinline__ void qk_factors(const float *s_q, const float *s_k, int lane, float &rq, float &rk,
                                            float &kq) {
     float sq = 0.f, sk = 0.f, sqk = 0.f;
@@ -219,8 +234,8 @@ __device__ __forceinline__ void qk_factors(const float *s_q, const float *s_k, i
     sq = omh_lane_sum_below<OMH_WAVE>(sq);
     sk = omh_lane_sum_below<OMH_WAVE>(sk);
     sqk = omh_lane_sum_below<OMH_WAVE>(sqk);
-    rq = (1.f / sqrtf(sq + 1e-6f)) * (1.f / sqrtf((float)KD));
-    rk = 1.f / sqrtf(sk + 1e-6f);
+    rq = (FAST ? rsqrtf(sq + 1e-6f) : 1.f / sqrtf(sq + 1e-6f)) * (1.f / sqrtf((float)KD));
+    rk = FAST ? rsqrtf(sk + 1e-6f) : 1.f / sqrtf(sk + 1e-6f);
     kq = sqk * rq * rk;
 }
 
@@ -362,7 +377,7 @@ __device__ __forceinline__ void paired_head(float4 (&s)[RPT], float *Sp, float *
     if (rg == 0) {
         const float rn = 1.f / sqrtf(ss / (float)VD + eps);     // qwen.c:353-357
         const float4 zz = *reinterpret_cast<const float4 *>(&s_z[c4 * 4]);
-        const float4 y = gated(o, rn, gn, zz);
+        const float4 y = gated<false>(o, rn, gn, zz);
         *reinterpret_cast<float4 *>(core + c4 * 4) = y;
         if constexpr (VD % 64 == 0)
             if (po.xb) write_x(po, tok, col0 + c4 * 4, c4, y);
@@ -442,7 +457,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     for (int it = 0; it < NIT; it++) {
         if (cin.gch[it] < 0) continue;
         const int c = tid + it * TPB;
-        const float y = cin.conv(it, K);
+        const float y = cin.template conv<false>(it, K);
         if (c < KD) s_q[c] = y;
         else if (c < 2 * KD) s_k[c - KD] = y;
         else s_v[c - 2 * KD] = y;
@@ -461,7 +476,7 @@ void gdn_decode_paired_kernel(const DecodeArgs args) {
     }
     omh_lds_barrier();
     HeadCoef hc;
-    qk_factors<KD>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
+    qk_factors<KD, false>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
 
     // (3)+(4) value heads in order; the next head's state is in flight while
     // the current one is reduced and written back.  Heads alternate between
@@ -564,7 +579,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     for (int it = 0; it < NIT; it++) {
         if (cin.gch[it] < 0) continue;
         const int c = tid + it * TPB;
-        const float y = cin.conv(it, K);
+        const float y = cin.template conv<true>(it, K);
         bool own = true;
         if (c < KD) { s_q[c] = y; own = own_qk; }
         else if (c < 2 * KD) { s_k[c - KD] = y; own = own_qk; }
@@ -580,7 +595,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     }
     omh_lds_barrier();
     HeadCoef hc;
-    qk_factors<KD>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
+    qk_factors<KD, true>(s_q, s_k, lane, hc.rq, hc.rk, hc.kq);
     hc.gam = s_gam;
     hc.beta = s_beta;
 
@@ -595,8 +610,8 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
     float *core = args.core + tok * vdim + (size_t)h * VD;
     if constexpr (NCS == 1) {
         if (rg == 0) {
-            const float rn = 1.f / sqrtf(ss / (float)VD + args.eps);
-            const float4 y = gated(o, rn, gn, zz);
+            const float rn = rsqrtf(ss / (float)VD + args.eps);
+            const float4 y = gated<true>(o, rn, gn, zz);
             *reinterpret_cast<float4 *>(core + c4 * 4) = y;
             if constexpr (VD % 64 == 0)
                 if (args.xb) write_x(PlaneOut{args.xb, args.xb_T, vdim, args.xb_i8}, args.xb_t0 + b, h * VD + c4 * 4, c4, y);
@@ -605,7 +620,7 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
         // Deferred norm: this slice's o * gnorm * silu(z) and its sum of
         // squares of o; the next launch (out_proj's GEMV) applies 1 / rms as
         // it loads them, so no slice waits for another.
-        if (rg == 0) *reinterpret_cast<float4 *>(core + col0 + c4 * 4) = gated(o, 1.f, gn, zz);
+        if (rg == 0) *reinterpret_cast<float4 *>(core + col0 + c4 * 4) = gated<true>(o, 1.f, gn, zz);
         if (tid == 0) args.ssq_out[(tok * vh + h) * NCS + cs] = ss;
     } else {
         // Cross-slice exchange with device-coherent (agent-scope) relaxed
@@ -634,14 +649,14 @@ void gdn_decode_core_kernel(const DecodeArgs args) {
 #pragma unroll
                 for (int k = 0; k < NCS; k++)
                     tot += __hip_atomic_load(L.ssq + hb * kMaxSlices + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float rn = 1.f / sqrtf(tot / (float)VD + args.eps);
+                const float rn = rsqrtf(tot / (float)VD + args.eps);
                 const float *src = L.o_raw + hb * VD + tid * 4;
                 float4 oo;
                 oo.x = __hip_atomic_load(src + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 oo.y = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 oo.z = __hip_atomic_load(src + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 oo.w = __hip_atomic_load(src + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *reinterpret_cast<float4 *>(core + tid * 4) = gated(oo, rn, gn, zz);
+                *reinterpret_cast<float4 *>(core + tid * 4) = gated<true>(oo, rn, gn, zz);
             }
             if (tid == 0) __hip_atomic_store(L.cnt + hb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

@@ -267,7 +267,7 @@ __device__ __forceinline__ void gemv_q8_rows(const ProjArgs &p, int r0, int ks, 
                     ss += sq[c][t].y;
                     ss += sq[c][t].z;
                     ss += sq[c][t].w;
-                    const float rn = 1.f / sqrtf(ss / (float)p.gvd + p.geps);
+                    const float rn = rsqrtf(ss / (float)p.gvd + p.geps);
 #pragma unroll
                     for (int e = 0; e < 16; e++) x[c][t][e] *= rn;
                 }
