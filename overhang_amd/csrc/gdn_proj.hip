@@ -1066,8 +1066,7 @@ void proj_split_i8_kernel(const float *__restrict__ x, int64_t ldx, int8_t *__re
         const float4 u = *reinterpret_cast<const float4 *>(xr + k);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
     }
-#pragma unroll
-    for (int off = 1; off < OMH_WAVE; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, OMH_WAVE));
+    m = omh_lane_max(m);
     if (threadIdx.x % OMH_WAVE == 0) s_m[threadIdx.x / OMH_WAVE] = m;
     __syncthreads();
     m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
@@ -1118,8 +1117,7 @@ void proj_split_i8_tile_kernel(const float *__restrict__ x, int64_t ldx, int8_t 
             const float4 v = *reinterpret_cast<const float4 *>(xr + k);
             m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
-#pragma unroll
-        for (int off = 1; off < OMH_WAVE; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, OMH_WAVE));
+        m = omh_lane_max(m);
         if (lane == 0) s_e[w] = omh_i8_exponent(m);
     }
     __syncthreads();
