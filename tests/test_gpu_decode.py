@@ -197,6 +197,45 @@ def test_argument_errors_are_reported():
     L.free()
 
 
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("form", ["auto", "paired", "sliced1", "sliced4"])
+def test_conv_widths_every_kernel(K, form, monkeypatch):
+    """Conv widths 2-4 through every decode kernel, two sequences, seven
+    steps each (the ring of four slots wraps), after a prefill of 5 tokens
+    that leaves the ring at a phase other than 0: outputs, state and conv
+    history against the oracle.  The sliced kernel requests every ring slot
+    and picks the history slots by the phase afterwards; the paired kernel
+    requests only the history slots."""
+    for k in ("OMH_DECODE_KERNEL", "OMH_DECODE_NCS"):
+        monkeypatch.delenv(k, raising=False)
+    if form != "auto":
+        monkeypatch.setenv("OMH_DECODE_KERNEL", "paired" if form == "paired" else "sliced")
+        if form != "paired":
+            monkeypatch.setenv("OMH_DECODE_NCS", form[-1])
+    d = GdnDims(2, 4, 32, 32, K, 0)
+    seed = 500 + 10 * K + len(form)
+    w = synth.layer_weights(d, seed, gnorm_std=0.2, projections=False)
+    conv0, S0 = synth.states(d, seed, B=2)
+    L = gdn.GdnLayer(new_li(), d, w, max_seqs=2)
+    for s_ in range(2):
+        L.set_state(s_, conv0[s_], S0[s_])
+    pre = synth.core_inputs(d, 5, seed + 1)
+    L.prefill_core(0, pre["qkv"], pre["z"], pre["a"], pre["b"])
+    _, c0, s0 = oracle.core_seq(d, w, pre["qkv"], pre["z"], pre["a"], pre["b"], conv0[0], S0[0])
+    T = 7
+    inp = synth.core_inputs(d, T, seed + 2, B=2)
+    got = np.stack([L.decode_core(inp["qkv"][:, t], inp["z"][:, t], inp["a"][:, t], inp["b"][:, t])
+                    for t in range(T)], axis=1)
+    for s_, (cs, ss) in enumerate([(c0, s0), (conv0[1], S0[1])]):
+        ref, cref, Sref = oracle.core_seq(d, w, inp["qkv"][s_], inp["z"][s_], inp["a"][s_], inp["b"][s_], cs, ss)
+        conv, S = L.get_state(s_)
+        what = f"K={K} {form} seq{s_}"
+        assert_close(got[s_], ref, what=what + " core")
+        assert_close(S, Sref, what=what + " S")
+        assert np.array_equal(conv, cref), what + ": conv history is a copy of the inputs"
+    L.free()
+
+
 @pytest.mark.parametrize("ncs", [1, 2, 4, 8])
 def test_column_slices_agree_with_oracle(ncs, monkeypatch):
     """Every column-slice count (incl. the cross-slice gated-norm epilogue)."""
