@@ -38,19 +38,22 @@
 //    result does not depend on arrival order.
 //
 // Conv history lives in a per-channel ring (omh_internal.h): readers use
-// the K-1 history slots, the single owner of a channel writes the new input
-// into the free slot.
+// the K-1 history slots (the sliced kernel requests every slot and picks by
+// the phase once it arrives), the single owner of a channel writes the new
+// input into the free slot.
 //
-// When the step feeds an int8 out_proj, the epilogue also writes the gated
-// output as that projection's exact bf16 x 3 planes and 64-wide block sums
-// (write_planes), so the projection needs no split launch.  A launch covers
+// When the step feeds an int8 out_proj of more than 4 tokens, the epilogue
+// also writes the gated output as that projection's x planes (int8 x 3 with
+// a scale per 128-wide block, or exact bf16 x 3 with 64-wide block sums;
+// write_x), so the projection needs no split launch.  A launch covers
 // sequences b0 .. b0+B-1; the host runs one layer's large batch as several
 // launches that each fit one round of resident workgroups.
 //
 // Thread layout: TPB threads hold RPT rows x 4 adjacent columns (a float4)
 // of a head (or slice); a wavefront's loads cover whole consecutive row
 // segments.  Column sums over rows are butterflies across the row groups of
-// a wave, then across waves through LDS.
+// a wave (DPP row operations and permlane swaps, omh_lane_sum_from), then
+// across waves through LDS.
 #include "omh_device.h"
 #include "omh_internal.h"
 
