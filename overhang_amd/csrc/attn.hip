@@ -645,6 +645,14 @@ bool flash_fp32() {
     const char *e = getenv("OMH_ATTN_FLASH");
     return e && e[0] == 'f';
 }
+// the bf16 x 3 kernel converting every tile itself instead of copying tile
+// images (OMH_ATTN_FLASH=reg, for comparison)
+bool flash_reg() {
+    const char *e = getenv("OMH_ATTN_FLASH");
+    return e && e[0] == 'r';
+}
+// prompt steps of at least this many tokens stage their tiles from images
+constexpr int kFlashImageMinT = 256;
 
 template <int HD>
 __global__ __launch_bounds__(8 * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -811,11 +819,85 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
 }
 __device__ __forceinline__ float bf16_rest(float x) { return x - (float)(__bf16)x; }
 
+// One 32-key tile of K and V on its way to the flash kernel's LDS image: the
+// fp32 rows of keys kt .. kt + 31 (past nkeys, the tile's first row again)
+// into registers (load), then as bf16 hi / lo planes, K by rows and V
+// transposed, in the Flash3Shape stage layout (put: to an LDS stage, or to
+// a tile image in memory that the kernel later copies into LDS whole).
 template <int HD>
+struct Flash3Tile {
+    using F = Flash3Shape<HD>;
+    static constexpr int KT = F::KT, KLD = F::KLD, VLD = F::VLD, NT = 8 * OMH_WAVE;
+    omh_v4f kr[F::PK], vr[F::PV][2];
+    // V unit e: the key pair at V^T positions 2 pp, 2 pp + 1 (pp = e % 16) for
+    // head dims 4 c .. 4 c + 3 (c = e / 16), so the 16 lanes of a position
+    // pair sweep write one 64-byte run of a V^T row: no bank conflicts.
+    // Position 8 g + j holds key 16 (j / 4) + 4 g + j % 4.
+    static __device__ __forceinline__ int vkey(int pp) {
+        const int pos = 2 * pp, g8 = pos / 8, j = pos % 8;
+        return 16 * (j / 4) + 4 * g8 + j % 4;
+    }
+    __device__ __forceinline__ void load(const float *Kg, const float *Vg, int kt, int nkeys, int tid) {
+        auto key_of = [&](int kk) { return (size_t)(kt + kk < nkeys ? kt + kk : kt); };
+#pragma unroll
+        for (int i = 0; i < F::PK; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + key_of(kk) * HD + 4 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < F::PV; i++) {
+            const int e = tid + NT * i, k0 = vkey(e % 16), c = e / 16;
+            vr[i][0] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(k0) * HD + 4 * c);
+            vr[i][1] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(k0 + 1) * HD + 4 * c);
+        }
+    }
+    __device__ __forceinline__ void put(unsigned char *st, int tid) const {
+        unsigned char *Kh = st, *Kl = st + F::KPL, *Vh = st + 2 * F::KPL, *Vl = Vh + F::VPL;
+#pragma unroll
+        for (int i = 0; i < F::PK; i++) {
+            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
+            const omh_v4f x = kr[i];
+            uint2 hi, lo;
+            hi.x = bf16_pair(x[0], x[1]);
+            hi.y = bf16_pair(x[2], x[3]);
+            lo.x = bf16_pair(bf16_rest(x[0]), bf16_rest(x[1]));
+            lo.y = bf16_pair(bf16_rest(x[2]), bf16_rest(x[3]));
+            *reinterpret_cast<uint2 *>(Kh + kk * KLD + 8 * c) = hi;
+            *reinterpret_cast<uint2 *>(Kl + kk * KLD + 8 * c) = lo;
+        }
+#pragma unroll
+        for (int i = 0; i < F::PV; i++) {
+            const int e = tid + NT * i, pos = 2 * (e % 16), c = e / 16;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const float x0 = vr[i][0][d], x1 = vr[i][1][d];
+                *reinterpret_cast<uint32_t *>(Vh + (4 * c + d) * VLD + 2 * pos) = bf16_pair(x0, x1);
+                *reinterpret_cast<uint32_t *>(Vl + (4 * c + d) * VLD + 2 * pos) = bf16_pair(bf16_rest(x0), bf16_rest(x1));
+            }
+        }
+    }
+};
+
+// The tile images of keys 0 .. pos + T - 1 of the step's sequence, one
+// workgroup per (kv head, tile): image (g, i) at a.img + (g * a.img_tiles +
+// i) * STAGE holds exactly what attn_flash3_kernel stages in LDS for tile i.
+template <int HD>
+__global__ __launch_bounds__(8 * OMH_WAVE) void attn_tile_image_kernel(const AttnArgs a) {
+    using F = Flash3Shape<HD>;
+    const int g = blockIdx.x % a.KV, ti = blockIdx.x / a.KV;
+    const size_t cache0 = ((size_t)a.seq * a.KV + g) * a.max_t;
+    Flash3Tile<HD> t;
+    t.load(a.Kc + cache0 * HD, a.Vc + cache0 * HD, ti * F::KT, a.pos + a.T, threadIdx.x);
+    t.put(a.img + ((size_t)g * a.img_tiles + ti) * F::STAGE, threadIdx.x);
+}
+
+// IMG: each tile goes from its image (attn_tile_image_kernel) into LDS as
+// whole 1 KiB runs (buffer loads to LDS), with no conversion in the kernel.
+template <int HD, bool IMG>
 __global__ __launch_bounds__(8 * OMH_WAVE) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_flash3_kernel(const AttnArgs a) {
     using F = Flash3Shape<HD>;
-    constexpr int KT = F::KT, KLD = F::KLD, VLD = F::VLD, NS = F::NS, NJ = F::NJ, NT = 8 * OMH_WAVE;
+    constexpr int KT = F::KT, KLD = F::KLD, VLD = F::VLD, NS = F::NS, NJ = F::NJ;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem3[];
     const int H = a.H, KV = a.KV, grp = H / KV;
     const int nunit = (a.T + 15) / 16 * grp, wpg = (nunit + 7) / 8;
@@ -849,62 +931,44 @@ void attn_flash3_kernel(const AttnArgs a) {
     }
     const size_t cache0 = ((size_t)a.seq * KV + g) * a.max_t;
     const float *Kg = a.Kc + cache0 * HD, *Vg = a.Vc + cache0 * HD;
-    omh_v4f kr[F::PK], vr[F::PV][2];
-    auto key_of = [&](int kt, int kk) { return (size_t)(kt + kk < nkeys ? kt + kk : kt); };
-    // V unit e: the key pair at V^T positions 2 pp, 2 pp + 1 (pp = e % 16) for
-    // head dims 4 c .. 4 c + 3 (c = e / 16), so the 16 lanes of a position
-    // pair sweep write one 64-byte run of a V^T row: no bank conflicts.
-    // Position 8 g + j holds key 16 (j / 4) + 4 g + j % 4.
-    auto vkey = [](int pp) { const int pos = 2 * pp, g8 = pos / 8, j = pos % 8; return 16 * (j / 4) + 4 * g8 + j % 4; };
-    auto load = [&](int kt) __attribute__((always_inline)) {
+    Flash3Tile<HD> tile;
+    // IMG: kv head g's tile images, F::STAGE bytes (whole 1 KiB runs) each
+    static_assert(F::STAGE % 1024 == 0, "an image tile is whole 1 KiB runs");
+    constexpr int NCH = F::STAGE / 1024;
+    const __amdgpu_buffer_rsrc_t irs =
+        omh_rsrc(IMG ? a.img + (size_t)g * a.img_tiles * F::STAGE : a.img, IMG ? a.img_tiles * F::STAGE : 0);
+    auto copy = [&](int kt, int stage) __attribute__((always_inline)) {
+        unsigned char *dst = smem3 + stage * F::STAGE;
+        const int src = kt / KT * F::STAGE;
 #pragma unroll
-        for (int i = 0; i < F::PK; i++) {
-            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
-            kr[i] = *reinterpret_cast<const omh_v4f *>(Kg + key_of(kt, kk) * HD + 4 * c);
-        }
-#pragma unroll
-        for (int i = 0; i < F::PV; i++) {
-            const int e = tid + NT * i, k0 = vkey(e % 16), c = e / 16;
-            vr[i][0] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, k0) * HD + 4 * c);
-            vr[i][1] = *reinterpret_cast<const omh_v4f *>(Vg + key_of(kt, k0 + 1) * HD + 4 * c);
+        for (int i = 0; i < (NCH + 7) / 8; i++) {
+            const int c = w + 8 * i;
+            if (c < NCH)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(irs, (__attribute__((address_space(3))) void *)(dst + c * 1024),
+                                                         16, 16 * lane, src + c * 1024, 0, 0);
         }
     };
-    auto put = [&](int stage) __attribute__((always_inline)) {
-        unsigned char *st = smem3 + stage * F::STAGE;
-        unsigned char *Kh = st, *Kl = st + F::KPL, *Vh = st + 2 * F::KPL, *Vl = Vh + F::VPL;
-#pragma unroll
-        for (int i = 0; i < F::PK; i++) {
-            const int e = tid + NT * i, kk = e / (HD / 4), c = e % (HD / 4);
-            const omh_v4f x = kr[i];
-            uint2 hi, lo;
-            hi.x = bf16_pair(x[0], x[1]);
-            hi.y = bf16_pair(x[2], x[3]);
-            lo.x = bf16_pair(bf16_rest(x[0]), bf16_rest(x[1]));
-            lo.y = bf16_pair(bf16_rest(x[2]), bf16_rest(x[3]));
-            *reinterpret_cast<uint2 *>(Kh + kk * KLD + 8 * c) = hi;
-            *reinterpret_cast<uint2 *>(Kl + kk * KLD + 8 * c) = lo;
-        }
-#pragma unroll
-        for (int i = 0; i < F::PV; i++) {
-            const int e = tid + NT * i, pos = 2 * (e % 16), c = e / 16;
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const float x0 = vr[i][0][d], x1 = vr[i][1][d];
-                *reinterpret_cast<uint32_t *>(Vh + (4 * c + d) * VLD + 2 * pos) = bf16_pair(x0, x1);
-                *reinterpret_cast<uint32_t *>(Vl + (4 * c + d) * VLD + 2 * pos) = bf16_pair(bf16_rest(x0), bf16_rest(x1));
-            }
-        }
-    };
+    auto load = [&](int kt) __attribute__((always_inline)) { tile.load(Kg, Vg, kt, nkeys, tid); };
+    auto put = [&](int stage) __attribute__((always_inline)) { tile.put(smem3 + stage * F::STAGE, tid); };
 
     omh_v4f o[NJ];                                 // O^T: o[j][i] = O[token tq][dim 16 j + 4 gq + i]
 #pragma unroll
     for (int j = 0; j < NJ; j++) o[j] = omh_v4f{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
-    load(0);
-    put(0);
+    if constexpr (IMG) {
+        copy(0, 0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);     // vmcnt(0): this wave's copies have landed
+    } else {
+        load(0);
+        put(0);
+    }
     __syncthreads();
     for (int kt = 0, st = 0; kt < nkeys; kt += KT, st ^= 1) {
-        if (kt + KT < nkeys) load(kt + KT);
+        // (stage st ^ 1 was last read before the barrier that ended the previous step)
+        if (kt + KT < nkeys) {
+            if constexpr (IMG) copy(kt + KT, st ^ 1);
+            else load(kt + KT);
+        }
         const unsigned char *sb = smem3 + st * F::STAGE;
         const unsigned char *Kh = sb, *Kl = sb + F::KPL, *Vh = sb + 2 * F::KPL, *Vl = Vh + F::VPL;
         // S^T for keys kt + 16 n + 4 gq + i (register i of sc[n]), query row tq
@@ -965,7 +1029,8 @@ void attn_flash3_kernel(const AttnArgs a) {
             o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[j], 0, 0, 0);
             o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[j], 0, 0, 0);
         }
-        if (kt + KT < nkeys) put(st ^ 1);
+        if constexpr (IMG) __builtin_amdgcn_s_waitcnt(0x0f70);
+        else if (kt + KT < nkeys) put(st ^ 1);
         __syncthreads();
     }
     // normalise and gate (qwen.c:420-421)
@@ -1058,11 +1123,22 @@ hipError_t launch_attn_d(const AttnArgs &a, hipStream_t st) {
                 if (!ok) return hipErrorInvalidValue;
                 hipLaunchKernelGGL((attn_flash_kernel<HD>), grid, blk, FlashShape<HD>::LDS, st, a);
             } else {
-                static const bool ok = hipFuncSetAttribute((const void *)attn_flash3_kernel<HD>,
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                           (int)Flash3Shape<HD>::LDS) == hipSuccess;
+                static const bool ok =
+                    hipFuncSetAttribute((const void *)attn_flash3_kernel<HD, false>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)Flash3Shape<HD>::LDS) == hipSuccess &&
+                    hipFuncSetAttribute((const void *)attn_flash3_kernel<HD, true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)Flash3Shape<HD>::LDS) == hipSuccess;
                 if (!ok) return hipErrorInvalidValue;
-                hipLaunchKernelGGL((attn_flash3_kernel<HD>), grid, blk, Flash3Shape<HD>::LDS, st, a);
+                if (a.img) {
+                    // the images of every tile of keys 0 .. pos + T - 1, then the kernel copying them
+                    const long tiles = ((long)a.pos + a.T + Flash3Shape<HD>::KT - 1) / Flash3Shape<HD>::KT;
+                    if (a.img_tiles != tiles || (size_t)tiles * Flash3Shape<HD>::STAGE > (size_t)INT32_MAX)
+                        return hipErrorInvalidValue;
+                    hipLaunchKernelGGL((attn_tile_image_kernel<HD>), dim3((unsigned)(a.KV * tiles)), blk, 0, st, a);
+                    hipLaunchKernelGGL((attn_flash3_kernel<HD, true>), grid, blk, Flash3Shape<HD>::LDS, st, a);
+                } else {
+                    hipLaunchKernelGGL((attn_flash3_kernel<HD, false>), grid, blk, Flash3Shape<HD>::LDS, st, a);
+                }
             }
             return hipGetLastError();
         }
@@ -1105,6 +1181,23 @@ bool attn_uses_flash(int T, int hd) {
     if (const char *e = getenv("OMH_ATTN_FLASH"))
         if (e[0] == '0') return false;
     return T >= kFlashMinT && (hd == 128 || hd == 256);
+}
+
+template <int HD>
+size_t flash_image_bytes_d(int KV, int pos, int T, int *tiles) {
+    using F = Flash3Shape<HD>;
+    const size_t n = ((size_t)pos + T + F::KT - 1) / F::KT;
+    // one kv head's images are addressed with 32-bit buffer offsets: longer
+    // steps stage their tiles in the kernel
+    if (n * F::STAGE > (size_t)INT32_MAX) return 0;
+    *tiles = (int)n;
+    return (size_t)KV * n * F::STAGE;
+}
+
+size_t attn_flash_image_bytes(int hd, int KV, int pos, int T, int *tiles) {
+    *tiles = 0;
+    if (!attn_uses_flash(T, hd) || T < kFlashImageMinT || flash_fp32() || flash_reg()) return 0;
+    return hd == 256 ? flash_image_bytes_d<256>(KV, pos, T, tiles) : flash_image_bytes_d<128>(KV, pos, T, tiles);
 }
 
 bool attn_supported(int hd, int H, int KV, int rot) {

@@ -433,7 +433,7 @@ struct AttnLayer {
     float *Kc = nullptr, *Vc = nullptr;
 };
 AttnLayer g_A[kMaxLayers];
-Scratch g_arow, g_aqb, g_actx, g_apo, g_apml;
+Scratch g_arow, g_aqb, g_actx, g_apo, g_apml, g_aimg;
 
 void free_attn(AttnLayer &A) {
     void *ps[] = {A.Qin, A.Sin, A.Win, A.Qout, A.Sout, A.Wout, A.Qtin, A.Qtout, A.qn, A.kn, A.inv, A.Kc, A.Vc};
@@ -473,6 +473,10 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
         if (int rc = ensure(g_xb, xbn)) return rc;
         xb = static_cast<uint16_t *>(g_xb.p);
     }
+    int img_tiles = 0;
+    const size_t imgn = attn_flash_image_bytes(hd, d.n_kv, pos, T, &img_tiles);
+    if (imgn)
+        if (int rc = ensure(g_aimg, imgn)) return rc;
     float *rowb = static_cast<float *>(g_arow.p), *ctx = static_cast<float *>(g_actx.p);
     ProjArgs p{};
     p.counters = g_counters; p.ncounters = kCounters;
@@ -490,6 +494,8 @@ int attn_forward(int li, int seq, int pos, int T, const float *x, float *out, hi
     a.ns = ns; a.kps = kps;
     a.eps = d.eps;
     a.scale = 1.f / sqrtf((float)hd);                // qwen.c:405
+    a.img = imgn ? static_cast<unsigned char *>(g_aimg.p) : nullptr;
+    a.img_tiles = img_tiles;
     HIP_OK(launch_attn(a, hd, st));
     ProjArgs q{};
     q.counters = g_counters; q.ncounters = kCounters;

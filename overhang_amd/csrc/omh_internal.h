@@ -215,8 +215,14 @@ struct AttnArgs {
     int seq, pos, T, H, KV, rot, max_t;
     int ns, kps;                       // key splits and keys per split (attn_plan)
     float eps, scale;                  // RMSNorm eps, hd^-1/2
+    unsigned char *img;                // or null: the bf16 x 3 flash kernel's tile images [KV][img_tiles][stage]
+    int img_tiles;                     //   (attn_flash_image_bytes), made in the same call from the cache
 };
 bool attn_supported(int hd, int H, int KV, int rot);
+// bytes of the tile images a prompt step of T tokens at position pos takes
+// (keys 0 .. pos + T - 1 of each kv head; *tiles = tiles per kv head), or 0
+// (*tiles = 0) where its flash kernel stages tiles itself
+size_t attn_flash_image_bytes(int hd, int KV, int pos, int T, int *tiles);
 // whether a prompt step of T tokens runs on the flash kernel (no split partials)
 bool attn_uses_flash(int T, int hd);
 // splits for pos + T visible keys: ns * KV * T >= 256 workgroups where the keys allow

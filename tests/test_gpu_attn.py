@@ -270,6 +270,37 @@ def test_flash_bf16x3_matches_fp32_products(monkeypatch):
     assert_close(outs["bf16x3"], outs["fp32"], atol=2e-5, rtol=2e-4, what="flash bf16x3 vs fp32")
 
 
+@pytest.mark.parametrize("shape,steps", [(Q35B_ATTN, [300]), (Q35B_ATTN, [37, 300]), ((512, 16, 1, 128, 128), [257])],
+                         ids=["35b-T300", "35b-pos37-T300", "hd128-T257"])
+def test_flash_tile_images_match_tiles_staged_in_kernel(shape, steps, monkeypatch):
+    """Prompt steps of 256 tokens and more stage the bf16 x 3 flash kernel's
+    tiles from images made once per call (attn_tile_image_kernel); the
+    kernel converting every tile itself (OMH_ATTN_FLASH=reg) must give the
+    same outputs and cache rows bit for bit: masked keys contribute exactly
+    zero either way."""
+    D, H, KV, hd, rot = shape
+    rng = np.random.default_rng(31)
+    w = _weights(rng, D, H, KV, hd)
+    total = sum(steps)
+    xs = [rng.normal(0, 1, (T, D)).astype(np.float32) for T in steps]
+    res = {}
+    for mode in ("reg", "img"):
+        monkeypatch.delenv("OMH_ATTN_FLASH", raising=False)
+        if mode == "reg":
+            monkeypatch.setenv("OMH_ATTN_FLASH", "reg")
+        L = gdn.AttnLayer(new_li(), D, H, KV, hd, rot, 1e7, 1e-6, total, w)
+        try:
+            pos, outs = 0, []
+            for x in xs:
+                outs.append(L.forward(0, pos, x))
+                pos += x.shape[0]
+            res[mode] = (np.concatenate(outs), L.cache_get(0, 0, total))
+        finally:
+            L.free()
+    assert np.array_equal(res["img"][0], res["reg"][0]), "outputs differ"
+    assert np.array_equal(res["img"][1][0], res["reg"][1][0]) and np.array_equal(res["img"][1][1], res["reg"][1][1])
+
+
 @pytest.mark.parametrize("shape", [Q35B_ATTN, (256, 8, 8, 32, 32), (512, 16, 1, 128, 128), (1024, 4, 4, 256, 256)],
                          ids=["35b", "hd32-grp1", "hd128-grp16", "hd256-fullrope"])
 def test_decode_prep_in_split_kernel_matches_prep_launch(shape, monkeypatch):
