@@ -65,7 +65,9 @@ __device__ __forceinline__ void rope_table(const AttnArgs &a, int p, float *cs, 
 // into an LDS row (the RoPE pairs are read back from it).  cs_t / sn_t: the
 // token's rope_table.  prep_row_regs takes the row (v, element lane + 64 i
 // in v[i]) and the weights (wv, likewise) already in registers, so a caller
-// can issue those loads ahead of others; prep_row loads them itself.
+// can issue those loads ahead of others; prep_row loads them itself.  On
+// return v holds the row as written (its fences order LDS only, so global
+// loads a caller issued ahead stay in flight).
 template <int HD>
 __device__ __forceinline__ void prep_row_regs(const AttnArgs &a, float (&v)[(HD + OMH_WAVE - 1) / OMH_WAVE],
                                               const float (&wv)[(HD + OMH_WAVE - 1) / OMH_WAVE], bool norm, float *row,
@@ -85,7 +87,7 @@ __device__ __forceinline__ void prep_row_regs(const AttnArgs &a, float (&v)[(HD 
                 row[j] = v[i];
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");   // the wave's row is in LDS
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // the wave's row is in LDS
         __builtin_amdgcn_wave_barrier();
         const int half = a.rot / 2;
 #pragma unroll
@@ -98,7 +100,7 @@ __device__ __forceinline__ void prep_row_regs(const AttnArgs &a, float (&v)[(HD 
                 v[i] = j < half ? a0 * cs - b0 * sn : b0 * cs + a0 * sn;
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");   // every lane has read its pair
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup", "local");   // every lane has read its pair
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
@@ -124,38 +126,58 @@ __device__ __forceinline__ void prep_row(const AttnArgs &a, const float *src, co
 // The prep: one workgroup of kPrepWaves waves per token.  The token's RoPE
 // cos and sin (rot / 2 frequencies) go into LDS once, then wave w takes rows
 // w, w + kPrepWaves, ... of [H q heads, KV k heads, KV v heads]: q into the
-// scratch, k and v into the cache rows pos + t.
+// scratch, k and v into the cache rows pos + t.  A wave's next row (and its
+// norm weights) is requested before the current one is formed, and its
+// first before the RoPE table, so the rows' HBM round trips overlap.
 constexpr int kPrepWaves = 4;
 template <int HD>
 __global__ __launch_bounds__(kPrepWaves * OMH_WAVE) void attn_prep_kernel(const AttnArgs a) {
+    constexpr int NE = (HD + OMH_WAVE - 1) / OMH_WAVE;
     __shared__ float cs[HD / 2], sn[HD / 2], sv[kPrepWaves][HD];
     const int H = a.H, KV = a.KV, nr = H + 2 * KV;
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid % OMH_WAVE;
     const int wv = __builtin_amdgcn_readfirstlane(tid / OMH_WAVE);
     const int p = a.pos + t;
+    const float *row = a.qkv + (size_t)t * a.ld_qkv;
+    // row r's source and norm weights (null: a v row, copied)
+    auto src_of = [&](int r, const float *&w) -> const float * {
+        if (r < H) { w = a.qn; return row + (size_t)r * 2 * HD; }                          // q of head r (then its gate)
+        if (r < H + KV) { w = a.kn; return row + (size_t)2 * H * HD + (size_t)(r - H) * HD; }   // k of kv head r - H
+        w = nullptr;
+        return row + (size_t)2 * H * HD + (size_t)(r - H) * HD;                          // v of kv head r - H - KV
+    };
+    float v[NE], wt[NE];
+    auto fetch = [&](int r) __attribute__((always_inline)) {
+        const float *w;
+        const float *src = src_of(r, w);
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            const int j = lane + OMH_WAVE * i;
+            v[i] = j < HD ? src[j] : 0.f;
+            wt[i] = w && j < HD ? w[j] : 0.f;
+        }
+    };
+    if (wv < nr) fetch(wv);
     rope_table(a, p, cs, sn, tid, kPrepWaves * OMH_WAVE);
     __syncthreads();
-    const float *row = a.qkv + (size_t)t * a.ld_qkv;
     for (int r = wv; r < nr; r += kPrepWaves) {
-        const float *src, *w = nullptr;
-        float *dst;
-        if (r < H) {                                   // q of head r (then its gate)
-            src = row + (size_t)r * 2 * HD;
-            w = a.qn;
-            dst = a.qb + ((size_t)t * H + r) * HD;
-        } else if (r < H + KV) {                       // k of kv head g
-            const int g = r - H;
-            src = row + (size_t)2 * H * HD + (size_t)g * HD;
-            w = a.kn;
-            dst = a.Kc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
-        } else {                                       // v of kv head g
-            const int g = r - H - KV;
-            src = row + (size_t)2 * H * HD + (size_t)(KV + g) * HD;
-            dst = a.Vc + (((size_t)a.seq * KV + g) * a.max_t + p) * HD;
+        float cv[NE], cw[NE];
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            cv[i] = v[i];
+            cw[i] = wt[i];
         }
-        prep_row<HD>(a, src, w, sv[wv], lane, cs, sn);
-        // (each lane copies the entries it wrote itself)
-        for (int j = lane; j < HD; j += OMH_WAVE) dst[j] = sv[wv][j];
+        if (r + kPrepWaves < nr) fetch(r + kPrepWaves);
+        float *dst;
+        if (r < H) dst = a.qb + ((size_t)t * H + r) * HD;
+        else if (r < H + KV) dst = a.Kc + (((size_t)a.seq * KV + (r - H)) * a.max_t + p) * HD;
+        else dst = a.Vc + (((size_t)a.seq * KV + (r - H - KV)) * a.max_t + p) * HD;
+        prep_row_regs<HD>(a, cv, cw, r < H + KV, sv[wv], lane, cs, sn);
+#pragma unroll
+        for (int i = 0; i < NE; i++) {
+            const int j = lane + OMH_WAVE * i;
+            if (j < HD) dst[j] = cv[i];
+        }
     }
 }
 
